@@ -1,0 +1,227 @@
+// extern "C" entry points of include/cuda_llm_abi.h: argument validation,
+// error reporting and dispatch to the gfx950 launchers.
+//
+// Validation mirrors the reference binding's TORCH_CHECKs
+// (fused_softmax_binding.cpp:52-67 prefill, :116-132 paged, :313-322 decode,
+// :650-669 fp8 paged), extended with GQA, alignment and size checks; every
+// launch is followed by hipGetLastError (the reference checks nothing after
+// launching, e.g. flash_attention_v2_kernel.cuh:233-304).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/cuda_llm_abi.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+ca_status fail(ca_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+ca_status from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return CA_OK;
+  if (e == hipErrorInvalidValue)
+    return fail(CA_INVALID_ARGUMENT, "%s: invalid launch configuration (%s)", what,
+                hipGetErrorString(e));
+  return fail(CA_LAUNCH_FAILED, "%s: launch failed: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+ca_status check_16bit_dtype(ca_dtype dt, const char* what) {
+  if (dt == CA_BF16 || dt == CA_F16) return CA_OK;
+  if (dt == CA_F32)
+    return fail(CA_UNSUPPORTED, "%s: float32 tensors are not supported on gfx950 yet (use bf16/fp16)", what);
+  return fail(CA_INVALID_ARGUMENT, "%s: unknown dtype %d", what, (int)dt);
+}
+
+ca_status check_heads(int hq, int hkv, const char* what) {
+  if (hq <= 0 || hkv <= 0) return fail(CA_INVALID_ARGUMENT, "%s: head counts must be positive", what);
+  if (hq % hkv != 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: num_q_heads (%d) must be a multiple of num_kv_heads (%d)",
+                what, hq, hkv);
+  return CA_OK;
+}
+
+ca_status check_head_dim(int d, const char* what) {
+  if (d == 64 || d == 128) return CA_OK;
+  return fail(CA_INVALID_ARGUMENT, "%s: Only head_dim 64 and 128 are currently supported (got %d)",
+              what, d);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ca_last_error(void) { return g_last_error.c_str(); }
+
+const char* ca_version(void) { return "cuda_llm-amd 0.1 (gfx950)"; }
+
+size_t ca_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_tokens) {
+  if (num_seqs <= 0 || num_q_heads <= 0 || head_dim <= 0 || max_tokens <= 0) return 0;
+  return ca::decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_tokens);
+}
+
+ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                 void* o, int batch, int num_q_heads, int num_kv_heads,
+                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
+                                 void* stream) {
+  const char* what = "flash_attention";
+  ca_status st;
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (batch < 0 || seq_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0 || seq_len == 0) return CA_OK;
+  if (!q || !k || !v || !o) return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
+  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  return from_hip(ca::launch_prefill((int)dtype, q, k, v, o, batch, num_q_heads, num_kv_heads,
+                                     seq_len, head_dim, softmax_scale, is_causal != 0,
+                                     (hipStream_t)stream),
+                  what);
+}
+
+ca_status ca_flash_decode(ca_dtype dtype, const void* q, const void* k, const void* v, void* o,
+                          int batch, int num_q_heads, int num_kv_heads, int kv_len, int head_dim,
+                          float softmax_scale, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  const char* what = "flash_decode";
+  ca_status st;
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (batch < 0 || kv_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0) return CA_OK;
+  if (!q || !o || (kv_len > 0 && (!k || !v)))
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
+  const size_t need = ca::decode_workspace_bytes(batch, num_q_heads, head_dim, kv_len);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
+                workspace_bytes);
+  return from_hip(ca::launch_flash_decode((int)dtype, q, k, v, o, batch, num_q_heads,
+                                          num_kv_heads, kv_len, head_dim, softmax_scale,
+                                          workspace, workspace_bytes, (hipStream_t)stream),
+                  what);
+}
+
+static ca_status paged_common_checks(const char* what, const void* query, const void* kc,
+                                     const void* vc, const int32_t* bt, const int32_t* lens,
+                                     void* out, int num_seqs, int hq, int hkv, int head_dim,
+                                     int max_blocks, int page_size, int num_blocks,
+                                     void* workspace, size_t workspace_bytes) {
+  ca_status st;
+  if ((st = check_heads(hq, hkv, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (page_size != 16) return fail(CA_INVALID_ARGUMENT, "%s: Only page_size 16 is currently supported (got %d)", what, page_size);
+  if (num_seqs < 0 || max_blocks < 0 || num_blocks < 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (num_seqs == 0) return CA_OK;
+  if (num_blocks == 0 && max_blocks > 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: empty cache with a non-empty block table", what);
+  if (!query || !out || !lens || (max_blocks > 0 && (!kc || !vc || !bt)))
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(query) || !aligned16(kc) || !aligned16(vc) || !aligned16(out))
+    return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
+  const size_t need = ca::decode_workspace_bytes(num_seqs, hq, head_dim, max_blocks * page_size);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
+                workspace_bytes);
+  return CA_OK;
+}
+
+ca_status ca_paged_attention(ca_dtype dtype, const void* query, const void* key_cache,
+                             const void* value_cache, const int32_t* block_tables,
+                             const int32_t* context_lens, void* out, int num_seqs,
+                             int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_blocks_per_seq, int page_size, int num_blocks,
+                             float softmax_scale, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  const char* what = "paged_attention";
+  ca_status st;
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = paged_common_checks(what, query, key_cache, value_cache, block_tables, context_lens,
+                                out, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                max_blocks_per_seq, page_size, num_blocks, workspace,
+                                workspace_bytes)) != CA_OK)
+    return st;
+  if (num_seqs == 0) return CA_OK;
+  return from_hip(ca::launch_paged_decode((int)dtype, 0, query, key_cache, value_cache, nullptr,
+                                          nullptr, 0, block_tables, context_lens, out, num_seqs,
+                                          num_q_heads, num_kv_heads, head_dim,
+                                          max_blocks_per_seq, num_blocks > 0 ? num_blocks : 1,
+                                          softmax_scale, workspace, workspace_bytes,
+                                          (hipStream_t)stream),
+                  what);
+}
+
+ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_t* key_cache,
+                                 const uint8_t* value_cache, const float* k_scale,
+                                 const float* v_scale, int per_block_scales,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 void* out, int num_seqs, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int max_blocks_per_seq, int page_size,
+                                 int num_blocks, float softmax_scale, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  const char* what = "fp8_paged_attention";
+  ca_status st;
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = paged_common_checks(what, query, key_cache, value_cache, block_tables, context_lens,
+                                out, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                max_blocks_per_seq, page_size, num_blocks, workspace,
+                                workspace_bytes)) != CA_OK)
+    return st;
+  if (num_seqs == 0) return CA_OK;
+  if (!k_scale || !v_scale) return fail(CA_INVALID_ARGUMENT, "%s: null scale pointer", what);
+  return from_hip(ca::launch_paged_decode((int)dtype, 1, query, key_cache, value_cache, k_scale,
+                                          v_scale, per_block_scales != 0, block_tables,
+                                          context_lens, out, num_seqs, num_q_heads,
+                                          num_kv_heads, head_dim, max_blocks_per_seq,
+                                          num_blocks > 0 ? num_blocks : 1, softmax_scale,
+                                          workspace, workspace_bytes, (hipStream_t)stream),
+                  what);
+}
+
+ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
+                                         const uint8_t* q_scale, const uint8_t* k,
+                                         const uint8_t* k_scale, const uint8_t* v,
+                                         const uint8_t* v_scale, void* out, int batch,
+                                         int num_heads, int seq_len, int head_dim,
+                                         float softmax_scale, int is_causal, void* stream) {
+  const char* what = "fused_microscaled_attention";
+  if (out_dtype != CA_BF16 && out_dtype != CA_F16)
+    return fail(out_dtype == CA_F32 ? CA_UNSUPPORTED : CA_INVALID_ARGUMENT,
+                "%s: output dtype must be bf16 or fp16", what);
+  if (head_dim != 128)
+    return fail(CA_INVALID_ARGUMENT, "%s: head_dim must be 128 (got %d)", what, head_dim);
+  if (batch < 0 || num_heads < 0 || seq_len < 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0 || num_heads == 0 || seq_len == 0) return CA_OK;
+  if (!q || !k || !v || !q_scale || !k_scale || !v_scale || !out)
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(CA_INVALID_ARGUMENT, "%s: code/output pointers must be 16-byte aligned", what);
+  if ((reinterpret_cast<uintptr_t>(k_scale) & 3u) != 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: k_scale must be 4-byte aligned", what);
+  return from_hip(ca::launch_mxfp8((int)out_dtype, q, q_scale, k, k_scale, v, v_scale, out, batch,
+                                   num_heads, seq_len, head_dim, softmax_scale, is_causal != 0,
+                                   (hipStream_t)stream),
+                  what);
+}
+
+}  // extern "C"

@@ -1,0 +1,49 @@
+// Internal launcher declarations shared by the kernel translation units and
+// the C ABI (abi.cpp). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ca {
+
+// dtype codes; the same values as ca_dtype in include/cuda_llm_abi.h
+constexpr int kDtypeF32 = 0;
+constexpr int kDtypeF16 = 1;
+constexpr int kDtypeBF16 = 2;
+
+hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
+                          int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
+                          hipStream_t stream);
+
+// Split-K geometry of the decode kernels: pages of 16 tokens, 4 waves per
+// workgroup, kPagesPerWave pages per wave.
+constexpr int kDecodePage = 16;
+constexpr int kDecodeWaves = 4;
+constexpr int kPagesPerWave = 16;
+constexpr int kPagesPerSplit = kDecodeWaves * kPagesPerWave;
+
+// Workspace for split-K partial results: [N][Hq][max_splits] x (D + 1) floats.
+size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens);
+
+// Paged decode. cache_kind: 0 = 16-bit cache of the query dtype, 1 = fp8 e4m3
+// bytes with fp32 scales (per head [Hkv] or per block [num_blocks, Hkv]).
+hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const void* kc,
+                               const void* vc, const float* k_scale, const float* v_scale,
+                               int per_block_scales, const int32_t* block_tables,
+                               const int32_t* context_lens, void* out, int N, int Hq, int Hkv,
+                               int D, int max_blocks_per_seq, int num_blocks, float scale,
+                               void* ws, size_t ws_bytes, hipStream_t stream);
+
+// Contiguous-cache decode (q_len = 1 over k/v [B, Hkv, S, D]).
+hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,
+                               int B, int Hq, int Hkv, int S, int D, float scale, void* ws,
+                               size_t ws_bytes, hipStream_t stream);
+
+// MXFP8 attention: e4m3 q/k/v [B, H, S, D] with e8m0 scale bytes [B, H, S, D/32].
+hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
+                        const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,
+                        int H, int S, int D, float scale, bool causal, hipStream_t stream);
+
+}  // namespace ca

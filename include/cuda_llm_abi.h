@@ -1,0 +1,126 @@
+/*
+ * cuda_llm_abi.h — C ABI of the MI355X (gfx950) attention forward hot path.
+ *
+ * Drop-in boundary for the reference's host API (kernels_api.h). The
+ * reference exposes C++ templates instantiated per element type; this ABI
+ * takes the element type as an enum argument and returns a status code, so
+ * any FFI (ctypes, cffi, a torch extension, another language) can bind it.
+ *
+ * Conventions
+ *  - All tensor arguments are raw device pointers to contiguous row-major
+ *    buffers in the layouts stated per function; 16-byte aligned.
+ *  - The library never allocates, frees or retains caller memory. Split-K
+ *    decode needs a caller-provided workspace of ca_decode_workspace_bytes().
+ *  - `stream` is a hipStream_t (NULL = the default stream). Calls enqueue
+ *    work asynchronously and never synchronise the host.
+ *  - Non-OK status: ca_last_error() returns a thread-local message.
+ *  - Element types: CA_BF16 and CA_F16 for 16-bit q/k/v/out. (CA_F32 is
+ *    reserved and currently returns CA_UNSUPPORTED.)
+ *  - head_dim must be 64 or 128 (fused_softmax_binding.cpp:65-67); the MXFP8
+ *    entry point requires 128.
+ *  - GQA: num_q_heads % num_kv_heads == 0, kv head = q head / (Hq / Hkv)
+ *    (fused_gqa_kernel.cuh:40-41, tests/_utils.py:67-72).
+ */
+#ifndef CUDA_LLM_ABI_H
+#define CUDA_LLM_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  CA_OK = 0,
+  CA_INVALID_ARGUMENT = 1,
+  CA_UNSUPPORTED = 2,
+  CA_LAUNCH_FAILED = 3
+} ca_status;
+
+typedef enum { CA_F32 = 0, CA_F16 = 1, CA_BF16 = 2 } ca_dtype;
+
+/* Prefill forward: O = softmax(Q K^T * scale [+ causal mask]) V.
+ * q, o: [batch, num_q_heads, seq_len, head_dim]; k, v: [batch, num_kv_heads,
+ * seq_len, head_dim]. Causal masking is top-left aligned (key j visible to
+ * query i iff j <= i).
+ * Replaces dispatch_flash_attention_v2<T> (kernels_api.h:29-33),
+ * dispatch_flash_attention_v3_hopper<T> (kernels_api.h:78-83) and
+ * dispatch_fused_gqa<T> (kernels_api.h:52-56). */
+ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                 void* o, int batch, int num_q_heads, int num_kv_heads,
+                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
+                                 void* stream);
+
+/* Single-token decode over a contiguous cache.
+ * q, o: [batch, num_q_heads, 1, head_dim]; k, v: [batch, num_kv_heads, kv_len,
+ * head_dim]. Replaces dispatch_async_flash_decode<T> (kernels_api.h:58-62).
+ * workspace: ca_decode_workspace_bytes(batch, num_q_heads, head_dim, kv_len). */
+ca_status ca_flash_decode(ca_dtype dtype, const void* q, const void* k, const void* v, void* o,
+                          int batch, int num_q_heads, int num_kv_heads, int kv_len, int head_dim,
+                          float softmax_scale, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Paged decode (vLLM layout), 16-bit cache of the query dtype.
+ * query, out: [num_seqs, num_q_heads, head_dim]; key_cache, value_cache:
+ * [num_blocks, num_kv_heads, head_dim, page_size] (page axis innermost);
+ * block_tables: int32 [num_seqs, max_blocks_per_seq]; context_lens: int32
+ * [num_seqs]. page_size must be 16. A sequence with context_len <= 0 gets a
+ * zero output row. Block ids outside [0, num_blocks) are clamped.
+ * Replaces dispatch_paged_attention<T> (kernels_api.h:35-41).
+ * workspace: ca_decode_workspace_bytes(num_seqs, num_q_heads, head_dim,
+ * max_blocks_per_seq * page_size). */
+ca_status ca_paged_attention(ca_dtype dtype, const void* query, const void* key_cache,
+                             const void* value_cache, const int32_t* block_tables,
+                             const int32_t* context_lens, void* out, int num_seqs,
+                             int num_q_heads, int num_kv_heads, int head_dim,
+                             int max_blocks_per_seq, int page_size, int num_blocks,
+                             float softmax_scale, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* FP8 paged decode: caches hold OCP e4m3 codes (1 byte each) in the paged
+ * layout above; k = code * k_scale, v = code * v_scale with fp32 scales per
+ * kv head ([num_kv_heads], per_block_scales = 0) or per (physical block, kv
+ * head) ([num_blocks, num_kv_heads], per_block_scales = 1). Output in the
+ * query dtype. Replaces dispatch_fp8_paged_attention<T_OUT, T_Q>
+ * (kernels_api.h:94-101), whose kernel decodes int8 rather than e4m3
+ * (fp8_paged_attention_kernel.cuh:102,135). */
+ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_t* key_cache,
+                                 const uint8_t* value_cache, const float* k_scale,
+                                 const float* v_scale, int per_block_scales,
+                                 const int32_t* block_tables, const int32_t* context_lens,
+                                 void* out, int num_seqs, int num_q_heads, int num_kv_heads,
+                                 int head_dim, int max_blocks_per_seq, int page_size,
+                                 int num_blocks, float softmax_scale, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* MXFP8 attention: q, k, v are OCP e4m3 codes [batch, num_heads, seq_len,
+ * head_dim] with one e8m0 scale byte per 32 elements along head_dim
+ * ([batch, num_heads, seq_len, head_dim / 32]); value = code * 2^(scale-127).
+ * Output [batch, num_heads, seq_len, head_dim] in out_dtype (CA_BF16 or
+ * CA_F16). Replaces dispatch_fused_microscaled_attention<T_OUT>
+ * (kernels_api.h:103-108), which takes the scales as float; e8m0 bytes are
+ * the MX storage format (README.md:29-31). */
+ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
+                                         const uint8_t* q_scale, const uint8_t* k,
+                                         const uint8_t* k_scale, const uint8_t* v,
+                                         const uint8_t* v_scale, void* out, int batch,
+                                         int num_heads, int seq_len, int head_dim,
+                                         float softmax_scale, int is_causal, void* stream);
+
+/* Bytes of workspace the decode entry points need (0 if none). max_tokens is
+ * kv_len for ca_flash_decode and max_blocks_per_seq * page_size for the paged
+ * entry points. No counterpart in the reference (its decode is not split). */
+size_t ca_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, int max_tokens);
+
+/* Thread-local description of the last non-OK status of this thread. */
+const char* ca_last_error(void);
+
+/* Library version string. */
+const char* ca_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUDA_LLM_ABI_H */

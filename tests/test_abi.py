@@ -1,0 +1,124 @@
+"""CPU tier: the C ABI library and the Python API's host logic.
+
+No kernel runs here: the library is loaded, its exports are compared with
+include/cuda_llm_abi.h, and calls that must be rejected before any launch are
+made with dummy pointers (they never reach the GPU).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import cuda_amd._lib as L
+import cuda_llm
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cuda_llm_abi.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = {}
+    for m in re.finditer(r"([A-Za-z_][\w\s\*]*?)\b(ca_\w+)\s*\(([^;{]*?)\)\s*;", text):
+        params = [p.strip() for p in m.group(3).split(",") if p.strip() and p.strip() != "void"]
+        decls[m.group(2)] = params
+    return decls
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return L.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    decls = _header_functions()
+    assert len(decls) >= 8
+    for name in decls:
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+
+
+def test_binding_table_matches_header():
+    decls = _header_functions()
+    assert set(decls) == set(L.SIGNATURES)
+    for name, params in decls.items():
+        assert len(params) == len(L.SIGNATURES[name][1]), name
+
+
+def test_version_and_workspace_sizes(lib):
+    assert b"gfx950" in lib.ca_version()
+    # one split (<= 64 pages) needs no workspace; otherwise N*Hq*splits*(D+1) floats
+    assert lib.ca_decode_workspace_bytes(4, 8, 128, 1024) == 0
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 8192) == 64 * 32 * 8 * 129 * 4
+    assert lib.ca_decode_workspace_bytes(256, 32, 128, 32768) == 256 * 32 * 32 * 129 * 4
+    assert lib.ca_decode_workspace_bytes(0, 32, 128, 32768) == 0
+
+
+P = ctypes.c_void_p(16)  # aligned dummy pointer: never dereferenced on these paths
+
+
+def _status(name, *args):
+    return getattr(L.load(), name)(*args)
+
+
+def test_prefill_rejects_bad_arguments():
+    st = _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 1, 4, 4, 64, 96, 0.1, 0, None)
+    assert st == L.CA_INVALID_ARGUMENT and b"head_dim" in L.load().ca_last_error()
+    st = _status("ca_flash_attention_fwd", L.CA_F32, P, P, P, P, 1, 4, 4, 64, 64, 0.1, 0, None)
+    assert st == L.CA_UNSUPPORTED
+    st = _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 1, 6, 4, 64, 64, 0.1, 0, None)
+    assert st == L.CA_INVALID_ARGUMENT and b"multiple" in L.load().ca_last_error()
+    st = _status("ca_flash_attention_fwd", L.CA_BF16, ctypes.c_void_p(18), P, P, P, 1, 4, 4, 64,
+                 64, 0.1, 0, None)
+    assert st == L.CA_INVALID_ARGUMENT and b"aligned" in L.load().ca_last_error()
+    # empty problems are a no-op success
+    assert _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 0, 4, 4, 64, 64, 0.1, 0, None) == L.CA_OK
+
+
+def test_paged_rejects_bad_arguments():
+    args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
+    bad_page = list(args)
+    bad_page[12] = 8
+    assert _status("ca_paged_attention", *bad_page) == L.CA_INVALID_ARGUMENT
+    assert b"page_size" in L.load().ca_last_error()
+    # 4 blocks x 16 = 64 tokens: one split, no workspace needed -> the size check passes;
+    # 200 blocks needs a workspace
+    long = list(args)
+    long[11] = 200
+    assert _status("ca_paged_attention", *long) == L.CA_INVALID_ARGUMENT
+    assert b"workspace" in L.load().ca_last_error()
+    fp8 = [L.CA_BF16, P, P, P, None, None, 1, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
+    assert _status("ca_fp8_paged_attention", *fp8) == L.CA_INVALID_ARGUMENT
+
+
+def test_mxfp8_rejects_bad_arguments():
+    st = _status("ca_fused_microscaled_attention", L.CA_BF16, P, P, P, P, P, P, P, 1, 2, 64, 64,
+                 0.1, 1, None)
+    assert st == L.CA_INVALID_ARGUMENT
+    st = _status("ca_fused_microscaled_attention", L.CA_F32, P, P, P, P, P, P, P, 1, 2, 64, 128,
+                 0.1, 1, None)
+    assert st == L.CA_UNSUPPORTED
+
+
+def test_python_api_requires_device_tensors():
+    q = torch.randn(1, 2, 8, 64)
+    with pytest.raises(RuntimeError, match="Inputs must be on CUDA"):
+        cuda_llm.flash_attention(q, q, q)
+    with pytest.raises(RuntimeError, match="Inputs must be on CUDA"):
+        cuda_llm.flash_decode(q[:, :, :1], q, q)
+    bt = torch.zeros(1, 1, dtype=torch.int32)
+    lens = torch.ones(1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="on CUDA"):
+        cuda_llm.paged_attention(q[:, :, 0], torch.zeros(1, 2, 64, 16), torch.zeros(1, 2, 64, 16), bt, lens)
+
+
+def test_mx_scale_conversion():
+    b = torch.randint(100, 150, (3, 4), dtype=torch.uint8)
+    assert torch.equal(cuda_llm.mx_scales_to_e8m0(b), b)
+    f = torch.ldexp(torch.ones(3, 4), b.to(torch.int32) - 127)
+    assert torch.equal(cuda_llm.mx_scales_to_e8m0(f), b)
+    assert torch.equal(cuda_llm.mx_scales_to_e8m0(b.view(torch.float8_e8m0fnu)), b)
+    with pytest.raises(RuntimeError, match="powers of two"):
+        cuda_llm.mx_scales_to_e8m0(torch.full((2,), 3.0))

@@ -1,0 +1,171 @@
+"""GPU tier: decode entry points vs the oracle.
+
+* paged_attention_forward — the reference grid (tests/test_kernels_misc.py:26-35
+  there: fp16/bf16, D in {64, 128}, context_lens [1,16,17] and [300,129,64],
+  H=4), GQA, long contexts that split, zero-length sequences, NaN bytes in
+  the unused tail of a page, and the BASELINE C3 shape on sampled sequences;
+* fp8_paged_attention_forward — the reference's e4m3 test (xfail there,
+  tests/test_kernels_misc.py:42-64; must pass here) with per-head scales, the
+  per-(block, head) form, GQA, and the BASELINE C4 shape on sampled sequences;
+* async_flash_decode / flash_decode — the reference grid
+  (tests/test_attention.py:76-86: kv_len in {1, 63, 64, 1000}) plus GQA and
+  split lengths;
+* the committed golden vectors.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import cuda_llm
+import oracle
+from _util import TOL_16BIT, TOL_FP8, assert_close, build_paged, paged_oracle, to_np
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+DTYPES = [torch.float16, torch.bfloat16]
+
+
+def _run_paged(case):
+    if "k_scale" in case:
+        return cuda_llm.fp8_paged_attention_forward(
+            case["query"], case["key_cache"], case["value_cache"], case["k_scale"],
+            case["v_scale"], case["block_tables"], case["context_lens"])
+    return cuda_llm.paged_attention_forward(case["query"], case["key_cache"], case["value_cache"],
+                                            case["block_tables"], case["context_lens"])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("context_lens", [[1, 16, 17], [300, 129, 64]])
+def test_paged_attention(dev, dtype, head_dim, context_lens):
+    case = build_paged(context_lens, 4, 4, head_dim, dtype, dev)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), paged_oracle(case), **TOL_16BIT, name="paged")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 1), (16, 16), (40, 2)])
+def test_paged_gqa_and_splits(dev, dtype, hq, hkv):
+    lens = [0, 1, 15, 16, 17, 1023, 1024, 1025, 3000, 5000]
+    case = build_paged(lens, hq, hkv, 128, dtype, dev, pool=2000)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    ref = paged_oracle(case)
+    assert_close(to_np(out), ref, **TOL_16BIT, name=f"paged gqa {hq}/{hkv}")
+    assert torch.all(out[0] == 0)
+
+
+def test_paged_nan_tail_does_not_leak(dev):
+    """Bytes past a sequence's length in its last page may be anything."""
+    case = build_paged([37, 5], 8, 2, 128, torch.bfloat16, dev)
+    ref = paged_oracle(case)
+    for i, L in enumerate([37, 5]):
+        blk = int(case["block_tables"][i, (L - 1) // 16])
+        case["key_cache"][blk, :, :, L % 16:] = float("nan")
+        case["value_cache"][blk, :, :, L % 16:] = float("nan")
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref, **TOL_16BIT, name="nan tail")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_fp8_paged_attention_e4m3(dev, dtype, head_dim):
+    """The reference's own FP8 test (per-head scales amax/448)."""
+    case = build_paged([300, 129, 64], 4, 4, head_dim, dtype, dev, fp8=True, per_block=False)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), paged_oracle(case), **TOL_FP8, name="fp8 per-head")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_fp8_paged_per_block_gqa(dev, dtype, head_dim):
+    lens = [0, 7, 16, 33, 1100, 2049, 4100]
+    case = build_paged(lens, 32, 8, head_dim, dtype, dev, fp8=True, per_block=True, pool=1000)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), paged_oracle(case), **TOL_FP8, name="fp8 per-block")
+
+
+def test_fp8_cache_as_float8_dtype(dev):
+    case = build_paged([100, 17], 8, 2, 128, torch.bfloat16, dev, fp8=True)
+    ref = paged_oracle(case)
+    case["key_cache"] = case["key_cache"].view(torch.float8_e4m3fn)
+    case["value_cache"] = case["value_cache"].view(torch.float8_e4m3fn)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref, **TOL_FP8, name="float8 dtype")
+
+
+def test_golden_paged(dev):
+    g = np.load(GOLDEN, allow_pickle=False)
+    c = {k.split("/", 1)[1]: g[k] for k in g.files if k.startswith("paged_d64/")}
+    t = lambda a, dt=None: torch.from_numpy(a).to(dev) if dt is None else torch.from_numpy(a).to(dev).to(dt)
+    out = cuda_llm.paged_attention_forward(t(c["query"], torch.bfloat16), t(c["key_cache"], torch.bfloat16),
+                                           t(c["value_cache"], torch.bfloat16), t(c["block_tables"]),
+                                           t(c["context_lens"]))
+    torch.cuda.synchronize()
+    assert_close(to_np(out), c["out"], **TOL_16BIT, name="golden paged")
+
+
+def test_golden_fp8_paged(dev):
+    g = np.load(GOLDEN, allow_pickle=False)
+    c = {k.split("/", 1)[1]: g[k] for k in g.files if k.startswith("fp8_paged_d128/")}
+    t = lambda a: torch.from_numpy(a).to(dev)
+    out = cuda_llm.fp8_paged_attention_forward(t(c["query"]).to(torch.bfloat16), t(c["key_cache"]),
+                                               t(c["value_cache"]), t(c["k_scale"]), t(c["v_scale"]),
+                                               t(c["block_tables"]), t(c["context_lens"]))
+    torch.cuda.synchronize()
+    assert_close(to_np(out), c["out"], **TOL_FP8, name="golden fp8 paged")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("kv_len", [1, 63, 64, 1000])
+def test_decode(dev, dtype, head_dim, kv_len):
+    q = torch.randn(2, 4, 1, head_dim, device=dev, dtype=dtype)
+    k = torch.randn(2, 4, kv_len, head_dim, device=dev, dtype=dtype)
+    v = torch.randn(2, 4, kv_len, head_dim, device=dev, dtype=dtype)
+    out = cuda_llm.async_flash_decode(q, k, v)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v))
+    assert_close(to_np(out), ref, **TOL_16BIT, name="decode")
+
+
+@pytest.mark.parametrize("hq,hkv,kv_len", [(32, 8, 5000), (8, 1, 1025), (4, 4, 9000)])
+def test_flash_decode_gqa_split(dev, hq, hkv, kv_len):
+    q = torch.randn(3, hq, 1, 128, device=dev, dtype=torch.bfloat16)
+    k = torch.randn(3, hkv, kv_len, 128, device=dev, dtype=torch.bfloat16)
+    v = torch.randn(3, hkv, kv_len, 128, device=dev, dtype=torch.bfloat16)
+    out = cuda_llm.flash_decode(q, k, v)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v))
+    assert_close(to_np(out), ref, **TOL_16BIT, name="flash_decode gqa")
+
+
+def test_baseline_c3_shape(dev):
+    """C3: N=64, Hq=32/Hkv=8, D=128, L ~ U[512, 8192], 40k-page pool, permuted."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 8193, (64,), generator=g).tolist()
+    case = build_paged(lens, 32, 8, 128, torch.bfloat16, dev, pool=40000)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    seqs = [0, 17, int(np.argmax(lens)), 63]
+    assert_close(to_np(out)[seqs], paged_oracle(case, seqs), **TOL_16BIT, name="C3")
+
+
+def test_baseline_c4_shape(dev):
+    """C4: N=256, L ~ U[2048, 32768], e4m3 cache with per-(page, kv-head) scales."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(2048, 32769, (256,), generator=g).tolist()
+    case = build_paged(lens, 32, 8, 128, torch.bfloat16, dev, fp8=True, per_block=True)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    seqs = [0, int(np.argmax(lens)), int(np.argmin(lens)), 255]
+    assert_close(to_np(out)[seqs], paged_oracle(case, seqs), **TOL_FP8, name="C4")

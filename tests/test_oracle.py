@@ -1,0 +1,283 @@
+"""CPU tier: pin the oracle before trusting it.
+
+Every oracle function is checked against something it does not share code
+with: plain-Python float64 loops (golden fixtures and brute force), torch's
+SDPA and float8 conversions, closed forms and invariants. A few checks plant a
+mistake in the oracle (on the CPU) to show the check would catch it.
+"""
+import importlib
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from golden.make_golden import attend_rows
+
+oattn = importlib.import_module("oracle.attention")
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+def _case(g, name):
+    pre = name + "/"
+    return {k[len(pre):]: g[k] for k in g.files if k.startswith(pre)}
+
+
+# ---------------------------------------------------------------------------
+# golden vectors (float64 pure-Python loops)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["attn_causal_d64", "attn_full_d64", "attn_gqa_causal_d128"])
+def test_attention_matches_golden(golden, name):
+    c = _case(golden, name)
+    out = oracle.attention(c["q"], c["k"], c["v"], is_causal=bool(c["causal"]))
+    np.testing.assert_allclose(out, c["out"], atol=2e-6, rtol=0)
+
+
+def test_paged_decode_matches_golden(golden):
+    c = _case(golden, "paged_d64")
+    out = oracle.paged_decode(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],
+                              c["context_lens"])
+    np.testing.assert_allclose(out, c["out"], atol=2e-6, rtol=0)
+    assert np.all(out[3] == 0)  # context length 0 -> zeros
+
+
+def test_fp8_paged_decode_matches_golden(golden):
+    c = _case(golden, "fp8_paged_d128")
+    out = oracle.paged_decode(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],
+                              c["context_lens"], k_scale=c["k_scale"], v_scale=c["v_scale"])
+    np.testing.assert_allclose(out, c["out"], atol=5e-6, rtol=0)
+
+
+def test_mx_attention_matches_golden(golden):
+    c = _case(golden, "mx_causal")
+    deq = {n: oracle.mx_dequantize(c[n], c[n + "_scale"]) for n in "qkv"}
+    out = oracle.attention(deq["q"], deq["k"], deq["v"], is_causal=bool(c["causal"]))
+    np.testing.assert_allclose(out, c["out"], atol=1e-4 * max(1.0, np.abs(c["out"]).max()), rtol=0)
+
+
+def test_planted_gqa_mistake_is_caught(golden, monkeypatch):
+    """A wrong kv-head mapping (h % Hkv instead of h // group) must fail."""
+    c = _case(golden, "attn_gqa_causal_d128")
+    monkeypatch.setattr(oattn, "_kv_head", lambda h, hq, hkv: h % hkv)
+    out = oracle.attention(c["q"], c["k"], c["v"], is_causal=True)
+    assert np.abs(out - c["out"]).max() > 1e-2
+
+
+def test_planted_causal_mistake_is_caught(golden):
+    """Dropping the causal mask must fail the causal golden vector."""
+    c = _case(golden, "attn_causal_d64")
+    out = oracle.attention(c["q"], c["k"], c["v"], is_causal=False)
+    assert np.abs(out - c["out"]).max() > 1e-2
+
+
+# ---------------------------------------------------------------------------
+# brute force and library cross-checks
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("s,d,causal", [(1, 8, True), (5, 8, False), (17, 16, True), (64, 8, False)])
+def test_attention_vs_bruteforce(s, d, causal):
+    rng = np.random.default_rng(s * 10 + d)
+    q, k, v = (rng.standard_normal((1, 1, s, d)) for _ in range(3))
+    ref = attend_rows(q[0, 0].tolist(), k[0, 0].tolist(), v[0, 0].tolist(), 1 / math.sqrt(d),
+                      0 if causal else None)
+    out = oracle.attention(q, k, v, is_causal=causal, dtype=np.float64)
+    np.testing.assert_allclose(out[0, 0], np.array(ref), atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hq,hkv,s,d", [(4, 4, 100, 64), (8, 2, 77, 128), (4, 1, 256, 64)])
+def test_attention_vs_torch_sdpa(causal, hq, hkv, s, d):
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(2, hq, s, d, generator=g)
+    k = torch.randn(2, hkv, s, d, generator=g)
+    v = torch.randn(2, hkv, s, d, generator=g)
+    rep = hq // hkv
+    ref = F.scaled_dot_product_attention(q, k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1),
+                                         is_causal=causal)
+    out = oracle.attention(q.numpy(), k.numpy(), v.numpy(), is_causal=causal)
+    np.testing.assert_allclose(out, ref.numpy(), atol=2e-5, rtol=0)
+
+
+def test_lse_vs_torch():
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, 2, 50, 64, generator=g)
+    k = torch.randn(1, 2, 50, 64, generator=g)
+    s = (q @ k.transpose(-1, -2)) / 8.0
+    s = s.masked_fill(~torch.ones(50, 50, dtype=torch.bool).tril(), float("-inf"))
+    np.testing.assert_allclose(oracle.attention_lse(q.numpy(), k.numpy(), is_causal=True),
+                               torch.logsumexp(s, -1).numpy(), atol=2e-5, rtol=0)
+
+
+# ---------------------------------------------------------------------------
+# invariants (closed forms)
+# ---------------------------------------------------------------------------
+def test_causal_first_row_is_first_value():
+    rng = np.random.default_rng(3)
+    q, k, v = (rng.standard_normal((2, 3, 40, 64)).astype(np.float32) for _ in range(3))
+    out = oracle.attention(q, k, v, is_causal=True)
+    np.testing.assert_allclose(out[:, :, 0], v[:, :, 0], atol=1e-6)
+
+
+def test_constant_keys_give_prefix_mean():
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((1, 1, 30, 64)).astype(np.float32)
+    k = np.tile(rng.standard_normal((1, 1, 1, 64)).astype(np.float32), (1, 1, 30, 1))
+    v = rng.standard_normal((1, 1, 30, 64)).astype(np.float32)
+    out = oracle.attention(q, k, v, is_causal=True)
+    means = np.cumsum(v[0, 0], axis=0) / np.arange(1, 31)[:, None]
+    np.testing.assert_allclose(out[0, 0], means, atol=1e-5)
+
+
+def test_zero_scale_gives_mean():
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((1, 1, 20, 64)).astype(np.float32) for _ in range(3))
+    out = oracle.attention(q, k, v, is_causal=False, scale=0.0)
+    np.testing.assert_allclose(out[0, 0], np.broadcast_to(v[0, 0].mean(0), (20, 64)), atol=1e-5)
+
+
+def test_key_permutation_invariance():
+    rng = np.random.default_rng(6)
+    q, k, v = (rng.standard_normal((1, 2, 33, 64)).astype(np.float32) for _ in range(3))
+    p = rng.permutation(33)
+    a = oracle.attention(q, k, v)
+    b = oracle.attention(q, k[:, :, p], v[:, :, p])
+    np.testing.assert_allclose(a, b, atol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# the kernels' blocking, restated on the CPU
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("s,qscale", [(100, 1.0), (300, 30.0), (129, 100.0)])
+def test_tiled_online_softmax_equals_attention(causal, s, qscale):
+    """Lazy rescaling (threshold 8 in log2 units) must be exact in fp32; large
+    q scales force many rescale events."""
+    rng = np.random.default_rng(s)
+    q = (rng.standard_normal((1, 2, s, 64)) * qscale).astype(np.float32)
+    k, v = (rng.standard_normal((1, 2, s, 64)).astype(np.float32) for _ in range(2))
+    ref = oracle.attention(q, k, v, is_causal=causal, dtype=np.float64)
+    out = oracle.attention_tiled(q, k, v, is_causal=causal)
+    # fp32 logits of magnitude ~qscale*8 carry ~6e-8*|s| absolute rounding
+    np.testing.assert_allclose(out, ref, atol=2e-5 * max(1.0, qscale / 5), rtol=0)
+
+
+def test_split_merge_equals_full_attention():
+    rng = np.random.default_rng(7)
+    d, L = 64, 1000
+    q = rng.standard_normal((1, 1, 1, d))
+    k = rng.standard_normal((1, 1, L, d))
+    v = rng.standard_normal((1, 1, L, d))
+    full = oracle.attention(q, k, v, dtype=np.float64)[0, 0, 0]
+    bounds = [0, 0, 100, 517, 1000, 1000]  # includes empty splits
+    o_parts, l_parts = [], []
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        o_parts.append(oracle.attention(q, k[:, :, a:b], v[:, :, a:b], dtype=np.float64)[0, 0, 0])
+        l_parts.append(oracle.attention_lse(q, k[:, :, a:b], dtype=np.float64)[0, 0, 0] if b > a else -np.inf)
+    merged = oracle.split_merge(np.array(o_parts), np.array(l_parts))
+    np.testing.assert_allclose(merged, full, atol=1e-12)
+    assert np.all(oracle.split_merge(np.zeros((2, d)), np.array([-np.inf, -np.inf])) == 0)
+
+
+# ---------------------------------------------------------------------------
+# paged layout
+# ---------------------------------------------------------------------------
+def test_paged_gather_roundtrip_is_bit_exact():
+    rng = np.random.default_rng(8)
+    n, h, t, d = 3, 2, 70, 64
+    k = rng.standard_normal((n, h, t, d)).astype(np.float32)
+    v = rng.standard_normal((n, h, t, d)).astype(np.float32)
+    perm = rng.permutation(n * 5)
+    kc, vc, bt = oracle.make_paged_cache(k, v, 16, perm=perm)
+    assert kc.shape == (n * 5, h, d, 16)
+    for i in range(n):
+        assert np.array_equal(oracle.gather_paged(kc, bt[i], t), k[i])
+        assert np.array_equal(oracle.gather_paged(vc, bt[i], t), v[i])
+
+
+def test_paged_decode_equals_contiguous_decode():
+    rng = np.random.default_rng(9)
+    n, hq, hkv, t, d = 3, 8, 2, 50, 64
+    q = rng.standard_normal((n, hq, d)).astype(np.float32)
+    k = rng.standard_normal((n, hkv, t, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, t, d)).astype(np.float32)
+    lens = np.array([50, 1, 33])
+    kc, vc, bt = oracle.make_paged_cache(k, v, 16, perm=rng.permutation(n * 4))
+    a = oracle.paged_decode(q, kc, vc, bt, lens)
+    b = oracle.decode(q, k, v, lens)
+    np.testing.assert_allclose(a, b, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# FP8 / MX codecs
+# ---------------------------------------------------------------------------
+def test_e4m3_decode_all_codes_vs_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    out = oracle.e4m3_decode(codes)
+    assert np.array_equal(np.isnan(ref), np.isnan(out))
+    assert np.array_equal(ref[~np.isnan(ref)], out[~np.isnan(out)])
+
+
+def test_e4m3_encode_vs_torch():
+    rng = np.random.default_rng(10)
+    x = np.concatenate([
+        np.linspace(-500, 500, 100001), rng.standard_normal(50000) * 50,
+        rng.standard_normal(50000) * 1e-2, rng.standard_normal(20000) * 1e-3,
+        # all representable values and every midpoint between neighbours (ties)
+        oracle.e4m3_decode(np.arange(256, dtype=np.uint8)),
+        [2.0 ** -10, 1.5 * 2.0 ** -9, 464.0, -464.0, 463.99, np.inf, -np.inf, np.nan, 0.0, -0.0],
+    ]).astype(np.float32)
+    vals = np.sort(np.unique(oracle.e4m3_decode(np.arange(256, dtype=np.uint8))))
+    vals = vals[np.isfinite(vals)]
+    x = np.concatenate([x, ((vals[1:] + vals[:-1]) / 2).astype(np.float32)])
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    out = oracle.e4m3_encode(x)
+    assert np.array_equal(ref, out)
+
+
+def test_e8m0_decode_vs_torch():
+    b = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(b).view(torch.float8_e8m0fnu).float().numpy()
+    out = oracle.e8m0_decode(b)
+    assert np.array_equal(np.isnan(ref), np.isnan(out))
+    assert np.array_equal(ref[~np.isnan(ref)], out[~np.isnan(out)])
+
+
+def test_mx_quantize_closed_form():
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((7, 128)) * rng.uniform(0.5, 4, (7, 128))).astype(np.float32)
+    codes, sc = oracle.mx_quantize(x)
+    amax = np.abs(x.reshape(7, 4, 32)).max(-1)
+    assert np.array_equal(sc.astype(int) - 127, np.floor(np.log2(amax)).astype(int) - 8)
+    deq = oracle.mx_dequantize(codes, sc)
+    # elements within 2^-4 relative (e4m3 RNE) except saturated ones, which are <= 448 * X
+    xs = x.reshape(7, 4, 32) / np.ldexp(1.0, sc.astype(int) - 127)[..., None]
+    ok = np.abs(xs) <= 448
+    rel = np.abs(deq.reshape(7, 4, 32) - x.reshape(7, 4, 32)) / np.maximum(np.abs(x.reshape(7, 4, 32)), 2.0 ** -6 * np.ldexp(1.0, sc.astype(int) - 127)[..., None])
+    assert rel[ok].max() <= 2.0 ** -4 + 1e-7
+    assert np.all(np.abs(deq.reshape(7, 4, 32)[~ok]) == 448 * np.ldexp(1.0, sc.astype(int) - 127)[..., None].repeat(32, -1)[~ok])
+
+
+def test_mx_equal_scales_reduce_to_fp8():
+    codes = np.arange(128, dtype=np.uint8).reshape(1, 128)
+    codes[codes == 0x7F] = 0
+    deq = oracle.mx_dequantize(codes, np.full((1, 4), 127, dtype=np.uint8))
+    assert np.array_equal(deq, oracle.e4m3_decode(codes))
+
+
+def test_per_page_quantization_matches_reference_recipe():
+    g = torch.Generator().manual_seed(12)
+    pages = torch.randn(5, 2, 64, 16, generator=g)
+    codes, scale = oracle.quantize_per_page_fp8(pages.numpy())
+    ref_scale = (pages.abs().amax(dim=(2, 3)) / 448.0).clamp_min(1e-8)
+    ref_codes = (pages / ref_scale[:, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    np.testing.assert_array_equal(scale, ref_scale.numpy())
+    np.testing.assert_array_equal(codes, ref_codes.numpy())
