@@ -1,26 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the attention forward hot path on one MI355X.
 
-Headline line (BASELINE.json metric, config C2): bf16 causal prefill,
-q/k/v ~ N(0,1) [4, 32, 4096, 128], fp32 accumulate, bf16 out, inputs resident
-in HBM. A step is one ``cuda_llm.flash_attention`` call; FLOPs per step follow
-the reference's convention 2*B*H*S^2*D for causal (benchmark_pytorch.py:115-117).
-The same JSON line carries, under "fp8_decode", the second half of the
-metric: FP8 paged GQA decode at config C4 (N=256, Hq=32/Hkv=8, D=128,
-L ~ U[2048, 32768], e4m3 cache with per-(page, kv-head) scales), whose
-algorithmic bytes are the K/V bytes of the context tokens plus scales, q, out
-and block-table entries.
+Headline (BASELINE.json metric, config C2): bf16 causal prefill, q/k/v ~ N(0,1)
+[4, 32, 4096, 128], fp32 accumulate, bf16 out, inputs resident in HBM. A step
+is one ``cuda_llm.flash_attention`` call; FLOPs per step follow the
+reference's convention 2*B*H*S^2*D for causal, 4*B*H*S^2*D otherwise
+(benchmark_pytorch.py:115-117).
+
+The same JSON line carries, under "fp8_decode", the metric's second half:
+FP8 paged GQA decode at C4 (N=256, Hq=32/Hkv=8, D=128, L ~ U[2048, 32768],
+e4m3 cache with per-(page, kv-head) fp32 scales). Its algorithmic bytes are
+the K/V codes of the context tokens, the scales of the pages read, q, out and
+the block-table entries. "extra" holds the other BASELINE configs (C2'
+non-causal prefill, C3 bf16 paged decode, C5 MXFP8) and a plain copy used to
+calibrate HBM counters.
 
 Timing: W untimed warm-up steps, then K steps between HIP events recorded on
-the stream the kernels run on (torch's current stream), bracketed by
-device synchronisation. ``cpu_baseline`` times the numpy oracle on a bounded
-sample of the same workload on this host's cores.
+the stream the kernels run on (torch's current stream), bracketed by device
+synchronisation. ``cpu_baseline`` times the numpy oracle on a bounded sample
+of the same inputs on this host's cores (a reported baseline only).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|copy]
 """
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -30,6 +34,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16/fp16 MFMA (published)
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 / MXFP8 MFMA (published)
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
 
 
@@ -55,7 +60,8 @@ def time_steps(fn, steps, warmup):
 
 def _traffic(key):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, copy-kernel calibrated), committed in profiles/traffic.json."""
+    WRITE_SIZE, scaled by the copy-kernel calibration), committed in
+    profiles/traffic.json."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
@@ -74,112 +80,141 @@ def blas_threads():
         return os.cpu_count()
 
 
+def _gen(seed=0):
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
 # ---------------------------------------------------------------------------
-# C2 prefill
+# workloads: each returns dict(ms, value, unit, bound, peak, state...)
 # ---------------------------------------------------------------------------
-def bench_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
+def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
     import torch
     import cuda_llm
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0)
+    g = _gen()
     q, k, v = (torch.randn(B, H, S, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
-    fn = lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal)
-    ms = time_steps(fn, steps, warmup)
+    ms = time_steps(lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal), steps, warmup)
     flops = (2.0 if causal else 4.0) * B * H * S * S * D
-    return dict(ms=ms, flops=flops, tflops=flops / (ms * 1e-3) / 1e12, q=q, k=k, v=v)
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, value=tf, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_TFLOPS,
+                work=flops, qkv=(q, k, v), causal=causal,
+                config={"workload": f"C2{'' if causal else chr(39)} bf16 {'causal' if causal else 'non-causal'} prefill (flash_attention)",
+                        "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal})
 
 
-def cpu_baseline_prefill(q, k, v, causal, seconds):
+def cpu_prefill(r, seconds):
     """Oracle (numpy fp32) on as many (b, h) heads of the same inputs as fit in
     ~``seconds``; heads are independent, so the rate scales exactly."""
     import oracle
+    q, k, v = r["qkv"]
     B, H, S, D = q.shape
-    pairs = [(b, h) for b in range(B) for h in range(H)]
-    done = 0
-    el = 0.0  # oracle time only; device->host copies are excluded
-    for (b, h) in pairs:
-        qq = q[b:b + 1, h:h + 1].float().cpu().numpy()
-        kk = k[b:b + 1, h:h + 1].float().cpu().numpy()
-        vv = v[b:b + 1, h:h + 1].float().cpu().numpy()
-        t1 = time.perf_counter()
-        oracle.attention(qq, kk, vv, is_causal=causal)
-        el += time.perf_counter() - t1
-        done += 1
+    done, el = 0, 0.0  # oracle time only; device->host copies excluded
+    for b in range(B):
+        for h in range(H):
+            qq, kk, vv = (t[b:b + 1, h:h + 1].float().cpu().numpy() for t in (q, k, v))
+            t1 = time.perf_counter()
+            oracle.attention(qq, kk, vv, is_causal=r["causal"])
+            el += time.perf_counter() - t1
+            done += 1
+            if el >= seconds:
+                break
         if el >= seconds:
             break
-    flops = (2.0 if causal else 4.0) * S * S * D * done
+    flops = (2.0 if r["causal"] else 4.0) * S * S * D * done
     return dict(value=flops / el / 1e12, unit="TFLOP/s", cores=blas_threads(), kind="port",
-                sample=f"{done} of {B * H} (b,h) heads of the same C2 inputs, numpy fp32 oracle "
+                sample=f"{done} of {B * H} (b,h) heads of the same inputs, numpy fp32 oracle "
                        f"(oracle/attention.py), {el:.1f} s")
 
 
-# ---------------------------------------------------------------------------
-# C4 FP8 paged decode
-# ---------------------------------------------------------------------------
-def make_c4(seed=0, N=256, Hq=32, Hkv=8, D=128, lo=2048, hi=32768):
+def make_paged(N, Hq, Hkv, D, lens, fp8, pool=None, seed=0):
     import torch
-    gc = torch.Generator().manual_seed(seed)
-    lens = torch.randint(lo, hi + 1, (N,), generator=gc)
     pages = (lens + 15) // 16
-    P = int(pages.sum())
+    need = int(pages.sum())
+    P = max(pool or need, need)
     dev = torch.device("cuda")
-    g = torch.Generator(device=dev)
-    g.manual_seed(seed)
+    g = _gen(seed)
     perm = torch.randperm(P, device=dev, generator=g).to(torch.int32)
     max_blocks = int(pages.max())
     tables = torch.zeros(N, max_blocks, dtype=torch.int32, device=dev)
     starts = torch.cumsum(pages, 0) - pages
     for i in range(N):
         tables[i, :int(pages[i])] = perm[int(starts[i]):int(starts[i]) + int(pages[i])]
-    kc = torch.empty(P, Hkv, D, 16, dtype=torch.uint8, device=dev)
-    vc = torch.empty_like(kc)
-    ks = torch.empty(P, Hkv, dtype=torch.float32, device=dev)
-    vs = torch.empty_like(ks)
+    case = dict(tables=tables, lens=lens.to(torch.int32).to(dev), lens_host=lens.tolist(), P=P)
     chunk = 32768
-    for c0 in range(0, P, chunk):
-        c1 = min(P, c0 + chunk)
-        for cache, sc in ((kc, ks), (vc, vs)):
-            x = torch.randn(c1 - c0, Hkv, D, 16, device=dev, generator=g)
-            s = (x.abs().amax(dim=(2, 3)) / 448.0).clamp_min(1e-8)
-            cache[c0:c1] = (x / s[:, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
-            sc[c0:c1] = s
-    q = torch.randn(N, Hq, D, device=dev, generator=g).to(torch.bfloat16)
-    lens_d = lens.to(torch.int32).to(dev)
-    total_tokens = int(lens.sum())
-    alg_bytes = (total_tokens * Hkv * D * 2          # K + V e4m3 codes of the context tokens
-                 + int(pages.sum()) * Hkv * 4 * 2    # k/v scales of the pages read
-                 + 2 * N * Hq * D * 2                # q in, out
-                 + int(pages.sum()) * 4 + N * 4)     # block-table entries, context lengths
-    return dict(query=q, kc=kc, vc=vc, ks=ks, vs=vs, tables=tables, lens=lens_d,
-                lens_host=lens.tolist(), alg_bytes=alg_bytes, P=P)
+    if fp8:
+        kc = torch.empty(P, Hkv, D, 16, dtype=torch.uint8, device=dev)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(P, Hkv, dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        for c0 in range(0, P, chunk):
+            c1 = min(P, c0 + chunk)
+            for cache, sc in ((kc, ks), (vc, vs)):
+                x = torch.randn(c1 - c0, Hkv, D, 16, device=dev, generator=g)
+                s = (x.abs().amax(dim=(2, 3)) / 448.0).clamp_min(1e-8)
+                cache[c0:c1] = (x / s[:, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+                sc[c0:c1] = s
+        case.update(kc=kc, vc=vc, ks=ks, vs=vs)
+    else:
+        kc = torch.empty(P, Hkv, D, 16, dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        for c0 in range(0, P, chunk):
+            c1 = min(P, c0 + chunk)
+            kc[c0:c1] = torch.randn(c1 - c0, Hkv, D, 16, device=dev, generator=g).to(torch.bfloat16)
+            vc[c0:c1] = torch.randn(c1 - c0, Hkv, D, 16, device=dev, generator=g).to(torch.bfloat16)
+        case.update(kc=kc, vc=vc)
+    case["query"] = torch.randn(N, Hq, D, device=dev, generator=g).to(torch.bfloat16)
+    elem = 1 if fp8 else 2
+    case["alg_bytes"] = (int(lens.sum()) * Hkv * D * 2 * elem     # K + V of the context tokens
+                         + (need * Hkv * 4 * 2 if fp8 else 0)     # k/v scales of the pages read
+                         + 2 * N * Hq * D * 2                     # q in, out
+                         + need * 4 + N * 4)                      # block-table entries, lengths
+    return case
 
 
-def bench_fp8_decode(steps, warmup):
+def w_decode(steps, warmup, fp8):
     import torch
     import cuda_llm
-    c = make_c4()
-    fn = lambda: cuda_llm.fp8_paged_attention_forward(c["query"], c["kc"], c["vc"], c["ks"], c["vs"],
-                                                      c["tables"], c["lens"])
+    gc = torch.Generator().manual_seed(0)
+    if fp8:   # C4
+        N, lens, pool = 256, torch.randint(2048, 32769, (256,), generator=gc), None
+    else:     # C3
+        N, lens, pool = 64, torch.randint(512, 8193, (64,), generator=gc), 40000
+    c = make_paged(N, 32, 8, 128, lens, fp8, pool=pool)
+    if fp8:
+        fn = lambda: cuda_llm.fp8_paged_attention_forward(c["query"], c["kc"], c["vc"], c["ks"], c["vs"],
+                                                          c["tables"], c["lens"])
+    else:
+        fn = lambda: cuda_llm.paged_attention_forward(c["query"], c["kc"], c["vc"], c["tables"], c["lens"])
     ms = time_steps(fn, steps, warmup)
     gbs = c["alg_bytes"] / (ms * 1e-3) / 1e9
-    return dict(ms=ms, gbs=gbs, case=c)
+    name = "C4 FP8 paged GQA decode" if fp8 else "C3 bf16 paged GQA decode"
+    return dict(ms=ms, value=gbs, unit="GB/s", bound="hbm", peak=PEAK_HBM_GBS, work=c["alg_bytes"],
+                case=c, fp8=fp8,
+                config={"workload": name, "num_seqs": N, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+                        "page": 16, "context": "U[2048, 32768]" if fp8 else "U[512, 8192]",
+                        "pool_pages": c["P"], "alg_bytes_per_step": c["alg_bytes"]})
 
 
-def cpu_baseline_decode(c, seconds):
+def cpu_decode(r, seconds):
     import numpy as np
     import oracle
-    done_tokens = 0
-    done = 0
-    t0 = time.perf_counter()
+    c = r["case"]
+    done_tokens = done = 0
     el = 0.0
-    for i in range(len(c["lens_host"])):
-        L = c["lens_host"][i]
+    for i, L in enumerate(c["lens_host"]):
         nb = (L + 15) // 16
         ids = c["tables"][i, :nb].long()
-        kc = c["kc"].index_select(0, ids).cpu().numpy()
-        vc = c["vc"].index_select(0, ids).cpu().numpy()
-        ks = c["ks"].index_select(0, ids).cpu().numpy()
-        vs = c["vs"].index_select(0, ids).cpu().numpy()
+        kc = c["kc"].index_select(0, ids)
+        vc = c["vc"].index_select(0, ids)
+        if r["fp8"]:
+            kc, vc = kc.cpu().numpy(), vc.cpu().numpy()
+            ks = c["ks"].index_select(0, ids).cpu().numpy()
+            vs = c["vs"].index_select(0, ids).cpu().numpy()
+        else:
+            kc, vc = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+            ks = vs = None
         q = c["query"][i:i + 1].float().cpu().numpy()
         t1 = time.perf_counter()
         oracle.paged_decode(q, kc, vc, np.arange(nb)[None], [L], k_scale=ks, v_scale=vs)
@@ -190,16 +225,71 @@ def cpu_baseline_decode(c, seconds):
             break
     bytes_per_token = c["alg_bytes"] / sum(c["lens_host"])
     return dict(value=done_tokens * bytes_per_token / el / 1e9, unit="GB/s", cores=blas_threads(),
-                kind="port", sample=f"{done} of {len(c['lens_host'])} sequences of the same C4 inputs, "
+                kind="port", sample=f"{done} of {len(c['lens_host'])} sequences of the same inputs, "
                                     f"numpy oracle (oracle/paged.py), {el:.1f} s")
 
 
+def w_mxfp8(steps, warmup, B=1, H=16, S=8192, D=128):
+    import torch
+    import cuda_llm
+    g = _gen()
+    x = {}
+    for n in "qkv":
+        v = torch.randn(B, H, S, D, device="cuda", generator=g) * \
+            torch.empty(B, H, S, D, device="cuda").uniform_(0.5, 4, generator=g)
+        blk = v.view(B, H, S, D // 32, 32)
+        amax = blk.abs().amax(-1)
+        e = torch.floor(torch.log2(amax)) - 8
+        sc = torch.ldexp(torch.ones_like(e), e.to(torch.int32))
+        x[n] = (blk / sc[..., None]).clamp(-448, 448).to(torch.float8_e4m3fn).view(B, H, S, D)
+        x[n + "s"] = (e + 127).to(torch.uint8)
+    fn = lambda: cuda_llm.fused_microscaled_attention(x["q"], x["qs"], x["k"], x["ks"], x["v"], x["vs"],
+                                                      is_causal=True)
+    ms = time_steps(fn, steps, warmup)
+    flops = 2.0 * B * H * S * S * D
+    return dict(ms=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s", bound="mfma",
+                peak=PEAK_FP8_TFLOPS, work=flops,
+                config={"workload": "C5 MXFP8 causal attention", "batch": B, "heads": H, "seq_len": S,
+                        "head_dim": D, "note": "QK on fp8 scaled MFMA, PV on bf16 MFMA"})
+
+
+def w_copy(steps, warmup, nbytes=2 << 30):
+    import torch
+    x = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    ms = time_steps(lambda: y.copy_(x), steps, warmup)
+    return dict(ms=ms, value=2 * nbytes / (ms * 1e-3) / 1e9, unit="GB/s", bound="hbm",
+                peak=PEAK_HBM_GBS, work=2 * nbytes,
+                config={"workload": "device copy (HBM counter calibration)", "bytes": nbytes})
+
+
+WORKLOADS = {
+    "prefill": lambda s, w: w_prefill(s, w, causal=True),
+    "prefill_nc": lambda s, w: w_prefill(s, w, causal=False, S=2048),
+    "decode_fp8": lambda s, w: w_decode(s, w, fp8=True),
+    "decode_bf16": lambda s, w: w_decode(s, w, fp8=False),
+    "mxfp8": w_mxfp8,
+    "copy": w_copy,
+}
+TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
+               "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5"}
+
+
+def summary(name, r):
+    out = {"value": round(r["value"], 2), "unit": r["unit"], "ms_per_step": round(r["ms"], 4),
+           "config": r["config"],
+           "roofline": {"bound": r["bound"], "achieved": round(r["value"], 2), "peak": r["peak"],
+                        "unit": r["unit"], "frac": round(r["value"] / r["peak"], 4),
+                        "traffic": _traffic(TRAFFIC_KEY.get(name, name))}}
+    return out
+
+
 def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap = argparse.ArgumentParser(description="attention forward hot path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-secondary", action="store_true", help="skip the FP8 decode measurement")
+    ap.add_argument("--workload", default="all", choices=["all"] + list(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
@@ -215,54 +305,52 @@ def main():
     torch.cuda.set_device(0)
     props = torch.cuda.get_device_properties(0)
 
-    log("prefill C2 ...")
-    pf = bench_prefill(args.steps, args.warmup)
-    log(f"prefill: {pf['ms']:.3f} ms/step, {pf['tflops']:.1f} TFLOP/s")
+    head = "prefill" if args.workload == "all" else args.workload
+    log(f"{head} ...")
+    r = WORKLOADS[head](args.steps, args.warmup)
+    log(f"{head}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
+    s = summary(head, r)
     line = {
-        "metric": "prefill TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
-        "value": round(pf["tflops"], 2),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(pf["ms"], 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: q/k/v ~ N(0,1) cast to bf16, seed 0, resident in HBM",
-        "config": {"workload": "C2 bf16 causal prefill (flash_attention)", "batch": 4, "heads": 32,
-                   "seq_len": 4096, "head_dim": 128, "causal": True, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "mfma", "achieved": round(pf["tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(pf["tflops"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": _traffic("prefill_c2_causal")},
+        "metric": {"prefill": "prefill TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
+                   "prefill_nc": "prefill TFLOP/s (bf16 non-causal, B=4 H=32 S=2048 D=128)",
+                   "decode_fp8": "FP8 paged GQA decode HBM GB/s (C4)",
+                   "decode_bf16": "bf16 paged GQA decode HBM GB/s (C3)",
+                   "mxfp8": "MXFP8 causal attention TFLOP/s (C5)",
+                   "copy": "device copy GB/s"}[head],
+        "value": s["value"], "unit": s["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": s["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": {"prefill": "bf16", "prefill_nc": "bf16", "decode_fp8": "e4m3 KV / bf16 q,out / fp32 softmax",
+                  "decode_bf16": "bf16", "mxfp8": "mxfp8 e4m3+e8m0 / bf16 out", "copy": "bf16"}[head],
+        "data": "synthetic, seeded (torch generator seed 0), resident in HBM",
+        "config": dict(s["config"], parallelism="none (1 GPU)"),
+        "roofline": s["roofline"],
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
-    if not args.no_cpu_baseline:
-        log("cpu baseline (prefill) ...")
-        line["cpu_baseline"] = cpu_baseline_prefill(pf["q"], pf["k"], pf["v"], True, args.cpu_seconds)
-    del pf
+    if not args.no_cpu_baseline and head in ("prefill", "prefill_nc", "decode_fp8", "decode_bf16"):
+        log("cpu baseline ...")
+        line["cpu_baseline"] = (cpu_prefill if head.startswith("prefill") else cpu_decode)(r, args.cpu_seconds)
+    del r
     torch.cuda.empty_cache()
 
-    if not args.no_secondary:
-        log("fp8 paged decode C4 ...")
-        dc = bench_fp8_decode(args.steps, args.warmup)
-        log(f"fp8 decode: {dc['ms']:.3f} ms/step, {dc['gbs']:.1f} GB/s")
-        sec = {
-            "metric": "FP8 paged GQA decode HBM GB/s (C4)",
-            "value": round(dc["gbs"], 1), "unit": "GB/s", "ms_per_step": round(dc["ms"], 4),
-            "dtype": "e4m3 KV, bf16 q/out, fp32 softmax",
-            "config": {"workload": "C4 FP8 paged decode", "num_seqs": 256, "q_heads": 32,
-                       "kv_heads": 8, "head_dim": 128, "page": 16, "context": "U[2048, 32768]",
-                       "pool_pages": dc["case"]["P"], "alg_bytes_per_step": dc["case"]["alg_bytes"]},
-            "roofline": {"bound": "hbm", "achieved": round(dc["gbs"], 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(dc["gbs"] / PEAK_HBM_GBS, 4),
-                         "traffic": _traffic("fp8_decode_c4")},
-        }
+    if args.workload == "all":
+        r = WORKLOADS["decode_fp8"](args.steps, args.warmup)
+        log(f"decode_fp8: {r['ms']:.4f} ms/step, {r['value']:.1f} GB/s")
+        sec = summary("decode_fp8", r)
+        sec["metric"] = "FP8 paged GQA decode HBM GB/s (C4)"
         if not args.no_cpu_baseline:
-            log("cpu baseline (decode) ...")
-            sec["cpu_baseline"] = cpu_baseline_decode(dc["case"], args.cpu_seconds)
+            sec["cpu_baseline"] = cpu_decode(r, args.cpu_seconds)
         line["fp8_decode"] = sec
+        del r
+        torch.cuda.empty_cache()
+        extra = {}
+        for name in ("prefill_nc", "decode_bf16", "mxfp8"):
+            r = WORKLOADS[name](args.steps, args.warmup)
+            log(f"{name}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
+            extra[name] = summary(name, r)
+            del r
+            torch.cuda.empty_cache()
+        line["extra"] = extra
     print(json.dumps(line), flush=True)
 
 

@@ -215,8 +215,12 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
       for (int j = 0; j < 4; ++j) {
         const float p0 = fast_exp2(x[b0 + 2 * j] - msub);
         const float p1 = fast_exp2(x[b0 + 2 * j + 1] - msub);
-        psum += p0 + p1;
         const vec2 pk = BF16::pack2(p0, p1);
+        // the row sum uses the bf16-rounded weights that enter PV, so o / l is
+        // an exact weighted mean of V under slightly perturbed weights; with
+        // MX data |v| reaches ~16 and the unrounded sum would put the P
+        // rounding error (up to 2^-9 relative) straight into |o|
+        psum += (float)pk[0] + (float)pk[1];
         pb[kk][2 * j] = pk[0];
         pb[kk][2 * j + 1] = pk[1];
       }
