@@ -44,6 +44,12 @@ struct BF16 {
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // 16x16x16: 4 elements of k per lane (k = 4 * (lane / 16) + 0..3)
+  static __device__ __forceinline__ f32x4 mfma16k16(vec4 a, vec4 b, f32x4 c) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                     __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+  }
   static __device__ __forceinline__ vec4 tr_read(const CA_LDS void* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((CA_LDS vec4*)p);
   }
@@ -68,6 +74,9 @@ struct F16 {
   }
   static __device__ __forceinline__ f32x4 mfma16(vec8 a, vec8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16k16(vec4 a, vec4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ vec4 tr_read(const CA_LDS void* p) {
     typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));

@@ -10,24 +10,26 @@
 // dispatch_async_flash_decode (kernels_api.h:58-62). The reference walks each
 // (sequence, head) serially in one block; here contexts are split.
 //
-// Work decomposition (split-K)
-//   workgroup = (sequence n, kv head, query-head chunk of <= 16, split);
-//   a split covers kPagesPerSplit pages of 16 tokens, 4 waves x 16 pages;
-//   each wave walks its pages two at a time with the next two prefetched.
+// Work decomposition (split-K, one wave per split)
+//   a wave owns (sequence n, kv head, query-head chunk of <= 16, split) and
+//   walks kPagesPerWave pages of 16 tokens, two pages per step, with the next
+//   step's K and V already in flight in a second register set (the step loop
+//   is unrolled by two so the sets swap roles without copies). Waves never
+//   synchronise; a workgroup is just four independent waves.
 //   The GQA group of query heads (Hq / Hkv <= 16 per chunk) shares every K/V
 //   byte loaded, so each cache byte is read from HBM once per kv head.
-// Per wave and two pages (16x16x32 MFMAs, query heads padded to 16):
-//   S^T[16 tok x 16 heads] = K^T Q^T per page; the page is [D][16] with
-//   tokens contiguous, so the K^T operand (8 consecutive d for one token) is
-//   read from a wave-private LDS copy with ds_read_b64_tr_b16 / _tr_b8;
-//   online softmax over tokens, lazily rescaled;
-//   O[16 heads x D] += P V^T over the 32 tokens; the V^T operand (tokens
-//   contiguous for one d) comes straight from HBM in operand layout.
+// Per wave and step (16x16x32 MFMAs, query heads padded to 16):
+//   S^T[16 tok x 16 heads] = K^T Q^T per page; a page is [D][16] with tokens
+//   contiguous, so the K^T operand (8 consecutive d for one token) is read
+//   from a wave-private LDS copy with ds_read_b64_tr_b16 / _tr_b8;
+//   online softmax over tokens, rescaled only when the max grows by > 2^8;
+//   O[16 heads x D] += P V^T over the step's 32 tokens; the V^T operand
+//   (tokens contiguous for one d) is loaded from HBM in operand layout.
 //   FP8: codes are converted exactly to the MFMA element type; the k scale of
 //   a page multiplies that page's logits and the v scale is folded into P.
-// The 4 waves merge through LDS; a sequence with one split writes its output
-// directly, otherwise a partial (o / l, log2-sum-exp) goes to the workspace
-// and decode_merge_kernel combines the splits.
+// A sequence that fits one split writes its output directly; otherwise each
+// wave writes (o / l, log2-sum-exp) to the workspace and decode_merge_kernel
+// combines the splits.
 #include "common.h"
 #include "launch.h"
 
@@ -48,76 +50,102 @@ struct Fp8Conv<F16> {
   static __device__ __forceinline__ F16::vec2 cvt(uint32_t w) { return e4m3x2_to_f16<HI>(w); }
 };
 
+// 8 e4m3 codes (two dwords) -> 8 values of the MFMA element type; each
+// conversion fills one dword, so the operand is assembled without shuffles
 template <typename Tr>
 __device__ __forceinline__ typename Tr::vec8 fp8x8_to(uint32_t lo, uint32_t hi) {
-  using vec2 = typename Tr::vec2;
-  using vec8 = typename Tr::vec8;
-  const vec2 a = Fp8Conv<Tr>::template cvt<false>(lo), b = Fp8Conv<Tr>::template cvt<true>(lo);
-  const vec2 c = Fp8Conv<Tr>::template cvt<false>(hi), d = Fp8Conv<Tr>::template cvt<true>(hi);
-  vec8 r;
-  r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-  r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-  return r;
+  const u32x4 r = {__builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(lo)),
+                   __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(lo)),
+                   __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(hi)),
+                   __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(hi))};
+  return __builtin_bit_cast(typename Tr::vec8, r);
+}
+
+// Streaming loads: every cache byte is used once per launch, so they bypass
+// the cache hierarchy's retention (non-temporal).
+template <typename T>
+__device__ __forceinline__ T ld_stream(const void* p) {
+  return __builtin_nontemporal_load((const T*)p);
 }
 
 template <int D, int KIND>
-struct DecodeLds {
-  // per-wave staging of the two pages of one step
-  //   paged 16-bit: K pages [D][16] with a 64-element gap every 8 rows
-  //   paged fp8:    K pages [D][16] bytes, no gap
-  //   contiguous:   V rows [32][D + 16]
+struct DecodeGeom {
+  static constexpr int NKS = D / 32;  // S^T k-steps (32 d each)
+  static constexpr int NB = D / 16;   // PV output blocks (16 d each)
+  // 16-byte chunks per lane of one page: 16-bit [D][16] = D/32, fp8 = D/64;
+  // contiguous: the K^T operand itself, NKS x 16 B per page
+  static constexpr int KREG = KIND == kKindPaged16 ? D / 32 : KIND == kKindPagedFp8 ? D / 64 : NKS;
+  // contiguous V: 16 rows x D of one page as 16-byte chunks per lane
+  static constexpr int VROWREG = (16 * D * 2) / (64 * 16);
+  // wave-private LDS: paged 16-bit K pages [D][16] with a 64-element gap
+  // every 8 rows (conflict-free tr16 reads), fp8 K pages [D][16] bytes,
+  // contiguous V rows [32][D + 16]
   static constexpr int kPaged16PageElems = D * 16 + (D / 8) * 64;
-  static constexpr int kBytesPerWave =
-      KIND == kKindPaged16 ? 2 * kPaged16PageElems * 2
-      : KIND == kKindPagedFp8 ? 2 * D * 16
-                              : 32 * (D + 16) * 2;
-  static constexpr int kStageBytes = kDecodeWaves * kBytesPerWave;
-  static constexpr int kMergeBytes = kDecodeWaves * 16 * D * 4;
-  static constexpr int kBytes = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
+  static constexpr int kLdsBytesPerWave = KIND == kKindPaged16 ? 2 * kPaged16PageElems * 2
+                                          : KIND == kKindPagedFp8 ? 2 * D * 16
+                                                                  : 32 * (D + 16) * 2;
+};
+
+// Registers of one step (two pages): K and V as loaded from HBM.
+template <int D, int KIND>
+struct StepRegs {
+  using G = DecodeGeom<D, KIND>;
+  u32x4 k[2][G::KREG];
+  u32x2 v16[2][KIND == kKindPaged16 ? G::NB : 1];
+  uint32_t v8[2][KIND == kKindPagedFp8 ? G::NB : 1];
+  u32x4 vrow[2][KIND == kKindContig16 ? G::VROWREG : 1];
 };
 
 template <typename Tr, int D, int KIND>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
+// waves per SIMD: fp8 steps fit 3 (168 VGPRs), 16-bit steps carry twice the
+// bytes in flight and fit 2
+__global__ __launch_bounds__(kDecodeWgWaves * 64)
+__attribute__((amdgpu_waves_per_eu(KIND == kKindPagedFp8 ? 3 : 2, KIND == kKindPagedFp8 ? 3 : 2)))
+void decode_split_kernel(
     const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
     const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
     uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
     int Hkv, int max_blocks, int num_blocks, int S_contig, int max_splits, int n_hc,
-    float scale_log2) {
+    long long total_waves, float scale_log2) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
-  constexpr int NKS = D / 32;  // S^T k-steps (32 d each)
-  constexpr int NB = D / 16;   // PV output blocks (16 d each)
-  using L = DecodeLds<D, KIND>;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[L::kBytes];
-  __shared__ float m_w[kDecodeWaves][16], l_w[kDecodeWaves][16];
+  using G = DecodeGeom<D, KIND>;
+  constexpr int NKS = G::NKS, NB = G::NB;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kDecodeWgWaves * G::kLdsBytesPerWave];
+
+  // the wave index is uniform: readfirstlane keeps every per-wave quantity
+  // derived from it (work item, page range, masks) in scalar registers
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const long long wid = (long long)blockIdx.x * kDecodeWgWaves + wave;
+  if (wid >= total_waves) return;
 
   // ---- work item ----
-  int w = blockIdx.x;
-  const int split = w % max_splits;
+  long long w = wid;
+  const int split = (int)(w % max_splits);
   w /= max_splits;
-  const int hc = w % n_hc;
+  const int hc = (int)(w % n_hc);
   w /= n_hc;
-  const int hk = w % Hkv;
-  const int n = w / Hkv;
-  const int G = Hq / Hkv;
-  const int hq0 = hk * G + hc * 16;
-  const int Gc = min(16, G - hc * 16);
+  const int hk = (int)(w % Hkv);
+  const int n = (int)(w / Hkv);
+  const int Gq = Hq / Hkv;
+  const int hq0 = hk * Gq + hc * 16;
+  const int Gc = min(16, Gq - hc * 16);
 
   // a context longer than its block-table row is cut to the row (never read
   // past block_tables[n][max_blocks - 1])
   const int Lctx = (KIND == kKindContig16) ? S_contig
                                            : min(max(0, context_lens[n]), max_blocks * kDecodePage);
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = max(1, (n_pages + kPagesPerSplit - 1) / kPagesPerSplit);
+  const int n_splits = max(1, (n_pages + kPagesPerWave - 1) / kPagesPerWave);
   if (split >= n_splits) return;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, grp = lane >> 4;
-  const int p_begin = split * kPagesPerSplit + wave * kPagesPerWave;
+  const int p_begin = split * kPagesPerWave;
   const int p_end = min(p_begin + kPagesPerWave, n_pages);
-  const int n_steps = p_end > p_begin ? (p_end - p_begin + 1) / 2 : 0;
+  const int n_steps = (p_end - p_begin + 1) / 2;  // 0 only for an empty context
 
   // ---- Q^T operand: lane (head g = l16, k-group grp) ----
   vec8 qv[NKS];
@@ -134,17 +162,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
     }
   }
 
-  // ---- page ids and per-page scales (lane j < 16 holds page p_begin + j) ----
+  // ---- page ids and per-page scales: lane j < kPagesPerWave holds page p_begin + j ----
   int pid_lane = 0;
   float ksc_lane = 1.f, vsc_lane = 1.f;
   if (KIND != kKindContig16) {
-    if (l16 == lane && p_begin + lane < p_end) {
+    if (lane < kPagesPerWave && p_begin + lane < p_end) {
       pid_lane = block_tables[(size_t)n * max_blocks + p_begin + lane];
       pid_lane = min(max(pid_lane, 0), num_blocks - 1);
     }
     if (KIND == kKindPagedFp8) {
       if (per_block) {
-        if (l16 == lane && p_begin + lane < p_end) {
+        if (lane < kPagesPerWave && p_begin + lane < p_end) {
           ksc_lane = k_scale[(size_t)pid_lane * Hkv + hk];
           vsc_lane = v_scale[(size_t)pid_lane * Hkv + hk];
         }
@@ -154,24 +182,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
       }
     }
   }
+  unsigned char* wlds = lds + wave * G::kLdsBytesPerWave;
 
-  unsigned char* wlds = lds + wave * L::kBytesPerWave;
-
-  // ---- prefetch registers for one step (two pages) ----
-  // K: paged 16-bit 4 x 16 B per page, paged fp8 2 x 16 B per page,
-  //    contiguous: the K^T operand itself (NKS x 16 B per page)
-  // V: paged: operand layout (16-bit: NB x 8 B, fp8: NB x 4 B per page),
-  //    contiguous: 4 x 16 B per page of V rows (to LDS)
-  // 16-byte chunks per lane for one page: 16-bit [D][16] = D/32, fp8 = D/64
-  constexpr int KREG = KIND == kKindPaged16 ? D / 32 : KIND == kKindPagedFp8 ? D / 64 : NKS;
-  u32x4 kreg[2][KREG];
-  constexpr int VREG = KIND == kKindContig16 ? (16 * D * 2) / (64 * 16) : NB;
-  u32x4 vreg_c[2][KIND == kKindContig16 ? VREG : 1];
-  u32x2 vreg16[2][KIND == kKindPaged16 ? NB : 1];
-  uint32_t vreg8[2][KIND == kKindPagedFp8 ? NB : 1];
-
-  const size_t head_stride_pages = (size_t)D * 16;  // elements of one (page, head) chunk
-  auto load_step = [&](int step) {
+  // ---- HBM -> registers for one step ----
+  const size_t chunk_elems = (size_t)D * 16;  // one (page, head) chunk
+  auto load_step = [&](StepRegs<D, KIND>& R, int step) {
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       const int page = p_begin + 2 * step + pp;
@@ -182,45 +197,40 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
         const uint16_t* Vp = (const uint16_t*)Vc + base;
         const int tok = page * 16 + l16;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-          if (valid && tok < S_contig)
-            kreg[pp][ks] = *(const u32x4*)(Kp + (size_t)tok * D + 32 * ks + 8 * grp);
-          else
-            kreg[pp][ks] = u32x4{0, 0, 0, 0};
-        }
-        // V rows of the page: 16 rows x D, lanes take 16-byte chunks row-major
+        for (int ks = 0; ks < NKS; ++ks)
+          R.k[pp][ks] = (valid && tok < S_contig)
+                            ? ld_stream<u32x4>(Kp + (size_t)tok * D + 32 * ks + 8 * grp)
+                            : u32x4{0, 0, 0, 0};
         constexpr int CH = D / 8;
 #pragma unroll
-        for (int i = 0; i < VREG; ++i) {
+        for (int i = 0; i < G::VROWREG; ++i) {
           const int c = lane + 64 * i;
-          const int r = c / CH, col = (c % CH) * 8;
-          const int vt = page * 16 + r;
-          if (valid && vt < S_contig)
-            vreg_c[pp][i] = *(const u32x4*)(Vp + (size_t)vt * D + col);
-          else
-            vreg_c[pp][i] = u32x4{0, 0, 0, 0};
+          const int vt = page * 16 + c / CH;
+          R.vrow[pp][i] = (valid && vt < S_contig)
+                              ? ld_stream<u32x4>(Vp + (size_t)vt * D + (c % CH) * 8)
+                              : u32x4{0, 0, 0, 0};
         }
       } else {
         const int pid = __builtin_amdgcn_readlane(pid_lane, 2 * step + pp);
-        const size_t chunk = ((size_t)pid * Hkv + hk) * head_stride_pages;
+        const size_t chunk = ((size_t)pid * Hkv + hk) * chunk_elems;
         if (KIND == kKindPaged16) {
           const uint16_t* Kp = (const uint16_t*)Kc + chunk;
           const uint16_t* Vp = (const uint16_t*)Vc + chunk;
 #pragma unroll
-          for (int i = 0; i < KREG; ++i)
-            kreg[pp][i] = valid ? *(const u32x4*)(Kp + (lane + 64 * i) * 8) : u32x4{0, 0, 0, 0};
+          for (int i = 0; i < G::KREG; ++i)
+            R.k[pp][i] = valid ? ld_stream<u32x4>(Kp + (lane + 64 * i) * 8) : u32x4{0, 0, 0, 0};
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            vreg16[pp][nb] = valid ? *(const u32x2*)(Vp + (16 * nb + l16) * 16 + 4 * grp) : u32x2{0, 0};
+            R.v16[pp][nb] = valid ? ld_stream<u32x2>(Vp + (16 * nb + l16) * 16 + 4 * grp) : u32x2{0, 0};
         } else {
           const unsigned char* Kp = (const unsigned char*)Kc + chunk;
           const unsigned char* Vp = (const unsigned char*)Vc + chunk;
 #pragma unroll
-          for (int i = 0; i < KREG; ++i)
-            kreg[pp][i] = valid ? *(const u32x4*)(Kp + (lane + 64 * i) * 16) : u32x4{0, 0, 0, 0};
+          for (int i = 0; i < G::KREG; ++i)
+            R.k[pp][i] = valid ? ld_stream<u32x4>(Kp + (lane + 64 * i) * 16) : u32x4{0, 0, 0, 0};
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            vreg8[pp][nb] = valid ? *(const uint32_t*)(Vp + (16 * nb + l16) * 16 + 4 * grp) : 0u;
+            R.v8[pp][nb] = valid ? ld_stream<uint32_t>(Vp + (16 * nb + l16) * 16 + 4 * grp) : 0u;
         }
       }
     }
@@ -231,62 +241,38 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
   for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegInf, l_run = 0.f;
 
-  if (n_steps > 0) load_step(0);
-  for (int step = 0; step < n_steps; ++step) {
-    // ---- stage this step's K (paged) or V (contiguous) into wave LDS ----
+  // ---- one step of attention on registers R ----
+  auto compute_step = [&](const StepRegs<D, KIND>& R, int step) {
+    // stage K (paged) or V rows (contiguous) into the wave's LDS
     if (KIND == kKindPaged16) {
       uint16_t* kl = (uint16_t*)wlds;
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-        for (int i = 0; i < KREG; ++i) {
+        for (int i = 0; i < G::KREG; ++i) {
           const int e = (lane + 64 * i) * 8;  // element offset in the [D][16] page
-          const int row = e >> 4;
-          *(u32x4*)(kl + pp * L::kPaged16PageElems + e + (row >> 3) * 64) = kreg[pp][i];
+          *(u32x4*)(kl + pp * G::kPaged16PageElems + e + (e >> 7) * 64) = R.k[pp][i];
         }
     } else if (KIND == kKindPagedFp8) {
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-        for (int i = 0; i < KREG; ++i)
-          *(u32x4*)(wlds + pp * D * 16 + (lane + 64 * i) * 16) = kreg[pp][i];
+        for (int i = 0; i < G::KREG; ++i)
+          *(u32x4*)(wlds + pp * D * 16 + (lane + 64 * i) * 16) = R.k[pp][i];
     } else {
       uint16_t* vl = (uint16_t*)wlds;
       constexpr int CH = D / 8;
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-        for (int i = 0; i < VREG; ++i) {
+        for (int i = 0; i < G::VROWREG; ++i) {
           const int c = lane + 64 * i;
-          const int r = c / CH, col = (c % CH) * 8;
-          *(u32x4*)(vl + (16 * pp + r) * (D + 16) + col) = vreg_c[pp][i];
+          *(u32x4*)(vl + (16 * pp + c / CH) * (D + 16) + (c % CH) * 8) = R.vrow[pp][i];
         }
     }
-    // keep this step's V operand / contiguous K operand before the prefetch
-    // overwrites the registers
-    u32x2 v16[2][KIND == kKindPaged16 ? NB : 1];
-    uint32_t v8[2][KIND == kKindPagedFp8 ? NB : 1];
-    u32x4 kc_cur[2][KIND == kKindContig16 ? NKS : 1];
-    if (KIND == kKindPaged16) {
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) v16[pp][nb] = vreg16[pp][nb];
-    } else if (KIND == kKindPagedFp8) {
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) v8[pp][nb] = vreg8[pp][nb];
-    } else {
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) kc_cur[pp][ks] = kreg[pp][ks];
-    }
     __builtin_amdgcn_wave_barrier();
-    if (step + 1 < n_steps) load_step(step + 1);
 
-    // ---- S^T per page ----
+    // S^T per page
     f32x4 s[2];
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
@@ -296,13 +282,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
         vec8 a;
         if (KIND == kKindPaged16) {
           // tr16: source lane (j = l16/4, c = l16%4) -> row 32ks + 8grp + 4r + j, col 4c
+          const uint16_t* kl = (const uint16_t*)wlds + pp * G::kPaged16PageElems;
           const int row = 32 * ks + 8 * grp + (l16 >> 2);
-          const uint16_t* kl = (const uint16_t*)wlds + pp * L::kPaged16PageElems;
-          const uint16_t* p0 = kl + row * 16 + (row >> 3) * 64 + 4 * (l16 & 3);
           const int row4 = row + 4;
-          const uint16_t* p1 = kl + row4 * 16 + (row4 >> 3) * 64 + 4 * (l16 & 3);
-          const vec4 lo = Tr::tr_read((const CA_LDS void*)p0);
-          const vec4 hi = Tr::tr_read((const CA_LDS void*)p1);
+          const vec4 lo = Tr::tr_read((const CA_LDS void*)(kl + row * 16 + (row >> 3) * 64 + 4 * (l16 & 3)));
+          const vec4 hi = Tr::tr_read((const CA_LDS void*)(kl + row4 * 16 + (row4 >> 3) * 64 + 4 * (l16 & 3)));
           a = cat4<vec8, vec4>(lo, hi);
         } else if (KIND == kKindPagedFp8) {
           // tr8: source lane (j = l16/2, c = l16%2) -> row 32ks + 8grp + j, col 8c
@@ -310,20 +294,20 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
           const i32x2 raw = tr8_read((const CA_LDS void*)(wlds + pp * D * 16 + row * 16 + 8 * (l16 & 1)));
           a = fp8x8_to<Tr>((uint32_t)raw[0], (uint32_t)raw[1]);
         } else {
-          a = __builtin_bit_cast(vec8, kc_cur[pp][ks]);
+          a = __builtin_bit_cast(vec8, R.k[pp][ks]);
         }
         s[pp] = Tr::mfma16(a, qv[ks], s[pp]);
       }
     }
 
-    // ---- online softmax over the 32 tokens of the step ----
+    // online softmax over the step's 32 tokens
     const int pageA = p_begin + 2 * step;
     float cA = scale_log2, cB = scale_log2, vsA = 1.f, vsB = 1.f;
     if (KIND == kKindPagedFp8) {
-      cA *= __shfl(ksc_lane, 2 * step, 64);
-      cB *= __shfl(ksc_lane, 2 * step + 1, 64);
-      vsA = __shfl(vsc_lane, 2 * step, 64);
-      vsB = __shfl(vsc_lane, 2 * step + 1, 64);
+      cA *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), 2 * step));
+      cB *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), 2 * step + 1));
+      vsA = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), 2 * step));
+      vsB = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), 2 * step + 1));
     }
     float x[8];
 #pragma unroll
@@ -376,16 +360,14 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
       pa[4 + 2 * j + 1] = ub[1];
     }
 
-    // ---- O += P V^T ----
+    // O += P V^T
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       vec8 bv;
       if (KIND == kKindPaged16) {
-        const vec4 lo = __builtin_bit_cast(vec4, v16[0][nb]);
-        const vec4 hi = __builtin_bit_cast(vec4, v16[1][nb]);
-        bv = cat4<vec8, vec4>(lo, hi);
+        bv = cat4<vec8, vec4>(__builtin_bit_cast(vec4, R.v16[0][nb]), __builtin_bit_cast(vec4, R.v16[1][nb]));
       } else if (KIND == kKindPagedFp8) {
-        bv = fp8x8_to<Tr>(v8[0][nb], v8[1][nb]);
+        bv = fp8x8_to<Tr>(R.v8[0][nb], R.v8[1][nb]);
       } else {
         // tr16: source lane (j = l16/4, c = l16%4) -> row (16pp + 4grp + j), col 16nb + 4c
         const uint16_t* vl = (const uint16_t*)wlds;
@@ -403,85 +385,499 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_split_kernel(
       o[nb] = Tr::mfma16(pa, bv, o[nb]);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- the walk: register sets A and B alternate ----
+  StepRegs<D, KIND> A, B;
+  if (n_steps > 0) load_step(A, 0);
+  for (int step = 0; step < n_steps; step += 2) {
+    if (step + 1 < n_steps) load_step(B, step + 1);
+    compute_step(A, step);
+    if (step + 1 >= n_steps) break;
+    if (step + 2 < n_steps) load_step(A, step + 2);
+    compute_step(B, step + 1);
   }
 
-  // ---- per-wave totals: l over the 4 lanes of a head; m is already uniform ----
+  // ---- totals over the 4 lanes of a head; m is already uniform ----
   l_run = pair16_sum(l_run);
   l_run = pair32_sum(l_run);
-
-  __syncthreads();  // staging LDS is reused for the merge
-  float* om = (float*)lds;  // [wave][16][D]
-  if (lane < 16) {
-    m_w[wave][lane] = m_run;
-    l_w[wave][lane] = l_run;
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) om[(wave * 16 + 4 * grp + r) * D + 16 * nb + l16] = o[nb][r];
-  __syncthreads();
-
   const bool single = (n_splits == 1);
-  for (int idx = tid; idx < Gc * D; idx += kDecodeWaves * 64) {
-    const int g = idx / D, d = idx % D;
-    float M = kNegInf;
 #pragma unroll
-    for (int wv = 0; wv < kDecodeWaves; ++wv) M = __builtin_fmaxf(M, m_w[wv][g]);
-    float lsum = 0.f, acc = 0.f;
-    if (M != kNegInf) {
-#pragma unroll
-      for (int wv = 0; wv < kDecodeWaves; ++wv) {
-        const float f = (m_w[wv][g] == kNegInf) ? 0.f : fast_exp2(m_w[wv][g] - M);
-        lsum += l_w[wv][g] * f;
-        acc += om[(wv * 16 + g) * D + d] * f;
-      }
-    }
-    const float val = (lsum > 0.f) ? acc / lsum : 0.f;
+  for (int r = 0; r < 4; ++r) {
+    const int g = 4 * grp + r;
+    const float lg = __shfl(l_run, g, 64);
+    const float mg = __shfl(m_run, g, 64);
+    if (g >= Gc) continue;
+    const float inv = (lg > 0.f) ? 1.f / lg : 0.f;
     const int hq = hq0 + g;
     if (single) {
-      const vec2 pk = Tr::pack2(val, 0.f);
-      O[((size_t)n * Hq + hq) * D + d] = __builtin_bit_cast(uint16_t, pk[0]);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const vec2 pk = Tr::pack2(o[nb][r] * inv, 0.f);
+        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = __builtin_bit_cast(uint16_t, pk[0]);
+      }
     } else {
       const size_t slot = ((size_t)n * Hq + hq) * max_splits + split;
-      ws_o[slot * D + d] = val;
-      if (d == 0) ws_lse[slot] = (lsum > 0.f) ? M + __log2f(lsum) : kNegInf;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) ws_o[slot * D + 16 * nb + l16] = o[nb][r] * inv;
+      if (l16 == 0) ws_lse[slot] = (lg > 0.f) ? mg + __log2f(lg) : kNegInf;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Paged decode with HBM -> LDS direct loads.
+//
+// Same math and work split as decode_split_kernel, but the pages travel from
+// HBM straight into a per-wave LDS ring with global_load_lds_dwordx4 (each
+// lane's 16 bytes land at ring slot + 16 * lane), so bytes in flight cost no
+// VGPRs: a wave keeps kRing - 1 steps (two pages each, K and V) in flight.
+// LDS is read with hand-issued ds_read instructions and the vector-memory
+// counter is waited on explicitly (s_waitcnt vmcnt(N) with N = the loads
+// issued after the step being consumed); the compiler's own conservative
+// wait-for-everything before LDS reads would serialise the ring.
+// Layouts in a ring slot: K pages as loaded ([D][16]; the 16-bit page's
+// 16-byte chunks are XOR-swizzled on bit 3 of the chunk index by row-octet
+// parity so the tr16 reads of lane groups 0/1 and 2/3 hit disjoint banks),
+// V pages linear [D][16].
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)(const CA_LDS void*)p;
+}
+// The LDS reads and waits below are gfx950 instructions; the host pass of
+// the HIP compiler (which also parses device code) gets inert stand-ins.
+#if __HIP_DEVICE_COMPILE__
+#define CA_DEVICE_ASM(...) asm volatile(__VA_ARGS__)
+#else
+#define CA_DEVICE_ASM(...) (void)0
+#endif
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr8(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
+  uint32_t r = a;
+  CA_DEVICE_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_b64(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  CA_DEVICE_ASM("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { CA_DEVICE_ASM("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (dst is
+// wave-uniform: it is passed in M0). Cache policy "nt": every byte is read
+// once per launch, so it is streamed rather than retained.
+#ifndef CA_DMA_POLICY
+#define CA_DMA_POLICY 2
+#endif
+__device__ __forceinline__ void dma16(const void* src, CA_LDS void* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, CA_DMA_POLICY);
+}
+// Orders later uses of `x` after the preceding wait (the asm "rewrites" it).
+template <typename T>
+__device__ __forceinline__ void after_wait(T& x) {
+  CA_DEVICE_ASM("" : "+v"(x));
+}
+
+#ifndef CA_DMA_PPS
+#define CA_DMA_PPS 1
+#endif
+#ifndef CA_RING_FP8
+#define CA_RING_FP8 4
+#endif
+#ifndef CA_RING_16
+#define CA_RING_16 3
+#endif
+// Pages per step and ring depth of the direct-load decode. One page per step
+// keeps a ring slot small (K + V of one page), so more waves fit a CU's LDS
+// and more bytes are in flight per CU; the PV product then runs on 16x16x16
+// MFMAs, whose 4 k-values per lane are exactly the 4 tokens a lane holds.
+template <int KIND>
+struct DmaCfg {
+  static constexpr int kPagesPerStep = CA_DMA_PPS;
+  static constexpr int kRing = KIND == kKindPagedFp8 ? CA_RING_FP8 : CA_RING_16;
+};
+
+template <typename Tr, int D, int KIND>
+__global__ __launch_bounds__(64) void decode_dma_kernel(
+    const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
+    int Hkv, int max_blocks, int num_blocks, int max_splits, int n_hc, float scale_log2) {
+  using vec8 = typename Tr::vec8;
+  using vec4 = typename Tr::vec4;
+  using vec2 = typename Tr::vec2;
+  constexpr int NKS = D / 32, NB = D / 16;
+  constexpr bool FP8 = KIND == kKindPagedFp8;
+  constexpr int ELEM = FP8 ? 1 : 2;
+  constexpr int CHUNK = D * 16 * ELEM;        // bytes of one (page, head) chunk
+  constexpr int NDMA = CHUNK / 1024;          // 16 B x 64 lanes per load
+  constexpr int PPS = DmaCfg<KIND>::kPagesPerStep;
+  constexpr int STAGE = 2 * PPS * CHUNK;      // K and V of the step's pages
+  constexpr int RING = DmaCfg<KIND>::kRing;
+  constexpr int DPS = 2 * PPS * NDMA;         // loads per step
+  constexpr int KRD = FP8 ? NKS : 2 * NKS;    // LDS reads for one page's K^T operands
+  static_assert(PPS == 1 || PPS == 2, "pages per step");
+  static_assert(kPagesPerWave % PPS == 0, "whole steps per split");
+  static_assert((RING - 1) * DPS <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[RING * STAGE];
+
+  const int lane = threadIdx.x;
+  int w = blockIdx.x;
+  const int split = w % max_splits;
+  w /= max_splits;
+  const int hc = w % n_hc;
+  w /= n_hc;
+  const int hk = w % Hkv;
+  const int n = w / Hkv;
+  const int Gq = Hq / Hkv;
+  const int hq0 = hk * Gq + hc * 16;
+  const int Gc = min(16, Gq - hc * 16);
+  const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
+  const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
+  const int n_splits = max(1, (n_pages + kPagesPerWave - 1) / kPagesPerWave);
+  if (split >= n_splits) return;
+
+  const int l16 = lane & 15, grp = lane >> 4;
+  const int p_begin = split * kPagesPerWave;
+  const int p_end = min(p_begin + kPagesPerWave, n_pages);
+  const int n_steps = (p_end - p_begin + PPS - 1) / PPS;
+
+  vec8 qv[NKS];
+  {
+    const uint16_t* qrow = Q + ((size_t)n * Hq + hq0 + l16) * D;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (l16 < Gc) {
+        qv[ks] = *(const vec8*)(qrow + 32 * ks + 8 * grp);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
+      }
+    }
+  }
+  int pid_lane = 0;
+  float ksc_lane = 1.f, vsc_lane = 1.f;
+  if (p_begin + lane < p_end) {
+    pid_lane = block_tables[(size_t)n * max_blocks + p_begin + lane];
+    pid_lane = min(max(pid_lane, 0), num_blocks - 1);
+  }
+  if (FP8) {
+    if (per_block) {
+      if (p_begin + lane < p_end) {
+        ksc_lane = k_scale[(size_t)pid_lane * Hkv + hk];
+        vsc_lane = v_scale[(size_t)pid_lane * Hkv + hk];
+      }
+    } else {
+      ksc_lane = k_scale[hk];
+      vsc_lane = v_scale[hk];
+    }
+  }
+
+  // source byte offset of this lane's 16 bytes for load i of a K chunk
+  auto k_src = [&](int i) -> int {
+    const int p = 64 * i + lane;  // physical 16-byte slot in LDS
+    if (FP8) return 16 * p;
+    return 16 * (p ^ (((p >> 4) & 1) << 3));
+  };
+  const unsigned char* dummy = (const unsigned char*)Q;  // 16 valid bytes for padding loads
+  auto issue_step = [&](int step, int slot) {
+    unsigned char* base = ring + slot * STAGE;
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+      const int page = p_begin + PPS * step + pp;
+      const bool valid = step < n_steps && page < p_end;
+      const int idx = valid ? PPS * step + pp : 0;
+      const int pid = __builtin_amdgcn_readlane(pid_lane, idx);
+      const size_t chunk = ((size_t)pid * Hkv + hk) * (size_t)CHUNK;
+      const unsigned char* kp = (const unsigned char*)Kc + chunk;
+      const unsigned char* vp = (const unsigned char*)Vc + chunk;
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        dma16(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + pp * 2 * CHUNK + 1024 * i));
+        dma16(valid ? vp + 1024 * i + 16 * lane : dummy,
+              (CA_LDS void*)(base + pp * 2 * CHUNK + CHUNK + 1024 * i));
+      }
+    }
+  };
+
+  // per-lane LDS read offsets inside a page's K / V chunk
+  uint32_t k_lo, k_hi;
+  if (FP8) {
+    k_lo = 16 * (8 * grp + (l16 >> 1)) + 8 * (l16 & 1);
+    k_hi = 0;
+  } else {
+    const int c = l16 & 3, j = l16 >> 2, par = grp & 1;
+    k_lo = 16 * (16 * grp + 8 * par + 2 * j + (c >> 1)) + 8 * (c & 1);
+    k_hi = 16 * (16 * grp + 8 * (1 - par) + 2 * j + (c >> 1)) + 8 * (c & 1);
+  }
+  const uint32_t v_off = (uint32_t)(16 * l16 + 4 * grp) * ELEM;
+  const uint32_t ring0 = lds_off(ring);
+
+  f32x4 o[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf, l_run = 0.f;
+
+#pragma unroll
+  // RING steps in flight from the start; a slot is refilled as soon as its
+  // LDS reads have returned, so RING steps stay in flight during the math
+  for (int s = 0; s < RING; ++s) issue_step(s, s);
+  int slot = 0;
+  for (int step = 0; step < n_steps; ++step) {
+    wait_vmcnt<(RING - 1) * DPS>();  // this step's loads are the oldest outstanding
+    const uint32_t sb = ring0 + slot * STAGE;
+
+    // ---- LDS -> operands ----
+    u32x2 kraw[PPS][KRD];
+    uint32_t v8r[PPS][FP8 ? NB : 1];
+    u32x2 v16r[PPS][FP8 ? 1 : NB];
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+      const uint32_t kb = sb + pp * 2 * CHUNK;
+      const uint32_t vb = kb + CHUNK + v_off;
+      if (FP8) {
+        const uint32_t a = kb + k_lo;
+        kraw[pp][0] = lds_read_tr8<0>(a);
+        if (NKS > 1) kraw[pp][1 % KRD] = lds_read_tr8<512>(a);
+        if (NKS > 2) kraw[pp][2 % KRD] = lds_read_tr8<1024>(a);
+        if (NKS > 3) kraw[pp][3 % KRD] = lds_read_tr8<1536>(a);
+#define CA_V8(NBI) if (NBI < NB) v8r[pp][NBI % NB] = lds_read_b32<256 * NBI>(vb);
+        CA_V8(0) CA_V8(1) CA_V8(2) CA_V8(3) CA_V8(4) CA_V8(5) CA_V8(6) CA_V8(7)
+#undef CA_V8
+      } else {
+        const uint32_t alo = kb + k_lo, ahi = kb + k_hi;
+        kraw[pp][0] = lds_read_tr16<0>(alo);
+        kraw[pp][1] = lds_read_tr16<0>(ahi);
+        if (NKS > 1) { kraw[pp][2 % KRD] = lds_read_tr16<1024>(alo); kraw[pp][3 % KRD] = lds_read_tr16<1024>(ahi); }
+        if (NKS > 2) { kraw[pp][4 % KRD] = lds_read_tr16<2048>(alo); kraw[pp][5 % KRD] = lds_read_tr16<2048>(ahi); }
+        if (NKS > 3) { kraw[pp][6 % KRD] = lds_read_tr16<3072>(alo); kraw[pp][7 % KRD] = lds_read_tr16<3072>(ahi); }
+#define CA_V16(NBI) if (NBI < NB) v16r[pp][NBI % NB] = lds_read_b64<512 * NBI>(vb);
+        CA_V16(0) CA_V16(1) CA_V16(2) CA_V16(3) CA_V16(4) CA_V16(5) CA_V16(6) CA_V16(7)
+#undef CA_V16
+      }
+    }
+    wait_lgkm0();
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+#pragma unroll
+      for (int i = 0; i < KRD; ++i) after_wait(kraw[pp][i]);
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (FP8) after_wait(v8r[pp][i % (FP8 ? NB : 1)]);
+        else after_wait(v16r[pp][i % (FP8 ? 1 : NB)]);
+      }
+    }
+    issue_step(step + RING, slot);  // the slot's data is in registers now
+
+    // ---- S^T per page ----
+    f32x4 s[PPS];
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+      s[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        vec8 a;
+        if (FP8) {
+          a = fp8x8_to<Tr>(kraw[pp][ks % KRD][0], kraw[pp][ks % KRD][1]);
+        } else {
+          const u32x4 t = {kraw[pp][(2 * ks) % KRD][0], kraw[pp][(2 * ks) % KRD][1],
+                           kraw[pp][(2 * ks + 1) % KRD][0], kraw[pp][(2 * ks + 1) % KRD][1]};
+          a = __builtin_bit_cast(vec8, t);
+        }
+        s[pp] = Tr::mfma16(a, qv[ks], s[pp]);
+      }
+    }
+
+    // ---- online softmax over the step's 16 * PPS tokens ----
+    const int page0 = p_begin + PPS * step;
+    float c[PPS], vs[PPS];
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+      c[pp] = scale_log2;
+      vs[pp] = 1.f;
+      if (FP8) {
+        c[pp] *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), PPS * step + pp));
+        vs[pp] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), PPS * step + pp));
+      }
+    }
+    float x[4 * PPS];
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[4 * pp + r] = s[pp][r] * c[pp];
+    // tokens past the context (or the wave's last page) are masked; their V
+    // slots are zeroed too, so stale cache bytes (NaN patterns included) in
+    // a partially filled page cannot reach the PV product
+    const bool partial = (page0 + PPS) * 16 > Lctx || page0 + PPS > p_end;
+    bool slot_ok[4 * PPS];
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        slot_ok[4 * pp + r] = ((page0 + pp) * 16 + 4 * grp + r < Lctx) && (page0 + pp < p_end);
+    if (partial) {
+#pragma unroll
+      for (int i = 0; i < 4 * PPS; ++i)
+        if (!slot_ok[i]) x[i] = kNegInf;
+    }
+    float tmax = max3(x[0], x[1], __builtin_fmaxf(x[2], x[3]));
+    if (PPS == 2) tmax = max3(tmax, __builtin_fmaxf(x[4 % (4 * PPS)], x[5 % (4 * PPS)]),
+                              __builtin_fmaxf(x[6 % (4 * PPS)], x[7 % (4 * PPS)]));
+    tmax = pair16_max(tmax);
+    tmax = pair32_max(tmax);
+    const bool need = tmax > m_run + 8.0f;
+    if (wave_any(need)) {
+      const float m_new = __builtin_fmaxf(m_run, tmax);
+      const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+#pragma unroll
+      for (int i = 0; i < NB; ++i) o[i] *= alpha;
+      l_run *= alpha;
+      m_run = m_new;
+    }
+    const float msub = (m_run == kNegInf) ? 0.f : m_run;
+    float p[4 * PPS];
+#pragma unroll
+    for (int i = 0; i < 4 * PPS; ++i) p[i] = fast_exp2(x[i] - msub);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4 * PPS; ++i) psum += p[i];
+    l_run += psum;
+    // P operand (v scale folded in): PPS = 2 -> 8 values = 4 tokens of each
+    // page (16x16x32); PPS = 1 -> the lane's 4 tokens (16x16x16)
+    u32x4 pw;
+#pragma unroll
+    for (int pp = 0; pp < PPS; ++pp) {
+      pw[2 * pp] = __builtin_bit_cast(uint32_t, Tr::pack2(p[4 * pp] * vs[pp], p[4 * pp + 1] * vs[pp]));
+      pw[2 * pp + 1] = __builtin_bit_cast(uint32_t, Tr::pack2(p[4 * pp + 2] * vs[pp], p[4 * pp + 3] * vs[pp]));
+    }
+
+    // ---- O += P V^T ----
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      u32x4 bw;
+#pragma unroll
+      for (int pp = 0; pp < PPS; ++pp) {
+        if (FP8) {
+          const uint32_t v = v8r[pp][nb % (FP8 ? NB : 1)];
+          bw[2 * pp] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(v));
+          bw[2 * pp + 1] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(v));
+        } else {
+          bw[2 * pp] = v16r[pp][nb % (FP8 ? 1 : NB)][0];
+          bw[2 * pp + 1] = v16r[pp][nb % (FP8 ? 1 : NB)][1];
+        }
+      }
+      if (partial) {
+        // zero masked token slots: 16-bit halves of the operand dwords
+#pragma unroll
+        for (int i = 0; i < 4 * PPS; ++i)
+          if (!slot_ok[i]) bw[i >> 1] &= (i & 1) ? 0x0000ffffu : 0xffff0000u;
+      }
+      if (PPS == 2) {
+        o[nb] = Tr::mfma16(__builtin_bit_cast(vec8, pw), __builtin_bit_cast(vec8, bw), o[nb]);
+      } else {
+        const u32x2 a2 = {pw[0], pw[1]}, b2 = {bw[0], bw[1]};
+        o[nb] = Tr::mfma16k16(__builtin_bit_cast(vec4, a2), __builtin_bit_cast(vec4, b2), o[nb]);
+      }
+    }
+    slot = (slot == RING - 1) ? 0 : slot + 1;
+  }
+  wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
+
+  l_run = pair16_sum(l_run);
+  l_run = pair32_sum(l_run);
+  const bool single = (n_splits == 1);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int g = 4 * grp + r;
+    const float lg = __shfl(l_run, g, 64);
+    const float mg = __shfl(m_run, g, 64);
+    if (g >= Gc) continue;
+    const float inv = (lg > 0.f) ? 1.f / lg : 0.f;
+    const int hq = hq0 + g;
+    if (single) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const vec2 pk = Tr::pack2(o[nb][r] * inv, 0.f);
+        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = __builtin_bit_cast(uint16_t, pk[0]);
+      }
+    } else {
+      const size_t sl = ((size_t)n * Hq + hq) * max_splits + split;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) ws_o[sl * D + 16 * nb + l16] = o[nb][r] * inv;
+      if (l16 == 0) ws_lse[sl] = (lg > 0.f) ? mg + __log2f(lg) : kNegInf;
     }
   }
 }
 
 // Combines the split partials of every (sequence, query head) with more than
-// one split: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M).
+// one split: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). One wave per
+// (sequence, head); each lane owns D/64 output elements.
 template <typename Tr, int D>
-__global__ __launch_bounds__(D) void decode_merge_kernel(
+__global__ __launch_bounds__(64) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
     const float* __restrict__ ws_lse, uint16_t* __restrict__ O, int Hq, int max_splits) {
   using vec2 = typename Tr::vec2;
+  constexpr int PER = D / 64;
   const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
+  const int lane = threadIdx.x;
   const int Lctx = context_lens ? min(max(0, context_lens[n]), max_tokens) : max_tokens;
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = (n_pages + kPagesPerSplit - 1) / kPagesPerSplit;
+  const int n_splits = (n_pages + kPagesPerWave - 1) / kPagesPerWave;
   if (n_splits <= 1) return;
   const size_t slot0 = ((size_t)n * Hq + hq) * max_splits;
-  const int d = threadIdx.x;
   float M = kNegInf;
-  for (int s = 0; s < n_splits; ++s) M = __builtin_fmaxf(M, ws_lse[slot0 + s]);
-  float wsum = 0.f, acc = 0.f;
+  for (int s = lane; s < n_splits; s += 64) M = __builtin_fmaxf(M, ws_lse[slot0 + s]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, 64));
+  float wsum = 0.f;
+  float acc[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) acc[i] = 0.f;
   if (M != kNegInf) {
-    for (int s = 0; s < n_splits; ++s) {
-      const float lse = ws_lse[slot0 + s];
-      const float f = (lse == kNegInf) ? 0.f : fast_exp2(lse - M);
-      wsum += f;
-      acc += f * ws_o[(slot0 + s) * D + d];
+    for (int s0 = 0; s0 < n_splits; s0 += 64) {
+      const int s = s0 + lane;
+      const float lse = (s < n_splits) ? ws_lse[slot0 + s] : kNegInf;
+      const float wl = (lse == kNegInf) ? 0.f : fast_exp2(lse - M);
+      const int cnt = min(64, n_splits - s0);
+#pragma unroll 4
+      for (int j = 0; j < cnt; ++j) {
+        const float wj = __shfl(wl, j, 64);
+        wsum += wj;
+        const float* src = ws_o + (slot0 + s0 + j) * D + lane * PER;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) acc[i] += wj * src[i];
+      }
     }
   }
-  const float val = wsum > 0.f ? acc / wsum : 0.f;
-  const vec2 pk = Tr::pack2(val, 0.f);
-  O[((size_t)n * Hq + hq) * D + d] = __builtin_bit_cast(uint16_t, pk[0]);
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const vec2 pk = Tr::pack2(acc[i] * inv, 0.f);
+    O[((size_t)n * Hq + hq) * D + lane * PER + i] = __builtin_bit_cast(uint16_t, pk[0]);
+  }
 }
 
 size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
   const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  const int max_splits = (pages + kPagesPerSplit - 1) / kPagesPerSplit;
+  const int max_splits = (pages + kPagesPerWave - 1) / kPagesPerWave;
   if (max_splits <= 1) return 0;
   return (size_t)N * Hq * max_splits * (size_t)(D + 1) * sizeof(float);
 }
@@ -494,22 +890,33 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
                                   float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
   const int max_tokens = (KIND == kKindContig16) ? S_contig : max_blocks * kDecodePage;
   const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  const int max_splits = max(1, (pages + kPagesPerSplit - 1) / kPagesPerSplit);
-  const int G = Hq / Hkv;
-  const int n_hc = (G + 15) / 16;
+  const int max_splits = max(1, (pages + kPagesPerWave - 1) / kPagesPerWave);
+  const int Gq = Hq / Hkv;
+  const int n_hc = (Gq + 15) / 16;
   const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
   if (ws_bytes < need) return hipErrorInvalidValue;
   float* ws_o = (float*)ws;
   float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
-  const long long grid = (long long)N * Hkv * n_hc * max_splits;
-  if (grid == 0) return hipSuccess;
-  hipLaunchKernelGGL((decode_split_kernel<Tr, D, KIND>), dim3((unsigned)grid),
-                     dim3(kDecodeWaves * 64), 0, stream, (const uint16_t*)q, kc, vc, k_scale,
-                     v_scale, per_block, bt, lens, (uint16_t*)out, ws_o, ws_lse, Hq, Hkv,
-                     max_blocks, num_blocks, S_contig, max_splits, n_hc, scale * kLog2e);
+  const long long total_waves = (long long)N * Hkv * n_hc * max_splits;
+  if (total_waves == 0) return hipSuccess;
+  if (KIND != kKindContig16 && kDecodeDma) {
+    if (total_waves > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((decode_dma_kernel<Tr, D, KIND>), dim3((unsigned)total_waves), dim3(64), 0,
+                       stream, (const uint16_t*)q, kc, vc, k_scale, v_scale, per_block, bt, lens,
+                       (uint16_t*)out, ws_o, ws_lse, Hq, Hkv, max_blocks, num_blocks, max_splits,
+                       n_hc, scale * kLog2e);
+  } else {
+    const long long grid = (total_waves + kDecodeWgWaves - 1) / kDecodeWgWaves;
+    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((decode_split_kernel<Tr, D, KIND>), dim3((unsigned)grid),
+                       dim3(kDecodeWgWaves * 64), 0, stream, (const uint16_t*)q, kc, vc, k_scale,
+                       v_scale, per_block, bt, lens, (uint16_t*)out, ws_o, ws_lse, Hq, Hkv,
+                       max_blocks, num_blocks, S_contig, max_splits, n_hc, total_waves,
+                       scale * kLog2e);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_splits <= 1) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(D), 0, stream,
+  hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
                      KIND == kKindContig16 ? nullptr : lens, max_tokens, ws_o, ws_lse,
                      (uint16_t*)out, Hq, max_splits);
   return hipGetLastError();

@@ -17,12 +17,22 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
                           hipStream_t stream);
 
-// Split-K geometry of the decode kernels: pages of 16 tokens, 4 waves per
-// workgroup, kPagesPerWave pages per wave.
+// Split-K geometry of the decode kernels: pages of 16 tokens; one wave walks
+// one split of kPagesPerWave pages.
 constexpr int kDecodePage = 16;
-constexpr int kDecodeWaves = 4;
-constexpr int kPagesPerWave = 16;
-constexpr int kPagesPerSplit = kDecodeWaves * kPagesPerWave;
+#ifndef CA_PAGES_PER_WAVE
+#define CA_PAGES_PER_WAVE 32
+#endif
+#ifndef CA_DECODE_WG_WAVES
+#define CA_DECODE_WG_WAVES 4
+#endif
+#ifndef CA_DECODE_DMA
+#define CA_DECODE_DMA 1
+#endif
+constexpr int kPagesPerWave = CA_PAGES_PER_WAVE;  // <= 64: one page id per lane
+constexpr bool kDecodeDma = CA_DECODE_DMA != 0;   // paged decode via HBM -> LDS loads
+constexpr int kDecodeWgWaves = CA_DECODE_WG_WAVES;  // independent waves per workgroup
+static_assert(kPagesPerWave % 2 == 0 && kPagesPerWave <= 64, "pages per wave");
 
 // Workspace for split-K partial results: [N][Hq][max_splits] x (D + 1) floats.
 size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens);
