@@ -145,26 +145,35 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
       }
     }
 
-    float x[32];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[mb * 16 + r] = s[mb][r] * scale_log2;
+    // Softmax in the log2 domain with the scale folded into one FMA per
+    // logit: p = 2^(s*c - m). The row max is taken over the raw logits (min
+    // for a negative scale) and scaled once; a masked logit is set to the
+    // value whose scaled image is -inf.
     const bool need_mask = CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S);
+    const bool pos = scale_log2 >= 0.f;
     if (need_mask) {
+      const float mv = pos ? kNegInf : -kNegInf;
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + 32 * mb + 16 * (r >> 3) + 8 * hl + (r & 7);
           const bool masked = (key >= S) || (CAUSAL && key > myq);
-          if (masked) x[mb * 16 + r] = kNegInf;
+          if (masked) s[mb][r] = mv;
         }
     }
-    float tmax = x[0];
+    float tm;
+    if (pos) {
+      tm = max3(s[0][0], s[0][1], s[0][2]);
 #pragma unroll
-    for (int i = 1; i < 32; ++i) tmax = __builtin_fmaxf(tmax, x[i]);
-    tmax = pair32_max(tmax);
+      for (int i = 3; i < 31; i += 2) tm = max3(tm, s[i >> 4][i & 15], s[(i + 1) >> 4][(i + 1) & 15]);
+      tm = __builtin_fmaxf(tm, s[1][15]);
+    } else {
+      tm = s[0][0];
+#pragma unroll
+      for (int i = 1; i < 32; ++i) tm = __builtin_fminf(tm, s[i >> 4][i & 15]);
+    }
+    float tmax = pair32_max(tm * scale_log2);
     const bool need = tmax > m_run + 8.0f;
     if (wave_any(need)) {
       const float m_new = __builtin_fmaxf(m_run, tmax);
@@ -184,8 +193,9 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
       const int base = (kk >> 1) * 16 + (kk & 1) * 8;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float p0 = fast_exp2(x[base + 2 * j] - msub);
-        const float p1 = fast_exp2(x[base + 2 * j + 1] - msub);
+        const int i0 = base + 2 * j, i1 = i0 + 1;
+        const float p0 = fast_exp2(__builtin_fmaf(s[i0 >> 4][i0 & 15], scale_log2, -msub));
+        const float p1 = fast_exp2(__builtin_fmaf(s[i1 >> 4][i1 & 15], scale_log2, -msub));
         psum += p0 + p1;
         const vec2 pk = Tr::pack2(p0, p1);
         pb[kk][2 * j] = pk[0];
@@ -229,7 +239,10 @@ template <typename Tr, int D, bool CAUSAL>
 static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o,
                                    int B, int Hq, int Hkv, int S, float scale,
                                    hipStream_t stream) {
-  constexpr int NW = 4;
+#ifndef CA_PF_NW
+#define CA_PF_NW 4
+#endif
+  constexpr int NW = CA_PF_NW;  // waves per workgroup (32 query rows each)
   constexpr int BM = 32 * NW;
   const int n_qt = (S + BM - 1) / BM;
   const long long grid = (long long)n_qt * B * Hq;
