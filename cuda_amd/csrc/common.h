@@ -26,6 +26,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define CA_LDS __attribute__((address_space(3)))
+// for lambdas inside kernels: they capture register arrays by reference
+#define CA_INLINE __attribute__((always_inline))
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegInf = -__builtin_inff();
@@ -63,6 +65,11 @@ struct BF16 {
   static __device__ __forceinline__ float to_float(uint16_t x) {
     return __uint_as_float(((uint32_t)x) << 16);
   }
+  // acc + v[0] + v[1] in one v_dot2 (the sum of the rounded 16-bit values)
+  static __device__ __forceinline__ float dot2sum(vec2 v, float acc) {
+    const vec2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
+  }
 };
 
 struct F16 {
@@ -91,6 +98,10 @@ struct F16 {
   static __device__ __forceinline__ float to_float(uint16_t x) {
     _Float16 h = __builtin_bit_cast(_Float16, x);
     return (float)h;
+  }
+  static __device__ __forceinline__ float dot2sum(vec2 v, float acc) {
+    const vec2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(v, one, acc, false);
   }
 };
 

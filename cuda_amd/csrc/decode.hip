@@ -32,6 +32,7 @@
 // combines the splits.
 #include "common.h"
 #include "launch.h"
+#include "lds_dma.h"
 
 namespace ca {
 
@@ -441,59 +442,11 @@ void decode_split_kernel(
 // parity so the tr16 reads of lane groups 0/1 and 2/3 hit disjoint banks),
 // V pages linear [D][16].
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t lds_off(const void* p) {
-  return (uint32_t)(uintptr_t)(const CA_LDS void*)p;
-}
-// The LDS reads and waits below are gfx950 instructions; the host pass of
-// the HIP compiler (which also parses device code) gets inert stand-ins.
-#if __HIP_DEVICE_COMPILE__
-#define CA_DEVICE_ASM(...) asm volatile(__VA_ARGS__)
-#else
-#define CA_DEVICE_ASM(...) (void)0
-#endif
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_read_tr8(uint32_t a) {
-  u32x2 r = {a, a};
-  CA_DEVICE_ASM("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t a) {
-  u32x2 r = {a, a};
-  CA_DEVICE_ASM("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-template <int OFF>
-__device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
-  uint32_t r = a;
-  CA_DEVICE_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_read_b64(uint32_t a) {
-  u32x2 r = {a, a};
-  CA_DEVICE_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
-  return r;
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  CA_DEVICE_ASM("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { CA_DEVICE_ASM("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-// 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (dst is
-// wave-uniform: it is passed in M0). Cache policy "nt": every byte is read
-// once per launch, so it is streamed rather than retained.
+// Cache policy of the page loads: "nt" (every byte is read once per launch,
+// so it is streamed rather than retained).
 #ifndef CA_DMA_POLICY
 #define CA_DMA_POLICY 2
 #endif
-__device__ __forceinline__ void dma16(const void* src, CA_LDS void* dst) {
-  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, CA_DMA_POLICY);
-}
-// Orders later uses of `x` after the preceding wait (the asm "rewrites" it).
-template <typename T>
-__device__ __forceinline__ void after_wait(T& x) {
-  CA_DEVICE_ASM("" : "+v"(x));
-}
 
 #ifndef CA_DMA_PPS
 #define CA_DMA_PPS 1
@@ -611,8 +564,8 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       const unsigned char* vp = (const unsigned char*)Vc + chunk;
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
-        dma16(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + pp * 2 * CHUNK + 1024 * i));
-        dma16(valid ? vp + 1024 * i + 16 * lane : dummy,
+        dma16<CA_DMA_POLICY>(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + pp * 2 * CHUNK + 1024 * i));
+        dma16<CA_DMA_POLICY>(valid ? vp + 1024 * i + 16 * lane : dummy,
               (CA_LDS void*)(base + pp * 2 * CHUNK + CHUNK + 1024 * i));
       }
     }

@@ -1,0 +1,86 @@
+// HBM -> LDS direct loads and hand-issued LDS reads for gfx950.
+//
+// global_load_lds_dwordx4 moves 16 bytes per lane from global memory straight
+// into LDS (lane l's bytes land at the wave-uniform destination + 16 * l), so
+// bytes in flight cost no VGPRs and no ds_write. The compiler's own
+// wait-for-everything before LDS reads that might alias such a load would
+// serialise a multi-stage ring, so the kernels read LDS with hand-issued
+// ds_read instructions (inline asm the compiler does not treat as LDS
+// accesses) and wait on the counters explicitly:
+//   s_waitcnt vmcnt(N)    - all but the N most recent vector-memory loads done
+//   s_waitcnt lgkmcnt(N)  - all but the N most recent LDS reads done
+// and `after_wait(x)` re-defines a read's result after its wait so that no
+// use of it can be scheduled above the wait.
+#pragma once
+
+#include "common.h"
+
+namespace ca {
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(uintptr_t)(const CA_LDS void*)p;
+}
+
+// The LDS reads and waits are gfx950 instructions; the host pass of the HIP
+// compiler (which also parses device code) gets inert stand-ins.
+#if __HIP_DEVICE_COMPILE__
+#define CA_DEVICE_ASM(...) asm volatile(__VA_ARGS__)
+#else
+#define CA_DEVICE_ASM(...) (void)0
+#endif
+
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr8(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64_tr_b8 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_tr16(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
+  uint32_t r = a;
+  CA_DEVICE_ASM("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_read_b64(uint32_t a) {
+  u32x2 r = {a, a};
+  CA_DEVICE_ASM("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
+  u32x4 r = {a, a, a, a};
+  CA_DEVICE_ASM("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  CA_DEVICE_ASM("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_lgkm() {
+  CA_DEVICE_ASM("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { wait_lgkm<0>(); }
+
+// 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (dst is
+// wave-uniform: it is passed in M0). AUX is the cache policy: 0 = default
+// (data re-read by other workgroups stays in L2), 2 = nt (streamed once).
+template <int AUX>
+__device__ __forceinline__ void dma16(const void* src, CA_LDS void* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, AUX);
+}
+
+// Orders later uses of `x` after the preceding wait (the asm "rewrites" it).
+template <typename T>
+__device__ __forceinline__ void after_wait(T& x) {
+  CA_DEVICE_ASM("" : "+v"(x));
+}
+
+}  // namespace ca

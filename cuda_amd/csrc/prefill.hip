@@ -26,8 +26,11 @@
 // r%4 in register r) this makes register r of lane half h hold key
 // 16*(r/8) + 8*h + r%8, i.e. eight consecutive keys per PV k-step, exactly the
 // B-operand layout of the PV MFMA — no LDS round trip for P.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
+#include "lds_dma.h"
 
 namespace ca {
 
@@ -235,6 +238,508 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Head dim 128 kernel.
+//
+// One workgroup = 256 query rows of one (b, h), split over its waves: NH = 2
+// gives 4 waves of 64 rows (one wave per SIMD), NH = 1 gives 8 waves of 32
+// rows (two per SIMD). A wave owns NH 32-query halves; a K fragment read
+// from LDS feeds the S^T MFMAs of all of them and a V^T fragment their O^T
+// MFMAs, so LDS read bytes per FLOP fall as 1/NH. The O^T accumulators
+// (4 x NH blocks of 16 per lane), the S^T accumulators and Q live in AGPRs.
+//
+// K/V tiles of 64 keys travel HBM -> LDS with global_load_lds into a ring of
+// kStages tiles (each wave loads 1/NW of every K and V tile; one barrier per
+// tile). Tile layout: 64 rows x 256 bytes, unpadded; the 16-byte chunk c of
+// row r is stored at position c ^ swz(r), swz(r) = 4*(r%4) + (r/4)%4, which
+// makes both read patterns bank-conflict free:
+//   K, ds_read_b128: a 16-lane group reads one chunk of 16 consecutive rows
+//     -> 16 distinct positions;
+//   V, ds_read_b64_tr_b16: a 32-lane group reads chunks 4ob..4ob+3 of 4
+//     consecutive rows 4u..4u+3 -> position quad ob ^ (r%4) differs per row.
+// ---------------------------------------------------------------------------
+namespace pf128 {
+constexpr int kD = 128;
+constexpr int kBN = 64;                        // keys per tile
+constexpr int kRowB = kD * 2;                  // bytes per K/V row
+constexpr int kTileB = kBN * kRowB;            // bytes per K (or V) tile
+constexpr int kStageB = 2 * kTileB;            // K tile then V tile
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+}  // namespace pf128
+
+// acc *= alpha on an accumulator kept in AGPRs, element by element through one
+// VGPR, so the accumulator never needs a VGPR copy (a plain C++ multiply
+// makes the compiler keep a VGPR image of every accumulator of the loop).
+// The compiler does not see these AGPR accesses as dependent on the MFMAs
+// that write the accumulators, so the caller brackets them with acc_gap().
+__device__ __forceinline__ void scale_acc(f32x16& acc, float alpha) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float x = acc[r];
+    float tmp;
+    CA_DEVICE_ASM(
+        "v_accvgpr_read_b32 %1, %0\n\t"
+        "v_mul_f32 %1, %1, %2\n\t"
+        "v_accvgpr_write_b32 %0, %1"
+        : "+a"(x), "=&v"(tmp)
+        : "v"(alpha));
+    acc[r] = x;
+  }
+}
+// 24 wait states: longer than any MFMA-result -> VALU and VALU -> MFMA-operand
+// hazard of gfx950, so MFMAs issued before it have written their results.
+__device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
+
+// max(a, b, c) in one v_max3_f32. The plain fmaxf route makes the compiler
+// quiet possibly-signalling NaN inputs with an extra v_max per operand
+// (IEEE mode); logits are never signalling NaNs.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+#if __HIP_DEVICE_COMPILE__
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+#else
+  r = a;
+#endif
+  return r;
+}
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+  float r;
+#if __HIP_DEVICE_COMPILE__
+  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+#else
+  r = a;
+#endif
+  return r;
+}
+
+// Per tile two phases, each pairing MFMAs with VALU work they do not depend
+// on (order fixed with scheduling barriers):
+//   PIPE (software pipeline across tiles):
+//     A(t): S^T(t+1) = K(t+1) Q^T   with  P(t) = exp2(...) of the tile-t
+//           logits held in VGPRs;
+//     B(t): O^T += V(t)^T P(t)^T    with  copying S^T(t+1) out of the
+//           accumulators, masking it and taking its row max;
+//     after B(t) the running max and the (rare) O rescale for tile t+1 are
+//     settled, so A(t+1) can exponentiate;
+//   !PIPE: QK(t), max, exp, PV(t) in sequence; the overlap of MFMA and VALU
+//     comes from the other wave on the SIMD (NH = 1).
+// Waves per workgroup for BM query rows at 32*NH rows per wave, and the
+// workgroups per CU that keep 2/NH waves on each SIMD.
+constexpr int pf_waves(int bm, int nh) { return bm / (32 * nh); }
+constexpr int pf_wg_per_cu(int bm, int nh) {
+  return (8 / nh) / pf_waves(bm, nh) > 0 ? (8 / nh) / pf_waves(bm, nh) : 1;
+}
+#ifndef CA_PF_AG
+#define CA_PF_AG 0
+#endif
+template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
+__global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    int Hkv, float scale_log2, int n_qt) {
+  using namespace pf128;
+  using vec8 = typename Tr::vec8;
+  using vec4 = typename Tr::vec4;
+  using vec2 = typename Tr::vec2;
+  constexpr int D = kD;
+  constexpr int kBM = BM;                        // query rows per workgroup
+  constexpr int kStages = STAGES;                // K/V tiles in the LDS ring
+  constexpr int kRW = 32 * NH;                   // query rows per wave
+  constexpr int kNW = kBM / kRW;                 // waves per workgroup
+  constexpr int kDmaPerWave = kTileB / 1024 / kNW;  // 1 KB loads per wave per tile (K, and V)
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
+
+  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = work / n_qt;
+  const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
+  const int b = bh / Hq, h = bh % Hq;
+  const int hk = h / (Hq / Hkv);
+  const int q0 = qt * kBM;
+  const uint16_t* Qp = Q + (size_t)(b * Hq + h) * S * D;
+  uint16_t* Op = O + (size_t)(b * Hq + h) * S * D;
+  const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
+  const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int qw0 = q0 + wave * kRW;
+  int myq[NH];
+#pragma unroll
+  for (int nb = 0; nb < NH; ++nb) myq[nb] = qw0 + 32 * nb + l32;
+
+  // Q as the B operand of S^T = K Q^T, one set per 32-query half.
+  vec8 qv[NH][8];
+#pragma unroll
+  for (int nb = 0; nb < NH; ++nb) {
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      if (myq[nb] < S) {
+        qv[nb][ks] = *(const vec8*)(Qp + (size_t)myq[nb] * D + 16 * ks + 8 * hl);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[nb][ks][e] = 0;
+      }
+#if CA_PF_AG
+      CA_DEVICE_ASM("" : "+a"(qv[nb][ks]));  // Q lives in AGPRs (an MFMA operand may)
+#endif
+    }
+  }
+
+  const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
+  const int n_tiles = (kv_end + kBN - 1) / kBN;
+  // tiles this wave computes on (it still loads and synchronises for all)
+  const int w_end = CAUSAL ? min(kv_end, qw0 + kRW) : kv_end;
+  const int w_tiles = (qw0 < S) ? (w_end + kBN - 1) / kBN : 0;
+
+  // HBM -> LDS: load i of this wave covers tile rows 4*(kDmaPerWave*wave + i)
+  // + lane/16; the lane fetches the chunk that belongs at position lane % 16.
+  int dma_row[kDmaPerWave], dma_col[kDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    dma_row[i] = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
+    dma_col[i] = 8 * ((lane & 15) ^ swz(dma_row[i]));
+  }
+  auto issue = [&](int tt) CA_INLINE {
+    // past the last tile: reload it, so every iteration waits on the same count
+    const int k0 = min(tt, n_tiles - 1) * kBN;
+    unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
+#pragma unroll
+    for (int i = 0; i < kDmaPerWave; ++i) {
+      const size_t off = (size_t)min(k0 + dma_row[i], S - 1) * D + dma_col[i];
+      dma16<0>(Kp + off, (CA_LDS void*)(kdst + 1024 * i));
+      dma16<0>(Vp + off, (CA_LDS void*)(kdst + kTileB + 1024 * i));
+    }
+  };
+
+  // LDS read addresses (bytes from the stage base).
+  // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl.
+  const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+  const int fk = swz(krow);
+  const uint32_t kofs = krow * kRowB + 32 * (fk >> 1) + 16 * (hl ^ (fk & 1));  // ^ 32*ks
+  // V^T: tr16 source lane -> row tr_row (+4 for the second read), logical
+  // chunk 4*ob + c0, byte 8*(s16 & 1) of it.
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
+  const int c0 = 2 * (g16 & 1) + ((s16 & 3) >> 1);
+  const int fv = swz(tr_row);  // swz(tr_row + 4) == fv + 1
+  const uint32_t vofs1 = kTileB + tr_row * kRowB + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
+  const uint32_t vofs2 =
+      kTileB + (tr_row + 4) * kRowB + 64 * (fv >> 2) + 16 * (c0 ^ ((fv + 1) & 3)) + 8 * (s16 & 1);
+  const uint32_t lds0 = lds_off(lds);
+  auto stage = [&](int tt) CA_INLINE { return lds0 + (uint32_t)((tt % kStages) * kStageB); };
+
+  f32x16 o[4][NH];     // O^T accumulators (AGPRs)
+  f32x16 sacc[2][NH];  // S^T accumulators [mb][nb] of the tile being multiplied (AGPRs)
+  float sv[NH][32];    // VGPR copy of the S^T being normalised: sv[nb][16mb + r]
+  vec8 pb[NH][4];      // P^T, B operand of the O^T MFMAs
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][nb][r] = 0.f;
+  float m_run[NH], l_run[NH], msub[NH];
+#pragma unroll
+  for (int nb = 0; nb < NH; ++nb) { m_run[nb] = kNegInf; l_run[nb] = 0.f; msub[nb] = 0.f; }
+  constexpr float kMaskVal = POS ? kNegInf : -kNegInf;  // raw logit whose scaled image is -inf
+
+  // P for logit pair p (16 pairs per half: nb = p/16, P^T k-step kk = (p%16)/4,
+  // logits 8kk + 2j, +1 with j = p%4; sv[nb][8kk + e] <-> P^T k-step kk)
+  float psum[NH][2];
+  auto exp_pair = [&](int p) CA_INLINE {
+    const int nb = p >> 4, kk = (p >> 2) & 3, j = p & 3;
+    const int i0 = 8 * kk + 2 * j;
+    const float p0 = fast_exp2(__builtin_fmaf(sv[nb][i0], scale_log2, -msub[nb]));
+    const float p1 = fast_exp2(__builtin_fmaf(sv[nb][i0 + 1], scale_log2, -msub[nb]));
+    const vec2 pk = Tr::pack2(p0, p1);
+    pb[nb][kk][2 * j] = pk[0];
+    pb[nb][kk][2 * j + 1] = pk[1];
+    psum[nb][j & 1] = Tr::dot2sum(pk, psum[nb][j & 1]);
+  };
+  // copy logit pair p (nb = p/16, logits i0 = 2*(p%16), +1) out of the
+  // accumulators into sv (masked if MASK; a masked logit becomes the value
+  // whose exponential is 0) and fold it into the row max
+  float tm[NH];
+  auto take_pair = [&](int p, int k0, auto mask_tag) CA_INLINE {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int nb = p >> 4, i0 = 2 * (p & 15);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int i = i0 + e;
+      float x = sacc[i >> 4][nb][i & 15];
+      if (MASK) {
+        const int key = k0 + 32 * (i >> 4) + 16 * ((i >> 3) & 1) + 8 * hl + (i & 7);
+        if (key >= S || (CAUSAL && key > myq[nb])) x = kMaskVal;
+      }
+      if (PIPE) CA_DEVICE_ASM("" : "+v"(x));  // a real VGPR copy: the accumulators are reused
+      sv[nb][i] = x;
+    }
+    tm[nb] = POS ? vmax3(tm[nb], sv[nb][i0], sv[nb][i0 + 1])
+                 : vmin3(tm[nb], sv[nb][i0], sv[nb][i0 + 1]);
+  };
+  // running max, lazy O rescale, exponent offset for the tile now in sv
+  auto settle_max = [&]() CA_INLINE {
+    float tmax[NH];
+    bool any_need = false;
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) {
+      tmax[nb] = pair32_max(tm[nb] * scale_log2);
+      any_need |= tmax[nb] > m_run[nb] + 8.0f;
+    }
+    if (__builtin_expect(wave_any(any_need), 0)) {  // rare: the max rose by > 2^8
+      acc_gap();
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) {
+        const float m_new = __builtin_fmaxf(m_run[nb], tmax[nb]);
+        const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run[nb] - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#if CA_PF_AG
+          scale_acc(o[i][nb], alpha);
+#else
+          o[i][nb] *= alpha;
+#endif
+        }
+        l_run[nb] *= alpha;
+        m_run[nb] = m_new;
+      }
+      acc_gap();
+    }
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) msub[nb] = (m_run[nb] == kNegInf) ? 0.f : m_run[nb];
+  };
+
+  // Phase A: S^T(tn) = K(tn) Q^T (if QK), with the exponentials of the tile
+  // in sv (if EXP) after the MFMAs, one pair each.
+  auto phase_a = [&](int tn, auto qk_tag, auto exp_tag) CA_INLINE {
+    constexpr bool QK = decltype(qk_tag)::value;
+    constexpr bool EXP = decltype(exp_tag)::value;
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) psum[nb][0] = psum[nb][1] = 0.f;
+    if (QK) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NH; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[mb][nb][r] = 0.f;
+      const uint32_t ka = stage(tn) + kofs;
+      u32x4 kr[2][2];
+      kr[0][0] = lds_read_b128<0>(ka);
+      kr[0][1] = lds_read_b128<32 * kRowB>(ka);
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const int cb = ks & 1;
+        if (ks + 1 < 8) {
+          const uint32_t an = ka ^ (32 * (ks + 1));
+          kr[cb ^ 1][0] = lds_read_b128<0>(an);
+          kr[cb ^ 1][1] = lds_read_b128<32 * kRowB>(an);
+          wait_lgkm<2>();
+        } else {
+          wait_lgkm<0>();
+        }
+        after_wait(kr[cb][0]);
+        after_wait(kr[cb][1]);
+#pragma unroll
+        for (int j = 0; j < 2 * NH; ++j) {
+          const int mb = j / NH, nb = j % NH;
+          const vec8 a = __builtin_bit_cast(vec8, kr[cb][mb]);
+          sacc[mb][nb] = Tr::mfma32(a, qv[nb][ks], sacc[mb][nb]);
+          if (EXP) exp_pair(2 * NH * ks + j);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then the pair's VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if (EXP) {
+#pragma unroll
+      for (int p = 0; p < 16 * NH; ++p) exp_pair(p);
+    }
+    if (EXP) {
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) l_run[nb] += psum[nb][0] + psum[nb][1];
+    }
+  };
+
+  // Phase B: O^T += V(t)^T P^T (if PV), with S^T(tn) taken out of the
+  // accumulators (if NEXT; masked if MASK) after the MFMAs; then settle.
+  auto phase_b = [&](int t, int tn, auto pv_tag, auto next_tag, auto mask_tag) CA_INLINE {
+    constexpr bool PV = decltype(pv_tag)::value;
+    constexpr bool NEXT = decltype(next_tag)::value;
+    const int k0n = tn * kBN;
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) tm[nb] = kMaskVal;
+    if (PV) {
+      const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
+      u32x2 vr[3][2];
+      auto vread = [&](int st, int buf) CA_INLINE {
+        const uint32_t x = 64 * (st >> 2);
+        switch (st & 3) {
+          case 0: vr[buf][0] = lds_read_tr16<0>(va1 ^ x); vr[buf][1] = lds_read_tr16<0>(va2 ^ x); break;
+          case 1: vr[buf][0] = lds_read_tr16<4096>(va1 ^ x); vr[buf][1] = lds_read_tr16<4096>(va2 ^ x); break;
+          case 2: vr[buf][0] = lds_read_tr16<8192>(va1 ^ x); vr[buf][1] = lds_read_tr16<8192>(va2 ^ x); break;
+          default: vr[buf][0] = lds_read_tr16<12288>(va1 ^ x); vr[buf][1] = lds_read_tr16<12288>(va2 ^ x); break;
+        }
+      };
+      vread(0, 0);
+      vread(1, 1);
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int cb = st % 3;
+        if (st + 2 < 16) {
+          vread(st + 2, (st + 2) % 3);
+          wait_lgkm<4>();
+        } else if (st + 1 < 16) {
+          wait_lgkm<2>();
+        } else {
+          wait_lgkm<0>();
+        }
+        after_wait(vr[cb][0]);
+        after_wait(vr[cb][1]);
+        const int ob = st >> 2, kk = st & 3;
+        u32x4 w4 = {vr[cb][0][0], vr[cb][0][1], vr[cb][1][0], vr[cb][1][1]};
+        const vec8 a = __builtin_bit_cast(vec8, w4);
+#pragma unroll
+        for (int nb = 0; nb < NH; ++nb) {
+          o[ob][nb] = Tr::mfma32(a, pb[nb][kk], o[ob][nb]);
+          if (NEXT) take_pair(NH * st + nb, k0n, mask_tag);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if (NEXT) {
+#pragma unroll
+      for (int p = 0; p < 16 * NH; ++p) take_pair(p, k0n, mask_tag);
+    }
+    if (NEXT) settle_max();
+  };
+
+  // ---- the tile walk ----------------------------------------------------------
+  // Every wave walks all n_tiles tiles (it loads its share of each and meets
+  // the others at the per-tile barrier). Only a wave's last tile can need a
+  // mask (bounds or causal diagonal); it is masked when taken out of the
+  // accumulators.
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+#pragma unroll
+  for (int tt = 0; tt < kStages - 1; ++tt) issue(tt);
+  // Iteration t waits until tile t + LEAD is resident (PIPE: A(t) reads
+  // K(t+1)); the slot of tile t-1 is then free for tile t + kStages - 1.
+  constexpr int LEAD = PIPE ? 1 : 0;
+  auto sync = [&](int t) CA_INLINE {
+    wait_vmcnt<2 * kDmaPerWave * (kStages - 2 - LEAD)>();  // this wave's loads landed
+    __builtin_amdgcn_s_barrier();                          // ... and every wave's
+    issue(t + kStages - 1);
+  };
+  int t = 0;
+  if (PIPE) {
+    wait_vmcnt<2 * kDmaPerWave * (kStages - 2)>();  // tile 0 landed (this wave's part)
+    __builtin_amdgcn_s_barrier();                   // ... and every wave's
+    if (w_tiles > 0) {
+      phase_a(0, T_{}, F_{});             // S^T(0)
+      phase_b(-1, 0, F_{}, T_{}, T_{});   // its max (mask test exact for any tile)
+    }
+    for (; t + 2 < w_tiles; ++t) {  // next tile is not the wave's last
+      sync(t);
+      phase_a(t + 1, T_{}, T_{});
+      phase_b(t, t + 1, T_{}, T_{}, F_{});
+    }
+    if (t + 2 == w_tiles) {  // next tile is the wave's last: mask it
+      sync(t);
+      phase_a(t + 1, T_{}, T_{});
+      phase_b(t, t + 1, T_{}, T_{}, T_{});
+      ++t;
+    }
+    if (t + 1 == w_tiles) {  // the wave's last tile
+      sync(t);
+      phase_a(-1, F_{}, T_{});
+      phase_b(t, -1, T_{}, F_{}, F_{});
+      ++t;
+    }
+  } else {
+    for (; t + 1 < w_tiles; ++t) {
+      sync(t);
+      phase_a(t, T_{}, F_{});
+      phase_b(-1, t, F_{}, T_{}, F_{});
+      phase_a(-1, F_{}, T_{});
+      phase_b(t, -1, T_{}, F_{}, F_{});
+    }
+    if (t + 1 == w_tiles) {  // the wave's last tile, masked
+      sync(t);
+      phase_a(t, T_{}, F_{});
+      phase_b(-1, t, F_{}, T_{}, T_{});
+      phase_a(-1, F_{}, T_{});
+      phase_b(t, -1, T_{}, F_{}, F_{});
+      ++t;
+    }
+  }
+  for (; t < n_tiles; ++t) sync(t);
+  wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
+  acc_gap();
+
+#pragma unroll
+  for (int nb = 0; nb < NH; ++nb) {
+    const float l_tot = pair32_sum(l_run[nb]);
+    const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+    if (myq[nb] < S) {
+#pragma unroll
+      for (int ob = 0; ob < 4; ++ob) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int d = 32 * ob + 8 * a + 4 * hl;
+          const vec2 lo = Tr::pack2(o[ob][nb][4 * a] * inv, o[ob][nb][4 * a + 1] * inv);
+          const vec2 hi = Tr::pack2(o[ob][nb][4 * a + 2] * inv, o[ob][nb][4 * a + 3] * inv);
+          vec4 w;
+          w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
+          *(vec4*)(Op + (size_t)myq[nb] * D + d) = w;
+        }
+      }
+    }
+  }
+}
+
+#ifndef CA_PF_NH
+#define CA_PF_NH 1
+#endif
+#ifndef CA_PF_PIPE
+#define CA_PF_PIPE 0
+#endif
+#ifndef CA_PF_BM
+#define CA_PF_BM 256
+#endif
+template <typename Tr, bool CAUSAL>
+static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o,
+                                      int B, int Hq, int Hkv, int S, float scale,
+                                      hipStream_t stream) {
+  constexpr int NH = CA_PF_NH;
+  constexpr bool PIPE = CA_PF_PIPE;
+  constexpr int BM = CA_PF_BM;
+  // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
+  constexpr int kLdsPerWg = 160 * 1024 / pf_wg_per_cu(BM, NH);
+  constexpr int STAGES = kLdsPerWg / pf128::kStageB > 4 ? 4 : kLdsPerWg / pf128::kStageB;
+  static_assert(STAGES >= (PIPE ? 3 : 2), "LDS ring too short for the schedule");
+  const int n_qt = (S + BM - 1) / BM;
+  const long long grid = (long long)n_qt * B * Hq;
+  if (grid == 0) return hipSuccess;
+  const float sl2 = scale * kLog2e;
+  const dim3 block(64 * pf_waves(BM, NH));
+  if (sl2 >= 0.f) {
+    hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
+                       dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
+                       n_qt);
+  } else {
+    hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
+                       dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
+                       n_qt);
+  }
+  return hipGetLastError();
+}
+
 template <typename Tr, int D, bool CAUSAL>
 static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o,
                                    int B, int Hq, int Hkv, int S, float scale,
@@ -261,13 +766,23 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
     return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream) \
                   : launch_prefill_t<TR, DD, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream); \
   }
+#ifndef CA_PF_OLD128
+#define CA_PREFILL_128(TR)                                                                     \
+  if (D == 128) {                                                                              \
+    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)    \
+                  : launch_prefill_d128<TR, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);  \
+  }
+#else
+#define CA_PREFILL_128(TR) CA_PREFILL_CASE(TR, 128)
+#endif
   if (dtype == kDtypeBF16) {
     CA_PREFILL_CASE(BF16, 64)
-    CA_PREFILL_CASE(BF16, 128)
+    CA_PREFILL_128(BF16)
   } else if (dtype == kDtypeF16) {
     CA_PREFILL_CASE(F16, 64)
-    CA_PREFILL_CASE(F16, 128)
+    CA_PREFILL_128(F16)
   }
+#undef CA_PREFILL_128
 #undef CA_PREFILL_CASE
   return hipErrorInvalidValue;
 }
