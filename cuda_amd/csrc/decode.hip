@@ -442,6 +442,9 @@ void decode_split_kernel(
 // parity so the tr16 reads of lane groups 0/1 and 2/3 hit disjoint banks),
 // V pages linear [D][16].
 // ---------------------------------------------------------------------------
+#ifndef CA_DEC_SPLIT_OUTER
+#define CA_DEC_SPLIT_OUTER 1
+#endif
 // Cache policy of the page loads: "nt" (every byte is read once per launch,
 // so it is streamed rather than retained).
 #ifndef CA_DMA_POLICY
@@ -494,8 +497,16 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 
   const int lane = threadIdx.x;
   int w = blockIdx.x;
+#if CA_DEC_SPLIT_OUTER
+  // split index outermost: every sequence's first splits come first and the
+  // waves of splits past a sequence's end gather at the tail of the grid
+  const int per_split = (int)(gridDim.x / max_splits);
+  const int split = w / per_split;
+  w %= per_split;
+#else
   const int split = w % max_splits;
   w /= max_splits;
+#endif
   const int hc = w % n_hc;
   w /= n_hc;
   const int hk = w % Hkv;

@@ -21,7 +21,7 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
 // one split of kPagesPerWave pages.
 constexpr int kDecodePage = 16;
 #ifndef CA_PAGES_PER_WAVE
-#define CA_PAGES_PER_WAVE 32
+#define CA_PAGES_PER_WAVE 64
 #endif
 #ifndef CA_DECODE_WG_WAVES
 #define CA_DECODE_WG_WAVES 4

@@ -49,12 +49,12 @@ def test_binding_table_matches_header():
 
 def test_version_and_workspace_sizes(lib):
     assert b"gfx950" in lib.ca_version()
-    # a split is 32 pages of 16 tokens; one split needs no workspace, otherwise
+    # a split is 64 pages of 16 tokens; one split needs no workspace, otherwise
     # N * Hq * splits * (D + 1) floats
-    assert lib.ca_decode_workspace_bytes(4, 8, 128, 512) == 0
-    assert lib.ca_decode_workspace_bytes(4, 8, 128, 513) == 4 * 8 * 2 * 129 * 4
-    assert lib.ca_decode_workspace_bytes(64, 32, 128, 8192) == 64 * 32 * 16 * 129 * 4
-    assert lib.ca_decode_workspace_bytes(256, 32, 128, 32768) == 256 * 32 * 64 * 129 * 4
+    assert lib.ca_decode_workspace_bytes(4, 8, 128, 1024) == 0
+    assert lib.ca_decode_workspace_bytes(4, 8, 128, 1025) == 4 * 8 * 2 * 129 * 4
+    assert lib.ca_decode_workspace_bytes(64, 32, 128, 8192) == 64 * 32 * 8 * 129 * 4
+    assert lib.ca_decode_workspace_bytes(256, 32, 128, 32768) == 256 * 32 * 32 * 129 * 4
     assert lib.ca_decode_workspace_bytes(0, 32, 128, 32768) == 0
 
 
