@@ -393,23 +393,27 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   const int w_end = CAUSAL ? min(kv_end, qw0 + kRW) : kv_end;
   const int w_tiles = (qw0 < S) ? (w_end + kBN - 1) / kBN : 0;
 
-  // HBM -> LDS: load i of this wave covers tile rows 4*(kDmaPerWave*wave + i)
-  // + lane/16; the lane fetches the chunk that belongs at position lane % 16.
-  int dma_row[kDmaPerWave], dma_col[kDmaPerWave];
+  // HBM -> LDS with buffer loads over the keys this workgroup needs
+  // ([0, kv_end) of the (b, kv head) slice; rows past it read as zero, so
+  // partial and trailing tiles need no clamp). Load i of this wave covers
+  // tile rows 4*(kDmaPerWave*wave + i) + lane/16; the lane fetches the chunk
+  // that belongs at position lane % 16. Only the scalar tile offset changes
+  // from tile to tile.
+  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(Kp, (uint32_t)kv_end * kRowB);
+  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(Vp, (uint32_t)kv_end * kRowB);
+  uint32_t dma_off[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
-    dma_row[i] = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
-    dma_col[i] = 8 * ((lane & 15) ^ swz(dma_row[i]));
+    const int row = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
+    dma_off[i] = row * kRowB + 16 * ((lane & 15) ^ swz(row));
   }
   auto issue = [&](int tt) CA_INLINE {
-    // past the last tile: reload it, so every iteration waits on the same count
-    const int k0 = min(tt, n_tiles - 1) * kBN;
     unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
+    const uint32_t toff = (uint32_t)tt * kTileB;
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      const size_t off = (size_t)min(k0 + dma_row[i], S - 1) * D + dma_col[i];
-      dma16<0>(Kp + off, (CA_LDS void*)(kdst + 1024 * i));
-      dma16<0>(Vp + off, (CA_LDS void*)(kdst + kTileB + 1024 * i));
+      dma16_buf(k_rsrc, (CA_LDS void*)(kdst + 1024 * i), dma_off[i], toff);
+      dma16_buf(v_rsrc, (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i], toff);
     }
   };
 
@@ -456,7 +460,9 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     const vec2 pk = Tr::pack2(p0, p1);
     pb[nb][kk][2 * j] = pk[0];
     pb[nb][kk][2 * j + 1] = pk[1];
-    psum[nb][j & 1] = Tr::dot2sum(pk, psum[nb][j & 1]);
+    // fp32 adds: v_dot2 would share the matrix pipe with the other wave's MFMAs
+    psum[nb][0] += p0;
+    psum[nb][1] += p1;
   };
   // copy logit pair p (nb = p/16, logits i0 = 2*(p%16), +1) out of the
   // accumulators into sv (masked if MASK; a masked logit becomes the value
