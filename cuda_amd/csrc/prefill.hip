@@ -38,7 +38,7 @@ template <typename Tr, int D, int NW, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt) {
+    int Hkv, float scale_log2, int n_qt, int n_work) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * VS];
 
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int work = xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work);
   const int bh = work / n_qt;
   const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
   const int b = bh / Hq, h = bh % Hq;
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
   const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
 
-  const int tid = threadIdx.x;
+  const int tid = __builtin_amdgcn_workitem_id_x();
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hl = lane >> 5;
   const int qw0 = q0 + wave * 32;
@@ -290,28 +290,6 @@ __device__ __forceinline__ void scale_acc(f32x16& acc, float alpha) {
 // hazard of gfx950, so MFMAs issued before it have written their results.
 __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
 
-// max(a, b, c) in one v_max3_f32. The plain fmaxf route makes the compiler
-// quiet possibly-signalling NaN inputs with an extra v_max per operand
-// (IEEE mode); logits are never signalling NaNs.
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-#if __HIP_DEVICE_COMPILE__
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-#else
-  r = a;
-#endif
-  return r;
-}
-__device__ __forceinline__ float vmin3(float a, float b, float c) {
-  float r;
-#if __HIP_DEVICE_COMPILE__
-  asm("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-#else
-  r = a;
-#endif
-  return r;
-}
-
 // Per tile two phases, each pairing MFMAs with VALU work they do not depend
 // on (order fixed with scheduling barriers):
 //   PIPE (software pipeline across tiles):
@@ -336,7 +314,7 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt) {
+    int Hkv, float scale_log2, int n_qt, int n_work) {
   using namespace pf128;
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
@@ -350,7 +328,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
 
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
+  const int work = xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work);
   const int bh = work / n_qt;
   const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
   const int b = bh / Hq, h = bh % Hq;
@@ -361,8 +339,8 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
   const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = __builtin_amdgcn_workitem_id_x() & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_workitem_id_x() >> 6);
   const int l32 = lane & 31, hl = lane >> 5;
   const int qw0 = q0 + wave * kRW;
   int myq[NH];
@@ -460,14 +438,12 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     const vec2 pk = Tr::pack2(p0, p1);
     pb[nb][kk][2 * j] = pk[0];
     pb[nb][kk][2 * j + 1] = pk[1];
-    // fp32 adds: v_dot2 would share the matrix pipe with the other wave's MFMAs
-    psum[nb][0] += p0;
-    psum[nb][1] += p1;
+    psum[nb][j & 1] = Tr::dot2sum(pk, psum[nb][j & 1]);
   };
   // copy logit pair p (nb = p/16, logits i0 = 2*(p%16), +1) out of the
   // accumulators into sv (masked if MASK; a masked logit becomes the value
   // whose exponential is 0) and fold it into the row max
-  float tm[NH];
+  float tm[NH][2];  // two partial row maxima (independent dependency chains)
   auto take_pair = [&](int p, int k0, auto mask_tag) CA_INLINE {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int nb = p >> 4, i0 = 2 * (p & 15);
@@ -482,8 +458,9 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
       if (PIPE) CA_DEVICE_ASM("" : "+v"(x));  // a real VGPR copy: the accumulators are reused
       sv[nb][i] = x;
     }
-    tm[nb] = POS ? vmax3(tm[nb], sv[nb][i0], sv[nb][i0 + 1])
-                 : vmin3(tm[nb], sv[nb][i0], sv[nb][i0 + 1]);
+    float& m = tm[nb][(p >> 1) & 1];
+    m = POS ? __builtin_fmaxf(__builtin_fmaxf(m, sv[nb][i0]), sv[nb][i0 + 1])   // one v_max3
+            : __builtin_fminf(__builtin_fminf(m, sv[nb][i0]), sv[nb][i0 + 1]);
   };
   // running max, lazy O rescale, exponent offset for the tile now in sv
   auto settle_max = [&]() CA_INLINE {
@@ -491,7 +468,8 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     bool any_need = false;
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb) {
-      tmax[nb] = pair32_max(tm[nb] * scale_log2);
+      const float t2 = POS ? __builtin_fmaxf(tm[nb][0], tm[nb][1]) : __builtin_fminf(tm[nb][0], tm[nb][1]);
+      tmax[nb] = pair32_max(t2 * scale_log2);
       any_need |= tmax[nb] > m_run[nb] + 8.0f;
     }
     if (__builtin_expect(wave_any(any_need), 0)) {  // rare: the max rose by > 2^8
@@ -576,7 +554,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     constexpr bool NEXT = decltype(next_tag)::value;
     const int k0n = tn * kBN;
 #pragma unroll
-    for (int nb = 0; nb < NH; ++nb) tm[nb] = kMaskVal;
+    for (int nb = 0; nb < NH; ++nb) tm[nb][0] = tm[nb][1] = kMaskVal;
     if (PV) {
       const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
       u32x2 vr[3][2];
@@ -730,18 +708,19 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
   const int n_qt = (S + BM - 1) / BM;
   const long long grid = (long long)n_qt * B * Hq;
   if (grid == 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const float sl2 = scale * kLog2e;
   const dim3 block(64 * pf_waves(BM, NH));
   if (sl2 >= 0.f) {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt);
+                       n_qt, (int)grid);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt);
+                       n_qt, (int)grid);
   }
   return hipGetLastError();
 }
@@ -758,9 +737,10 @@ static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, 
   const int n_qt = (S + BM - 1) / BM;
   const long long grid = (long long)n_qt * B * Hq;
   if (grid == 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
                      dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt);
+                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, (int)grid);
   return hipGetLastError();
 }
 
