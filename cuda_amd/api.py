@@ -12,7 +12,8 @@ Differences from the reference, all widening what is accepted:
   * FP8 caches decode OCP e4m3, the reference test's intended semantics
     (tests/test_kernels_misc.py:42-64), and also accept float8_e4m3fn tensors;
   * a sequence with context length 0 yields zeros instead of an unwritten row.
-Not supported yet: float32 q/k/v (raises), autograd through flash_attention.
+float32 q/k/v are accepted where the reference instantiates float (prefill,
+flash_decode, paged decode). Not supported: autograd through flash_attention.
 """
 import ctypes
 import math

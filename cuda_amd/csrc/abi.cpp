@@ -42,7 +42,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 ca_status check_16bit_dtype(ca_dtype dt, const char* what) {
   if (dt == CA_BF16 || dt == CA_F16) return CA_OK;
   if (dt == CA_F32)
-    return fail(CA_UNSUPPORTED, "%s: float32 tensors are not supported on gfx950 yet (use bf16/fp16)", what);
+    return fail(CA_UNSUPPORTED, "%s: float32 queries are not supported (use bf16/fp16)", what);
+  return fail(CA_INVALID_ARGUMENT, "%s: unknown dtype %d", what, (int)dt);
+}
+
+// float32, fp16 or bf16: the entry points the reference instantiates for float.
+ca_status check_float_dtype(ca_dtype dt, const char* what) {
+  if (dt == CA_BF16 || dt == CA_F16 || dt == CA_F32) return CA_OK;
   return fail(CA_INVALID_ARGUMENT, "%s: unknown dtype %d", what, (int)dt);
 }
 
@@ -79,7 +85,7 @@ ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, c
                                  void* stream) {
   const char* what = "flash_attention";
   ca_status st;
-  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
   if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
   if (batch < 0 || seq_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
@@ -101,7 +107,7 @@ ca_status ca_flash_decode(ca_dtype dtype, const void* q, const void* k, const vo
                           void* stream) {
   const char* what = "flash_decode";
   ca_status st;
-  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
   if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
   if (batch < 0 || kv_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
@@ -154,7 +160,7 @@ ca_status ca_paged_attention(ca_dtype dtype, const void* query, const void* key_
                              void* stream) {
   const char* what = "paged_attention";
   ca_status st;
-  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = paged_common_checks(what, query, key_cache, value_cache, block_tables, context_lens,
                                 out, num_seqs, num_q_heads, num_kv_heads, head_dim,
                                 max_blocks_per_seq, page_size, num_blocks, workspace,

@@ -70,6 +70,10 @@ struct BF16 {
     const vec2 one = {(__bf16)1.0f, (__bf16)1.0f};
     return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
   }
+  // out[i] = x rounded to this type
+  static __device__ __forceinline__ void store(void* out, size_t i, float x) {
+    ((uint16_t*)out)[i] = __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
 };
 
 struct F16 {
@@ -102,6 +106,16 @@ struct F16 {
   static __device__ __forceinline__ float dot2sum(vec2 v, float acc) {
     const vec2 one = {(_Float16)1.0f, (_Float16)1.0f};
     return __builtin_amdgcn_fdot2(v, one, acc, false);
+  }
+  static __device__ __forceinline__ void store(void* out, size_t i, float x) {
+    ((uint16_t*)out)[i] = __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+};
+
+// fp32 element type (only the output store is used by shared kernels).
+struct F32 {
+  static __device__ __forceinline__ void store(void* out, size_t i, float x) {
+    ((float*)out)[i] = x;
   }
 };
 

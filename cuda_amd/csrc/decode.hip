@@ -797,8 +797,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 template <typename Tr, int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
-    const float* __restrict__ ws_lse, uint16_t* __restrict__ O, int Hq, int max_splits) {
-  using vec2 = typename Tr::vec2;
+    const float* __restrict__ ws_lse, void* __restrict__ O, int Hq, int max_splits) {
   constexpr int PER = D / 64;
   const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
   const int lane = threadIdx.x;
@@ -833,10 +832,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const vec2 pk = Tr::pack2(acc[i] * inv, 0.f);
-    O[((size_t)n * Hq + hq) * D + lane * PER + i] = __builtin_bit_cast(uint16_t, pk[0]);
-  }
+  for (int i = 0; i < PER; ++i) Tr::store(O, ((size_t)n * Hq + hq) * D + lane * PER + i, acc[i] * inv);
 }
 
 size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
@@ -881,9 +877,224 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_splits <= 1) return e;
   hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
-                     KIND == kKindContig16 ? nullptr : lens, max_tokens, ws_o, ws_lse,
-                     (uint16_t*)out, Hq, max_splits);
+                     KIND == kKindContig16 ? nullptr : lens, max_tokens, ws_o, ws_lse, out, Hq,
+                     max_splits);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// float32 decode, contiguous or paged cache (VALU).
+//
+// The reference instantiates its decode and paged kernels for float
+// (async_flash_decode_instantiations.cu:4, paged_attention_instantiations.cu);
+// fp32 has no 16-bit MFMA operand form and decode is HBM-bound, so here the
+// dot products are fp32 FMAs. Per step of 64 tokens each lane owns one token
+// for S = q.k (the wave's G query heads are broadcast from LDS, pre-scaled to
+// log2 units), the step's max is a wave reduction, and for O += P V each lane
+// owns D/64 head-dim elements with P broadcast from LDS. Same split-K
+// partition (kPagesPerWave pages per wave, split index outermost), workspace
+// layout and merge as the 16-bit kernels. A paged sequence's tokens past its
+// length are never read into O (their bytes may be anything).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max_f(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <int D, bool PAGED, int G>
+__global__ __launch_bounds__(64) void decode_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    float* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
+    int Hkv, int S_contig, int max_blocks, int max_splits, int n_hc, float scale_log2) {
+  constexpr int PER = D / 64;
+  constexpr int kSplitTokens = kPagesPerWave * kDecodePage;
+  __shared__ float qs[G][D];
+  __shared__ float ps[G][64];
+
+  const int lane = threadIdx.x;
+  int w = blockIdx.x;
+  const int per_split = (int)(gridDim.x / max_splits);
+  const int split = w / per_split;
+  w %= per_split;
+  const int hc = w % n_hc;
+  w /= n_hc;
+  const int hk = w % Hkv;
+  const int n = w / Hkv;
+  const int Gq = Hq / Hkv;
+  const int hq0 = hk * Gq + hc * G;
+  const int Gc = min(G, Gq - hc * G);
+  const int L = PAGED ? min(max(0, context_lens[n]), max_blocks * kDecodePage) : S_contig;
+  const int n_splits = max(1, (L + kSplitTokens - 1) / kSplitTokens);
+  if (split >= n_splits) return;
+  const int t_begin = split * kSplitTokens;
+  const int t_end = min(t_begin + kSplitTokens, L);
+
+  for (int i = lane; i < G * D; i += 64) {
+    const int g = i / D, d = i % D;
+    qs[g][d] = (g < Gc) ? Q[((size_t)n * Hq + hq0 + g) * D + d] * scale_log2 : 0.f;
+  }
+  __syncthreads();
+
+  float m_run[G], l_run[G], o[G][PER];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = kNegInf;
+    l_run[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[g][i] = 0.f;
+  }
+  const float* Kh = PAGED ? Kc : Kc + ((size_t)n * Hkv + hk) * S_contig * D;
+  const float* Vh = PAGED ? Vc : Vc + ((size_t)n * Hkv + hk) * S_contig * D;
+  const int32_t* bt = PAGED ? block_tables + (size_t)n * max_blocks : nullptr;
+
+  for (int t0 = t_begin; t0 < t_end; t0 += 64) {  // t0 is a multiple of 64: 4 whole pages
+    const int t = t0 + lane;
+    const bool valid = t < t_end;
+    const int tc = valid ? t : t_end - 1;
+    float s[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) s[g] = 0.f;
+    if (PAGED) {
+      const int blk = bt[tc / kDecodePage];
+      const float* kp = Kc + ((size_t)blk * Hkv + hk) * D * kDecodePage + (tc % kDecodePage);
+#pragma unroll 8
+      for (int d = 0; d < D; ++d) {
+        const float kv = kp[d * kDecodePage];
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = __builtin_fmaf(qs[g][d], kv, s[g]);
+      }
+    } else {
+      const float* kp = Kh + (size_t)tc * D;
+#pragma unroll 4
+      for (int d = 0; d < D; d += 4) {
+        const float4 kv = *(const float4*)(kp + d);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          s[g] = __builtin_fmaf(qs[g][d], kv.x, s[g]);
+          s[g] = __builtin_fmaf(qs[g][d + 1], kv.y, s[g]);
+          s[g] = __builtin_fmaf(qs[g][d + 2], kv.z, s[g]);
+          s[g] = __builtin_fmaf(qs[g][d + 3], kv.w, s[g]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float sm = valid ? s[g] : kNegInf;
+      const float m_new = __builtin_fmaxf(m_run[g], wave_max_f(sm));
+      const float alpha = (m_run[g] == kNegInf) ? 0.f : fast_exp2(m_run[g] - m_new);
+      const float p = valid ? fast_exp2(sm - m_new) : 0.f;
+      l_run[g] = l_run[g] * alpha + p;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) o[g][i] *= alpha;
+      m_run[g] = m_new;
+      ps[g][lane] = p;
+    }
+    __syncthreads();
+    const int nv = min(64, t_end - t0);
+    if (PAGED) {
+      for (int pg = 0; pg < 4 && 16 * pg < nv; ++pg) {
+        const int blk = bt[t0 / kDecodePage + pg];
+        const float* vp = Vc + ((size_t)blk * Hkv + hk) * D * kDecodePage;
+        const int cnt = min(16, nv - 16 * pg);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const float* vrow = vp + (size_t)(lane + 64 * i) * kDecodePage;
+          float vv[16];
+#pragma unroll
+          for (int j = 0; j < 16; j += 4) {
+            const float4 x = *(const float4*)(vrow + j);
+            vv[j] = x.x; vv[j + 1] = x.y; vv[j + 2] = x.z; vv[j + 3] = x.w;
+          }
+          for (int j = 0; j < cnt; ++j) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) o[g][i] = __builtin_fmaf(ps[g][16 * pg + j], vv[j], o[g][i]);
+          }
+        }
+      }
+    } else {
+      for (int j = 0; j < nv; ++j) {
+        const float* vrow = Vh + (size_t)(t0 + j) * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const float vv = vrow[lane + 64 * i];
+#pragma unroll
+          for (int g = 0; g < G; ++g) o[g][i] = __builtin_fmaf(ps[g][j], vv, o[g][i]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  const bool single = (n_splits == 1);
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (g >= Gc) break;
+    const float lt = wave_sum_f(l_run[g]);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const int hq = hq0 + g;
+    if (single) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) O[((size_t)n * Hq + hq) * D + lane + 64 * i] = o[g][i] * inv;
+    } else {
+      const size_t sl = ((size_t)n * Hq + hq) * max_splits + split;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) ws_o[sl * D + lane + 64 * i] = o[g][i] * inv;
+      if (lane == 0) ws_lse[sl] = (lt > 0.f) ? m_run[g] + __log2f(lt) : kNegInf;
+    }
+  }
+}
+
+template <int D, bool PAGED, int G>
+static hipError_t launch_decode_f32_t(const void* q, const void* kc, const void* vc,
+                                      const int32_t* bt, const int32_t* lens, void* out, int N,
+                                      int Hq, int Hkv, int max_blocks, int S_contig, float scale,
+                                      void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int max_tokens = PAGED ? max_blocks * kDecodePage : S_contig;
+  const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
+  const int max_splits = max(1, (pages + kPagesPerWave - 1) / kPagesPerWave);
+  const int Gq = Hq / Hkv;
+  const int n_hc = (Gq + G - 1) / G;
+  const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
+  if (ws_bytes < need) return hipErrorInvalidValue;
+  float* ws_o = (float*)ws;
+  float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
+  const long long grid = (long long)N * Hkv * n_hc * max_splits;
+  if (grid == 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((decode_f32_kernel<D, PAGED, G>), dim3((unsigned)grid), dim3(64), 0, stream,
+                     (const float*)q, (const float*)kc, (const float*)vc, bt, lens, (float*)out,
+                     ws_o, ws_lse, Hq, Hkv, S_contig, max_blocks, max_splits, n_hc,
+                     scale * kLog2e);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || max_splits <= 1) return e;
+  hipLaunchKernelGGL((decode_merge_kernel<F32, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
+                     PAGED ? lens : nullptr, max_tokens, ws_o, ws_lse, out, Hq, max_splits);
+  return hipGetLastError();
+}
+
+// Query heads per wave for the fp32 kernel: the group size rounded up to a
+// power of two, at most 8 (larger groups take several waves).
+template <int D, bool PAGED>
+static hipError_t launch_decode_f32(const void* q, const void* kc, const void* vc,
+                                    const int32_t* bt, const int32_t* lens, void* out, int N,
+                                    int Hq, int Hkv, int max_blocks, int S_contig, float scale,
+                                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int Gq = Hq / Hkv;
+#define CA_F32D(GG)                                                                          \
+  return launch_decode_f32_t<D, PAGED, GG>(q, kc, vc, bt, lens, out, N, Hq, Hkv, max_blocks, \
+                                           S_contig, scale, ws, ws_bytes, stream);
+  if (Gq <= 1) { CA_F32D(1) }
+  if (Gq <= 2) { CA_F32D(2) }
+  if (Gq <= 4) { CA_F32D(4) }
+  CA_F32D(8)
+#undef CA_F32D
 }
 
 hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const void* kc,
@@ -899,6 +1110,14 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
                                          max_blocks_per_seq, num_blocks, 0, scale, ws,      \
                                          ws_bytes, stream);
   if (cache_kind == 0) {
+    if (dtype == kDtypeF32) {
+      if (D == 64)
+        return launch_decode_f32<64, true>(q, kc, vc, block_tables, context_lens, out, N, Hq, Hkv,
+                                           max_blocks_per_seq, 0, scale, ws, ws_bytes, stream);
+      if (D == 128)
+        return launch_decode_f32<128, true>(q, kc, vc, block_tables, context_lens, out, N, Hq, Hkv,
+                                            max_blocks_per_seq, 0, scale, ws, ws_bytes, stream);
+    }
     if (dtype == kDtypeBF16) { CA_DEC(BF16, 64, kKindPaged16) CA_DEC(BF16, 128, kKindPaged16) }
     if (dtype == kDtypeF16) { CA_DEC(F16, 64, kKindPaged16) CA_DEC(F16, 128, kKindPaged16) }
   } else {
@@ -920,6 +1139,14 @@ hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const vo
   if (dtype == kDtypeBF16) { CA_FD(BF16, 64) CA_FD(BF16, 128) }
   if (dtype == kDtypeF16) { CA_FD(F16, 64) CA_FD(F16, 128) }
 #undef CA_FD
+  if (dtype == kDtypeF32) {
+    if (D == 64)
+      return launch_decode_f32<64, false>(q, k, v, nullptr, nullptr, o, B, Hq, Hkv, 0, S, scale,
+                                          ws, ws_bytes, stream);
+    if (D == 128)
+      return launch_decode_f32<128, false>(q, k, v, nullptr, nullptr, o, B, Hq, Hkv, 0, S, scale,
+                                           ws, ws_bytes, stream);
+  }
   return hipErrorInvalidValue;
 }
 

@@ -1,0 +1,226 @@
+// float32 prefill (flash-attention forward) for gfx950 on fp32 MFMAs.
+//
+// The reference instantiates its prefill entry points for float
+// (flash_attention_v2_instantiations.cu, flash_attention_v3_hopper_
+// instantiations.cu, fused_gqa_instantiations.cu; binding
+// fused_softmax_binding.cpp:77-81). Same contract as the 16-bit kernels:
+// O = softmax(Q K^T * scale [+ causal mask]) V per (b, q head), GQA by
+// kv_head = q_head / (Hq / Hkv), O = 0 for a row with no visible key.
+//
+// Work decomposition: one workgroup = 4 waves x 32 query rows of one (b, h);
+// K/V tiles of 32 keys, double-buffered in LDS (register-staged loads, one
+// barrier per tile). Per wave and tile, on v_mfma_f32_32x32x2_f32 (one fp32
+// element of each operand per lane, k = lane / 32):
+//   S^T[32 keys x 32 q] = K Q^T   over D/2 steps; lane half h contracts
+//     head-dim elements (D/2) h + step, so a lane's K row and Q row are read
+//     as contiguous float4s;
+//   O^T[D x 32 q] += V^T P^T       over 16 steps of two keys.
+// Key permutation: accumulator register r of lane half h holds S^T row
+// 8 (r/4) + 4 h + r%4 (the 32x32 accumulator layout); the A-operand lane for
+// that row reads key 16 h + r, so register r of half h is exactly the PV
+// B-operand element for key 16 h + r at step r: P never leaves its registers.
+// LDS: K row-major with row stride D + 4 floats, V transposed ([D][32 keys])
+// with row stride 36 floats; both make the float4 operand reads of a 16-lane
+// group hit 16 distinct 4-bank groups.
+#include "common.h"
+#include "launch.h"
+
+namespace ca {
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_work) {
+  constexpr int NW = 4;
+  constexpr int BM = 32 * NW;
+  constexpr int BN = 32;
+  constexpr int KS = D + 4;     // K row stride (floats)
+  constexpr int VS = BN + 4;    // V^T row stride (floats)
+  constexpr int HD = D / 2;     // S^T contraction steps
+  constexpr int NOB = D / 32;   // O^T row blocks
+  constexpr int F4_ROW = D / 4;                  // float4s per K/V row
+  constexpr int F4_TILE = BN * F4_ROW;           // float4s per tile
+  constexpr int F4_PER_THREAD = F4_TILE / (NW * 64);
+  static_assert(F4_PER_THREAD * NW * 64 == F4_TILE, "tile staging must cover the tile");
+
+  __shared__ __attribute__((aligned(16))) float Ks[2][BN * KS];
+  __shared__ __attribute__((aligned(16))) float Vt[2][D * VS];
+
+  const int work = xcd_remap(blockIdx.x, n_work);
+  const int bh = work / n_qt;
+  const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
+  const int b = bh / Hq, h = bh % Hq;
+  const int hk = h / (Hq / Hkv);
+  const int q0 = qt * BM;
+  const float* Qp = Q + (size_t)(b * Hq + h) * S * D;
+  float* Op = O + (size_t)(b * Hq + h) * S * D;
+  const float* Kp = K + (size_t)(b * Hkv + hk) * S * D;
+  const float* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int qw0 = q0 + wave * 32;
+  const int myq = qw0 + l32;
+
+  // Q as the B operand: qv[k] = Q[myq][HD * hl + k]
+  float qv[HD];
+#pragma unroll
+  for (int k4 = 0; k4 < HD; k4 += 4) {
+    float4 x = {0.f, 0.f, 0.f, 0.f};
+    if (myq < S) x = *(const float4*)(Qp + (size_t)myq * D + HD * hl + k4);
+    qv[k4] = x.x; qv[k4 + 1] = x.y; qv[k4 + 2] = x.z; qv[k4 + 3] = x.w;
+  }
+
+  const int kv_end = CAUSAL ? min(S, q0 + BM) : S;
+  const int n_tiles = (kv_end + BN - 1) / BN;
+
+  float4 kreg[F4_PER_THREAD], vreg[F4_PER_THREAD];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int it = 0; it < F4_PER_THREAD; ++it) {
+      const int idx = tid + NW * 64 * it;
+      const int row = idx / F4_ROW, c4 = idx % F4_ROW;
+      const int key = t * BN + row;
+      if (key < S) {
+        kreg[it] = *(const float4*)(Kp + (size_t)key * D + 4 * c4);
+        vreg[it] = *(const float4*)(Vp + (size_t)key * D + 4 * c4);
+      } else {
+        kreg[it] = float4{0.f, 0.f, 0.f, 0.f};
+        vreg[it] = float4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int it = 0; it < F4_PER_THREAD; ++it) {
+      const int idx = tid + NW * 64 * it;
+      const int row = idx / F4_ROW, c4 = idx % F4_ROW;
+      *(float4*)(&Ks[buf][row * KS + 4 * c4]) = kreg[it];
+      float* vt = &Vt[buf][(4 * c4) * VS + row];
+      vt[0] = vreg[it].x;
+      vt[VS] = vreg[it].y;
+      vt[2 * VS] = vreg[it].z;
+      vt[3 * VS] = vreg[it].w;
+    }
+  };
+
+  f32x16 o[NOB];
+#pragma unroll
+  for (int i = 0; i < NOB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m_run = kNegInf, l_run = 0.f;
+  const int krow = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
+
+  if (n_tiles > 0) gload(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    lstore(buf);
+    __syncthreads();
+    if (t + 1 < n_tiles) gload(t + 1);
+    const int k0 = t * BN;
+    if (CAUSAL && k0 > qw0 + 31) continue;  // tile entirely above this wave's rows
+
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+    const float* kr = Ks[buf] + krow * KS + HD * hl;
+#pragma unroll
+    for (int k4 = 0; k4 < HD; k4 += 4) {
+      const float4 a = *(const float4*)(kr + k4);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qv[k4], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qv[k4 + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qv[k4 + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qv[k4 + 3], s, 0, 0, 0);
+    }
+
+    // online softmax in the log2 domain; register r holds key k0 + 16 hl + r
+    float x[16];
+    float tm = kNegInf;
+    const bool need_mask = CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x[r] = s[r] * scale_log2;
+      if (need_mask) {
+        const int key = k0 + 16 * hl + r;
+        if (key >= S || (CAUSAL && key > myq)) x[r] = kNegInf;
+      }
+      tm = __builtin_fmaxf(tm, x[r]);
+    }
+    const float m_new = __builtin_fmaxf(m_run, pair32_max(tm));
+    const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+#pragma unroll
+    for (int i = 0; i < NOB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    m_run = m_new;
+    const float msub = (m_run == kNegInf) ? 0.f : m_run;
+    float p[16];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp2(x[r] - msub);
+      psum += p[r];
+    }
+    l_run = l_run * alpha + psum;
+
+    // O^T += V^T P^T: A = V^T[32 ob + l32][16 hl + step], B = p[step]
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) {
+      const float* vr = Vt[buf] + (32 * ob + l32) * VS + 16 * hl;
+#pragma unroll
+      for (int k4 = 0; k4 < 16; k4 += 4) {
+        const float4 a = *(const float4*)(vr + k4);
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, p[k4], o[ob], 0, 0, 0);
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, p[k4 + 1], o[ob], 0, 0, 0);
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, p[k4 + 2], o[ob], 0, 0, 0);
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, p[k4 + 3], o[ob], 0, 0, 0);
+      }
+    }
+  }
+
+  const float l_tot = pair32_sum(l_run);
+  const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+  if (myq < S) {
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int d = 32 * ob + 8 * a + 4 * hl;
+        const float4 w = {o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv, o[ob][4 * a + 2] * inv,
+                          o[ob][4 * a + 3] * inv};
+        *(float4*)(Op + (size_t)myq * D + d) = w;
+      }
+    }
+  }
+}
+
+template <int D, bool CAUSAL>
+static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void* v, void* o,
+                                       int B, int Hq, int Hkv, int S, float scale,
+                                       hipStream_t stream) {
+  constexpr int BM = 128;
+  const int n_qt = (S + BM - 1) / BM;
+  const long long grid = (long long)n_qt * B * Hq;
+  if (grid == 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream,
+                     (const float*)q, (const float*)k, (const float*)v, (float*)o, S, Hq, Hkv,
+                     scale * kLog2e, n_qt, (int)grid);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, int B,
+                              int Hq, int Hkv, int S, int D, float scale, bool causal,
+                              hipStream_t stream) {
+  if (D == 64)
+    return causal ? launch_prefill_f32_t<64, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
+                  : launch_prefill_f32_t<64, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+  if (D == 128)
+    return causal ? launch_prefill_f32_t<128, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
+                  : launch_prefill_f32_t<128, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ca

@@ -16,6 +16,10 @@ constexpr int kDtypeBF16 = 2;
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
                           hipStream_t stream);
+// float32 prefill (f32.hip)
+hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, int B,
+                              int Hq, int Hkv, int S, int D, float scale, bool causal,
+                              hipStream_t stream);
 
 // Split-K geometry of the decode kernels: pages of 16 tokens; one wave walks
 // one split of kPagesPerWave pages.

@@ -761,6 +761,7 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
 #else
 #define CA_PREFILL_128(TR) CA_PREFILL_CASE(TR, 128)
 #endif
+  if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, B, Hq, Hkv, S, D, scale, causal, stream);
   if (dtype == kDtypeBF16) {
     CA_PREFILL_CASE(BF16, 64)
     CA_PREFILL_128(BF16)

@@ -68,8 +68,12 @@ def _status(name, *args):
 def test_prefill_rejects_bad_arguments():
     st = _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 1, 4, 4, 64, 96, 0.1, 0, None)
     assert st == L.CA_INVALID_ARGUMENT and b"head_dim" in L.load().ca_last_error()
-    st = _status("ca_flash_attention_fwd", L.CA_F32, P, P, P, P, 1, 4, 4, 64, 64, 0.1, 0, None)
-    assert st == L.CA_UNSUPPORTED
+    # float32 is a supported dtype here (the reference instantiates float), so
+    # the other checks still apply to it
+    st = _status("ca_flash_attention_fwd", L.CA_F32, P, P, P, P, 1, 4, 4, 64, 96, 0.1, 0, None)
+    assert st == L.CA_INVALID_ARGUMENT and b"head_dim" in L.load().ca_last_error()
+    st = _status("ca_flash_attention_fwd", 7, P, P, P, P, 1, 4, 4, 64, 64, 0.1, 0, None)
+    assert st == L.CA_INVALID_ARGUMENT and b"dtype" in L.load().ca_last_error()
     st = _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 1, 6, 4, 64, 64, 0.1, 0, None)
     assert st == L.CA_INVALID_ARGUMENT and b"multiple" in L.load().ca_last_error()
     st = _status("ca_flash_attention_fwd", L.CA_BF16, ctypes.c_void_p(18), P, P, P, 1, 4, 4, 64,
@@ -93,6 +97,11 @@ def test_paged_rejects_bad_arguments():
     assert b"workspace" in L.load().ca_last_error()
     fp8 = [L.CA_BF16, P, P, P, None, None, 1, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
     assert _status("ca_fp8_paged_attention", *fp8) == L.CA_INVALID_ARGUMENT
+    # the FP8 cache entry point has no float32-query form (the reference's
+    # instantiations are half / bf16 only)
+    fp8_f32 = list(fp8)
+    fp8_f32[0] = L.CA_F32
+    assert _status("ca_fp8_paged_attention", *fp8_f32) == L.CA_UNSUPPORTED
 
 
 def test_mxfp8_rejects_bad_arguments():

@@ -1,0 +1,118 @@
+"""GPU tier: float32 inputs (prefill, flash_decode, paged decode) vs the oracle.
+
+The reference binding dispatches float32 for flash_attention / _v3_hopper /
+fused_gqa (fused_softmax_binding.cpp:77-81, 275-277), async_flash_decode and
+paged_attention (:142-146); its tests use fp16/bf16 only (tests/
+test_attention.py:13 there), so the grids below are its fp16/bf16 grids run in
+float32, plus split-K lengths, ragged S, the golden vectors and NaN bytes past
+a paged context's end. Tolerance: the reference's float32 tolerance
+(tests/_utils.py:23-27 there, 1e-4), here as max-abs 1e-4 and mean-abs 1e-5.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import cuda_llm
+import oracle
+from _util import assert_close, build_paged, paged_oracle, qkv, to_np
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
+TOL_F32 = dict(max_abs=1e-4, mean_abs=1e-5)
+F32 = torch.float32
+
+
+@pytest.mark.parametrize("fn_name", ["flash_attention_forward", "flash_attention_v3_hopper"])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("seq_len", [1, 64, 100, 256, 300])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_flash_forward_f32(dev, fn_name, head_dim, seq_len, is_causal):
+    q, k, v = qkv(2, 4, seq_len, head_dim, F32, dev)
+    out = getattr(cuda_llm, fn_name)(q, k, v, is_causal=is_causal)
+    torch.cuda.synchronize()
+    assert out.dtype == F32
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=is_causal, dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name=fn_name)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (8, 8), (4, 1)])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_gqa_f32(dev, head_dim, hq, hkv, is_causal):
+    q, k, v = qkv(1, hq, 100, head_dim, F32, dev, hkv=hkv)
+    out = cuda_llm.fused_gqa_forward(q, k, v, is_causal=is_causal)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=is_causal, dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name="gqa f32")
+
+
+@pytest.mark.parametrize("name", ["attn_causal_d64", "attn_full_d64", "attn_gqa_causal_d128"])
+def test_golden_vectors_f32(dev, name):
+    g = np.load(GOLDEN, allow_pickle=False)
+    q, k, v = (torch.from_numpy(g[f"{name}/{x}"]).to(dev).to(F32) for x in "qkv")
+    out = cuda_llm.flash_attention(q, k, v, is_causal=bool(g[f"{name}/causal"]))
+    torch.cuda.synchronize()
+    assert_close(to_np(out), g[f"{name}/out"], **TOL_F32, name=name)
+
+
+def test_large_logits_and_negative_scale_f32(dev):
+    q, k, v = qkv(1, 2, 200, 128, F32, dev)
+    q = q * 8.0
+    for scale in (0.5, -0.2):
+        out = cuda_llm.flash_attention(q, k, v, is_causal=True, softmax_scale=scale)
+        torch.cuda.synchronize()
+        ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=True, scale=scale,
+                               dtype=np.float64)
+        assert_close(to_np(out), ref, **TOL_F32, name=f"scale {scale}")
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("kv_len", [1, 63, 64, 1000, 2500])
+def test_flash_decode_f32(dev, head_dim, kv_len):
+    q = torch.randn(2, 4, 1, head_dim, device=dev, dtype=F32)
+    k = torch.randn(2, 4, kv_len, head_dim, device=dev, dtype=F32)
+    v = torch.randn(2, 4, kv_len, head_dim, device=dev, dtype=F32)
+    out = cuda_llm.async_flash_decode(q, k, v)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name="decode f32")
+
+
+@pytest.mark.parametrize("hq,hkv,kv_len", [(32, 8, 5000), (8, 1, 1025), (40, 2, 700)])
+def test_flash_decode_gqa_split_f32(dev, hq, hkv, kv_len):
+    q = torch.randn(2, hq, 1, 128, device=dev, dtype=F32)
+    k = torch.randn(2, hkv, kv_len, 128, device=dev, dtype=F32)
+    v = torch.randn(2, hkv, kv_len, 128, device=dev, dtype=F32)
+    out = cuda_llm.flash_decode(q, k, v)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name="flash_decode gqa f32")
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (32, 8), (40, 2)])
+def test_paged_f32(dev, head_dim, hq, hkv):
+    lens = [0, 1, 15, 16, 17, 300, 1023, 1024, 1025, 3000]
+    case = build_paged(lens, hq, hkv, head_dim, F32, dev, pool=800)
+    out = cuda_llm.paged_attention_forward(case["query"], case["key_cache"], case["value_cache"],
+                                           case["block_tables"], case["context_lens"])
+    torch.cuda.synchronize()
+    assert out.dtype == F32
+    assert_close(to_np(out), paged_oracle(case), **TOL_F32, name=f"paged f32 {hq}/{hkv}")
+    assert torch.all(out[0] == 0)
+
+
+def test_paged_f32_nan_tail_does_not_leak(dev):
+    """Bytes past a sequence's length in its last page may be anything."""
+    case = build_paged([37, 5, 1030], 8, 2, 128, F32, dev)
+    ref = paged_oracle(case)
+    for i, L in enumerate([37, 5, 1030]):
+        blk = int(case["block_tables"][i, (L - 1) // 16])
+        case["key_cache"][blk, :, :, L % 16:] = float("nan")
+        case["value_cache"][blk, :, :, L % 16:] = float("nan")
+    out = cuda_llm.paged_attention_forward(case["query"], case["key_cache"], case["value_cache"],
+                                           case["block_tables"], case["context_lens"])
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref, **TOL_F32, name="paged f32 nan tail")
