@@ -287,8 +287,10 @@ def summary(name, r):
 def main():
     ap = argparse.ArgumentParser(description="attention forward hot path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 200 warm-up launches (0.1-0.3 s) bring the GPU to its sustained clock;
+    # with a handful the first timed launches still run at a ramping clock
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="all", choices=["all"] + list(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)

@@ -65,11 +65,6 @@ struct BF16 {
   static __device__ __forceinline__ float to_float(uint16_t x) {
     return __uint_as_float(((uint32_t)x) << 16);
   }
-  // acc + v[0] + v[1] in one v_dot2 (the sum of the rounded 16-bit values)
-  static __device__ __forceinline__ float dot2sum(vec2 v, float acc) {
-    const vec2 one = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(v, one, acc, false);
-  }
   // out[i] = x rounded to this type
   static __device__ __forceinline__ void store(void* out, size_t i, float x) {
     ((uint16_t*)out)[i] = __builtin_bit_cast(uint16_t, (__bf16)x);
@@ -102,10 +97,6 @@ struct F16 {
   static __device__ __forceinline__ float to_float(uint16_t x) {
     _Float16 h = __builtin_bit_cast(_Float16, x);
     return (float)h;
-  }
-  static __device__ __forceinline__ float dot2sum(vec2 v, float acc) {
-    const vec2 one = {(_Float16)1.0f, (_Float16)1.0f};
-    return __builtin_amdgcn_fdot2(v, one, acc, false);
   }
   static __device__ __forceinline__ void store(void* out, size_t i, float x) {
     ((uint16_t*)out)[i] = __builtin_bit_cast(uint16_t, (_Float16)x);
@@ -193,6 +184,31 @@ __device__ __forceinline__ int xcd_remap(int w, int total) {
   const int q = total / kXcd, r = total % kXcd;
   const int x = w % kXcd, i = w / kXcd;
   return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+// Query tiles of one prefill workgroup (work index after xcd_remap).
+// Unpaired: one tile; the work index runs over (b, h) and, within a head,
+// over its tiles longest causal walk first. Paired (causal launches): tiles
+// n_qt-1-p and p of one (b, h), whose causal key walks add up to the same
+// length for every p, so all workgroups carry equal work and the grid ends
+// without a tail of long workgroups; an odd n_qt leaves the middle tile alone.
+struct QTileWork {
+  int bh, qt0, qt1;  // qt1 < 0: no second tile
+};
+__device__ __forceinline__ QTileWork prefill_work(int work, int n_qt, int paired) {
+  QTileWork w;
+  if (paired) {
+    const int n_pairs = (n_qt + 1) >> 1;
+    const int p = work % n_pairs;
+    w.bh = work / n_pairs;
+    w.qt0 = n_qt - 1 - p;
+    w.qt1 = (p == w.qt0) ? -1 : p;
+  } else {
+    w.bh = work / n_qt;
+    w.qt0 = n_qt - 1 - work % n_qt;
+    w.qt1 = -1;
+  }
+  return w;
 }
 
 }  // namespace ca

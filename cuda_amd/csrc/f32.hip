@@ -27,10 +27,12 @@
 
 namespace ca {
 
+// One query tile (BM rows of head bh): the key walk and the output store.
+// Other waves may still read the LDS tiles when a wave returns.
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
+__device__ CA_INLINE void prefill_f32_qtile(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_work) {
+    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int bh, int qt) {
   constexpr int NW = 4;
   constexpr int BM = 32 * NW;
   constexpr int BN = 32;
@@ -46,9 +48,6 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
   __shared__ __attribute__((aligned(16))) float Ks[2][BN * KS];
   __shared__ __attribute__((aligned(16))) float Vt[2][D * VS];
 
-  const int work = xcd_remap(blockIdx.x, n_work);
-  const int bh = work / n_qt;
-  const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
   const int q0 = qt * BM;
@@ -197,17 +196,33 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
 }
 
 template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_work,
+    int paired) {
+  const QTileWork wk = prefill_work(xcd_remap(blockIdx.x, n_work), n_qt, paired);
+  const int n_pass = wk.qt1 < 0 ? 1 : 2;
+#pragma clang loop unroll(disable)
+  for (int pass = 0; pass < n_pass; ++pass) {
+    // the second tile restages the LDS buffers: every wave must be done reading them
+    if (pass) __syncthreads();
+    prefill_f32_qtile<D, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, wk.bh, pass ? wk.qt1 : wk.qt0);
+  }
+}
+
+template <int D, bool CAUSAL>
 static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void* v, void* o,
                                        int B, int Hq, int Hkv, int S, float scale,
                                        hipStream_t stream) {
   constexpr int BM = 128;
   const int n_qt = (S + BM - 1) / BM;
-  const long long grid = (long long)n_qt * B * Hq;
+  int paired = 0;
+  const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, 2, &paired);
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream,
                      (const float*)q, (const float*)k, (const float*)v, (float*)o, S, Hq, Hkv,
-                     scale * kLog2e, n_qt, (int)grid);
+                     scale * kLog2e, n_qt, (int)grid, paired);
   return hipGetLastError();
 }
 

@@ -21,6 +21,30 @@ hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void*
                               int Hq, int Hkv, int S, int D, float scale, bool causal,
                               hipStream_t stream);
 
+// Compute units of the current device (cached per device; 0 if unknown).
+inline int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Workgroups of a prefill launch of n_qt query tiles per (b, h). A causal
+// launch pairs query tiles (n_qt-1-p with p, one workgroup each pair) when
+// the paired grid still gives every workgroup slot of the device at least one
+// workgroup; otherwise each workgroup takes one tile.
+inline long long prefill_grid(int B, int Hq, int n_qt, bool causal, int wg_per_cu, int* paired) {
+  const long long single = (long long)B * Hq * n_qt;
+  const long long pairs = (long long)B * Hq * ((n_qt + 1) / 2);
+  *paired = (causal && n_qt > 1 && pairs >= (long long)device_cus() * wg_per_cu) ? 1 : 0;
+  return *paired ? pairs : single;
+}
+
 // Split-K geometry of the decode kernels: pages of 16 tokens; one wave walks
 // one split of kPagesPerWave pages.
 constexpr int kDecodePage = 16;

@@ -68,6 +68,28 @@ __device__ __forceinline__ void wait_lgkm() {
   CA_DEVICE_ASM("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lgkm0() { wait_lgkm<0>(); }
+// wait_lgkm<n> for an n that is a constant once the caller's loop is unrolled
+// (the switch folds away); lgkmcnt holds at most 15.
+__device__ __forceinline__ void wait_lgkm_n(int n) {
+  switch (n) {
+    case 0: wait_lgkm<0>(); break;
+    case 1: wait_lgkm<1>(); break;
+    case 2: wait_lgkm<2>(); break;
+    case 3: wait_lgkm<3>(); break;
+    case 4: wait_lgkm<4>(); break;
+    case 5: wait_lgkm<5>(); break;
+    case 6: wait_lgkm<6>(); break;
+    case 7: wait_lgkm<7>(); break;
+    case 8: wait_lgkm<8>(); break;
+    case 9: wait_lgkm<9>(); break;
+    case 10: wait_lgkm<10>(); break;
+    case 11: wait_lgkm<11>(); break;
+    case 12: wait_lgkm<12>(); break;
+    case 13: wait_lgkm<13>(); break;
+    case 14: wait_lgkm<14>(); break;
+    default: wait_lgkm<15>(); break;
+  }
+}
 
 // 16 bytes per lane from `src` into LDS at `dst` + 16 * lane (dst is
 // wave-uniform: it is passed in M0). AUX is the cache policy: 0 = default

@@ -34,11 +34,13 @@
 
 namespace ca {
 
+// One query tile (BM rows of head bh): the whole key walk and the output
+// store. Other waves may still read the LDS tiles when a wave returns.
 template <typename Tr, int D, int NW, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
+__device__ CA_INLINE void prefill_fwd_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_work) {
+    int Hkv, float scale_log2, int bh, int qt) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
@@ -56,9 +58,6 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KS];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * VS];
 
-  const int work = xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work);
-  const int bh = work / n_qt;
-  const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
   const int q0 = qt * BM;
@@ -238,6 +237,22 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   }
 }
 
+template <typename Tr, int D, int NW, bool CAUSAL>
+__global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    int Hkv, float scale_log2, int n_qt, int n_work, int paired) {
+  const QTileWork wk = prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, paired);
+  const int n_pass = wk.qt1 < 0 ? 1 : 2;
+#pragma clang loop unroll(disable)
+  for (int pass = 0; pass < n_pass; ++pass) {
+    // the second tile restages the LDS buffers: every wave must be done reading them
+    if (pass) __syncthreads();
+    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, wk.bh,
+                                         pass ? wk.qt1 : wk.qt0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Head dim 128 kernel.
 //
@@ -310,11 +325,21 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 #ifndef CA_PF_AG
 #define CA_PF_AG 0
 #endif
+#ifndef CA_PF_KDEPTH
+#define CA_PF_KDEPTH 1
+#endif
+#ifndef CA_PF_VDEPTH
+#define CA_PF_VDEPTH 2
+#endif
+
+// One query tile (kBM rows of head bh) of the workgroup: the whole key walk
+// and the output store. On return every wave has waited for its own HBM ->
+// LDS loads, but other waves may still read the ring.
 template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
-__global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
+__device__ CA_INLINE void prefill_d128_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_work) {
+    int Hkv, float scale_log2, int bh, int qt) {
   using namespace pf128;
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
@@ -328,9 +353,6 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
 
-  const int work = xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work);
-  const int bh = work / n_qt;
-  const int qt = n_qt - 1 - (work % n_qt);  // longest causal tiles first
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
   const int q0 = qt * kBM;
@@ -438,7 +460,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     const vec2 pk = Tr::pack2(p0, p1);
     pb[nb][kk][2 * j] = pk[0];
     pb[nb][kk][2 * j + 1] = pk[1];
-    psum[nb][j & 1] = Tr::dot2sum(pk, psum[nb][j & 1]);
+    psum[nb][j & 1] += p0 + p1;
   };
   // copy logit pair p (nb = p/16, logits i0 = 2*(p%16), +1) out of the
   // accumulators into sv (masked if MASK; a masked logit becomes the value
@@ -510,20 +532,21 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[mb][nb][r] = 0.f;
       const uint32_t ka = stage(tn) + kofs;
-      u32x4 kr[2][2];
-      kr[0][0] = lds_read_b128<0>(ka);
-      kr[0][1] = lds_read_b128<32 * kRowB>(ka);
+      // K fragments of KD k-steps in flight ahead of the MFMAs (ring of KD + 1)
+      constexpr int KD = CA_PF_KDEPTH;
+      u32x4 kr[KD + 1][2];
+      auto kread = [&](int ks) CA_INLINE {
+        const uint32_t an = ka ^ (32 * ks);
+        kr[ks % (KD + 1)][0] = lds_read_b128<0>(an);
+        kr[ks % (KD + 1)][1] = lds_read_b128<32 * kRowB>(an);
+      };
+#pragma unroll
+      for (int ks = 0; ks < KD; ++ks) kread(ks);
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const int cb = ks & 1;
-        if (ks + 1 < 8) {
-          const uint32_t an = ka ^ (32 * (ks + 1));
-          kr[cb ^ 1][0] = lds_read_b128<0>(an);
-          kr[cb ^ 1][1] = lds_read_b128<32 * kRowB>(an);
-          wait_lgkm<2>();
-        } else {
-          wait_lgkm<0>();
-        }
+        const int cb = ks % (KD + 1);
+        if (ks + KD < 8) kread(ks + KD);
+        wait_lgkm_n(2 * (KD < 7 - ks ? KD : 7 - ks));  // k-step ks landed
         after_wait(kr[cb][0]);
         after_wait(kr[cb][1]);
 #pragma unroll
@@ -557,7 +580,10 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     for (int nb = 0; nb < NH; ++nb) tm[nb][0] = tm[nb][1] = kMaskVal;
     if (PV) {
       const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
-      u32x2 vr[3][2];
+      // V^T fragments of VD k-steps in flight ahead of the MFMAs (ring of VD + 1)
+      constexpr int VD = CA_PF_VDEPTH;
+      u32x2 vr[VD + 1][2];
+      // step st: O^T block ob = st / 4, P^T k-step kk = st % 4
       auto vread = [&](int st, int buf) CA_INLINE {
         const uint32_t x = 64 * (st >> 2);
         switch (st & 3) {
@@ -567,19 +593,13 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
           default: vr[buf][0] = lds_read_tr16<12288>(va1 ^ x); vr[buf][1] = lds_read_tr16<12288>(va2 ^ x); break;
         }
       };
-      vread(0, 0);
-      vread(1, 1);
+#pragma unroll
+      for (int st = 0; st < VD; ++st) vread(st, st);
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
-        const int cb = st % 3;
-        if (st + 2 < 16) {
-          vread(st + 2, (st + 2) % 3);
-          wait_lgkm<4>();
-        } else if (st + 1 < 16) {
-          wait_lgkm<2>();
-        } else {
-          wait_lgkm<0>();
-        }
+        const int cb = st % (VD + 1);
+        if (st + VD < 16) vread(st + VD, (st + VD) % (VD + 1));
+        wait_lgkm_n(2 * (VD < 15 - st ? VD : 15 - st));  // step st landed
         after_wait(vr[cb][0]);
         after_wait(vr[cb][1]);
         const int ob = st >> 2, kk = st & 3;
@@ -608,15 +628,17 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   // accumulators.
   using T_ = std::true_type;
   using F_ = std::false_type;
+  constexpr int DIST = kStages - 1;  // tiles in flight ahead of the one waited for
 #pragma unroll
-  for (int tt = 0; tt < kStages - 1; ++tt) issue(tt);
-  // Iteration t waits until tile t + LEAD is resident (PIPE: A(t) reads
-  // K(t+1)); the slot of tile t-1 is then free for tile t + kStages - 1.
+  for (int tt = 0; tt < DIST; ++tt) issue(tt);
+  // Barrier t: every wave has its loads of tile t + LEAD resident (PIPE: A(t)
+  // reads K(t+1)) and is past its last read of tile t - 1, whose slot then
+  // takes tile t + DIST.
   constexpr int LEAD = PIPE ? 1 : 0;
   auto sync = [&](int t) CA_INLINE {
-    wait_vmcnt<2 * kDmaPerWave * (kStages - 2 - LEAD)>();  // this wave's loads landed
-    __builtin_amdgcn_s_barrier();                          // ... and every wave's
-    issue(t + kStages - 1);
+    wait_vmcnt<2 * kDmaPerWave * (DIST - 1 - LEAD)>();  // this wave's loads landed
+    __builtin_amdgcn_s_barrier();                      // ... and every wave's
+    issue(t + DIST);
   };
   int t = 0;
   if (PIPE) {
@@ -685,6 +707,22 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   }
 }
 
+template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
+__global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    int Hkv, float scale_log2, int n_qt, int n_work, int paired) {
+  const QTileWork wk = prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, paired);
+  const int n_pass = wk.qt1 < 0 ? 1 : 2;
+#pragma clang loop unroll(disable)
+  for (int pass = 0; pass < n_pass; ++pass) {
+    // the second tile refills the LDS ring: every wave must be done reading it
+    if (pass) __builtin_amdgcn_s_barrier();
+    prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(Q, K, V, O, S, Hq, Hkv, scale_log2,
+                                                              wk.bh, pass ? wk.qt1 : wk.qt0);
+  }
+}
+
 #ifndef CA_PF_NH
 #define CA_PF_NH 1
 #endif
@@ -703,10 +741,15 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
   constexpr int BM = CA_PF_BM;
   // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
   constexpr int kLdsPerWg = 160 * 1024 / pf_wg_per_cu(BM, NH);
-  constexpr int STAGES = kLdsPerWg / pf128::kStageB > 4 ? 4 : kLdsPerWg / pf128::kStageB;
+#ifndef CA_PF_MAXSTAGES
+#define CA_PF_MAXSTAGES 4
+#endif
+  constexpr int STAGES = kLdsPerWg / pf128::kStageB > CA_PF_MAXSTAGES ? CA_PF_MAXSTAGES
+                                                                      : kLdsPerWg / pf128::kStageB;
   static_assert(STAGES >= (PIPE ? 3 : 2), "LDS ring too short for the schedule");
   const int n_qt = (S + BM - 1) / BM;
-  const long long grid = (long long)n_qt * B * Hq;
+  int paired = 0;
+  const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, pf_wg_per_cu(BM, NH), &paired);
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const float sl2 = scale * kLog2e;
@@ -715,12 +758,12 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, (int)grid);
+                       n_qt, (int)grid, paired);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, (int)grid);
+                       n_qt, (int)grid, paired);
   }
   return hipGetLastError();
 }
@@ -735,12 +778,14 @@ static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, 
   constexpr int NW = CA_PF_NW;  // waves per workgroup (32 query rows each)
   constexpr int BM = 32 * NW;
   const int n_qt = (S + BM - 1) / BM;
-  const long long grid = (long long)n_qt * B * Hq;
+  int paired = 0;
+  const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, 2, &paired);
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
                      dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, (int)grid);
+                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, (int)grid,
+                     paired);
   return hipGetLastError();
 }
 

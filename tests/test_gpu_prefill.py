@@ -117,3 +117,26 @@ def test_baseline_c2_shapes(dev, cfg):
     if cfg["causal"]:
         # row 0 attends only to key 0: output equals v[..., 0, :] up to bf16 rounding
         assert (out[:, :, 0].float() - v[:, :, 0].float()).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype,d,b,hq,hkv,s", [
+    (torch.bfloat16, 128, 1, 32, 8, 3800),   # 15 query tiles of 256: 7 pairs + a lone middle tile
+    (torch.float16, 128, 2, 32, 32, 4096),   # 16 tiles: 8 pairs
+    (torch.bfloat16, 64, 2, 32, 8, 1900),    # 15 tiles of 128
+])
+def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
+    """Causal grids big enough that each workgroup takes two query tiles of a
+    head (tiles n_qt-1-p and p, for equal work per workgroup on a 256-CU
+    device): sampled heads against the oracle, every head through row 0
+    (which sees key 0 only) and through finiteness."""
+    q, k, v = qkv(b, hq, s, d, dtype, dev, hkv=hkv)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    for (bi, hi) in [(0, 0), (b - 1, hq // 2 + 1), (b - 1, hq - 1)]:
+        kh = hi // (hq // hkv)
+        ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
+                               to_np(v[bi:bi + 1, kh:kh + 1]), is_causal=True)
+        assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_16BIT, name=f"head {bi},{hi}")
+    kv0 = v[:, :, 0].float().repeat_interleave(hq // hkv, dim=1)
+    assert (out[:, :, 0].float() - kv0).abs().max().item() <= 1e-2
