@@ -186,27 +186,40 @@ __device__ __forceinline__ int xcd_remap(int w, int total) {
   return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
 
-// Query tiles of one prefill workgroup (work index after xcd_remap).
-// Unpaired: one tile; the work index runs over (b, h) and, within a head,
-// over its tiles longest causal walk first. Paired (causal launches): tiles
-// n_qt-1-p and p of one (b, h), whose causal key walks add up to the same
-// length for every p, so all workgroups carry equal work and the grid ends
-// without a tail of long workgroups; an odd n_qt leaves the middle tile alone.
+// Query tiles of one prefill workgroup (work index after xcd_remap; n_bh =
+// B * Hq heads, n_qt tiles per head). Unpaired: one tile; the work index runs
+// over heads and, within a head, over its tiles longest causal walk first.
+// Paired (causal launches, n_qt > 1): tiles n_qt-1-p and p of one head, whose
+// causal key walks add up to the same length for every p, so all workgroups
+// carry equal work and the grid ends without a tail of long workgroups; for
+// an odd n_qt the middle tiles of heads 2m and 2m+1 make the last work items.
 struct QTileWork {
-  int bh, qt0, qt1;  // qt1 < 0: no second tile
+  int bh0, qt0, bh1, qt1;  // qt1 < 0: no second tile
 };
-__device__ __forceinline__ QTileWork prefill_work(int work, int n_qt, int paired) {
+__device__ __forceinline__ QTileWork prefill_work(int work, int n_qt, int n_bh, int paired) {
   QTileWork w;
-  if (paired) {
-    const int n_pairs = (n_qt + 1) >> 1;
-    const int p = work % n_pairs;
-    w.bh = work / n_pairs;
-    w.qt0 = n_qt - 1 - p;
-    w.qt1 = (p == w.qt0) ? -1 : p;
-  } else {
-    w.bh = work / n_qt;
+  w.bh1 = 0;
+  w.qt1 = -1;
+  if (!paired) {
+    w.bh0 = work / n_qt;
     w.qt0 = n_qt - 1 - work % n_qt;
-    w.qt1 = -1;
+    return w;
+  }
+  const int half = n_qt >> 1;  // full pairs per head
+  const int n_full = n_bh * half;
+  if (work < n_full) {
+    const int p = work % half;
+    w.bh0 = w.bh1 = work / half;
+    w.qt0 = n_qt - 1 - p;
+    w.qt1 = p;
+  } else {
+    const int m = work - n_full;
+    w.bh0 = 2 * m;
+    w.qt0 = half;
+    if (2 * m + 1 < n_bh) {
+      w.bh1 = 2 * m + 1;
+      w.qt1 = half;
+    }
   }
   return w;
 }

@@ -198,15 +198,16 @@ __device__ CA_INLINE void prefill_f32_qtile(
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_work,
-    int paired) {
-  const QTileWork wk = prefill_work(xcd_remap(blockIdx.x, n_work), n_qt, paired);
+    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh,
+    int n_work, int paired) {
+  const QTileWork wk = prefill_work(xcd_remap(blockIdx.x, n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
 #pragma clang loop unroll(disable)
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile restages the LDS buffers: every wave must be done reading them
     if (pass) __syncthreads();
-    prefill_f32_qtile<D, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, wk.bh, pass ? wk.qt1 : wk.qt0);
+    prefill_f32_qtile<D, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0,
+                                 pass ? wk.qt1 : wk.qt0);
   }
 }
 
@@ -222,7 +223,7 @@ static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void*
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream,
                      (const float*)q, (const float*)k, (const float*)v, (float*)o, S, Hq, Hkv,
-                     scale * kLog2e, n_qt, (int)grid, paired);
+                     scale * kLog2e, n_qt, B * Hq, (int)grid, paired);
   return hipGetLastError();
 }
 

@@ -35,12 +35,14 @@ inline int device_cus() {
 }
 
 // Workgroups of a prefill launch of n_qt query tiles per (b, h). A causal
-// launch pairs query tiles (n_qt-1-p with p, one workgroup each pair) when
-// the paired grid still gives every workgroup slot of the device at least one
-// workgroup; otherwise each workgroup takes one tile.
+// launch pairs query tiles (prefill_work: n_qt-1-p with p of a head, the
+// middle tiles of an odd n_qt two heads at a time) when the paired grid still
+// gives every workgroup slot of the device at least one workgroup; otherwise
+// each workgroup takes one tile.
 inline long long prefill_grid(int B, int Hq, int n_qt, bool causal, int wg_per_cu, int* paired) {
-  const long long single = (long long)B * Hq * n_qt;
-  const long long pairs = (long long)B * Hq * ((n_qt + 1) / 2);
+  const long long n_bh = (long long)B * Hq;
+  const long long single = n_bh * n_qt;
+  const long long pairs = n_bh * (n_qt / 2) + ((n_qt & 1) ? (n_bh + 1) / 2 : 0);
   *paired = (causal && n_qt > 1 && pairs >= (long long)device_cus() * wg_per_cu) ? 1 : 0;
   return *paired ? pairs : single;
 }

@@ -241,30 +241,31 @@ template <typename Tr, int D, int NW, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_work, int paired) {
-  const QTileWork wk = prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, paired);
+    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
+  const QTileWork wk =
+      prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
 #pragma clang loop unroll(disable)
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile restages the LDS buffers: every wave must be done reading them
     if (pass) __syncthreads();
-    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, wk.bh,
-                                         pass ? wk.qt1 : wk.qt0);
+    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2,
+                                         pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Head dim 128 kernel.
 //
-// One workgroup = 256 query rows of one (b, h), split over its waves: NH = 2
-// gives 4 waves of 64 rows (one wave per SIMD), NH = 1 gives 8 waves of 32
-// rows (two per SIMD). A wave owns NH 32-query halves; a K fragment read
+// One workgroup = BM query rows of one (b, h) (BM = 256 or 384), split over
+// its waves: NH = 1 gives BM/32 waves of 32 rows (two or three per SIMD),
+// NH = 2 waves of 64 rows. A wave owns NH 32-query halves; a K fragment read
 // from LDS feeds the S^T MFMAs of all of them and a V^T fragment their O^T
-// MFMAs, so LDS read bytes per FLOP fall as 1/NH. The O^T accumulators
-// (4 x NH blocks of 16 per lane), the S^T accumulators and Q live in AGPRs.
+// MFMAs, so LDS read bytes per FLOP fall as 1/NH. With CA_PF_AG the O^T
+// accumulators, the S^T accumulators and Q live in AGPRs.
 //
-// K/V tiles of 64 keys travel HBM -> LDS with global_load_lds into a ring of
-// kStages tiles (each wave loads 1/NW of every K and V tile; one barrier per
+// K/V tiles of 64 keys travel HBM -> LDS with buffer loads into a ring of
+// kStages tiles (the loaders share every K and V tile; one barrier per
 // tile). Tile layout: 64 rows x 256 bytes, unpadded; the 16-byte chunk c of
 // row r is stored at position c ^ swz(r), swz(r) = 4*(r%4) + (r/4)%4, which
 // makes both read patterns bank-conflict free:
@@ -349,7 +350,10 @@ __device__ CA_INLINE void prefill_d128_qtile(
   constexpr int kStages = STAGES;                // K/V tiles in the LDS ring
   constexpr int kRW = 32 * NH;                   // query rows per wave
   constexpr int kNW = kBM / kRW;                 // waves per workgroup
-  constexpr int kDmaPerWave = kTileB / 1024 / kNW;  // 1 KB loads per wave per tile (K, and V)
+  // waves that issue the HBM -> LDS loads: all of them when they divide the
+  // 16 1-KB loads of a tile evenly, else the first 8
+  constexpr int kLoaders = (kTileB / 1024) % kNW == 0 ? kNW : 8;
+  constexpr int kDmaPerWave = kTileB / 1024 / kLoaders;  // 1 KB loads per loader per tile (K, and V)
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
 
@@ -407,7 +411,9 @@ __device__ CA_INLINE void prefill_d128_qtile(
     const int row = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
     dma_off[i] = row * kRowB + 16 * ((lane & 15) ^ swz(row));
   }
+  const bool loader = kLoaders == kNW || wave < kLoaders;
   auto issue = [&](int tt) CA_INLINE {
+    if (!loader) return;
     unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
     const uint32_t toff = (uint32_t)tt * kTileB;
 #pragma unroll
@@ -636,13 +642,13 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // takes tile t + DIST.
   constexpr int LEAD = PIPE ? 1 : 0;
   auto sync = [&](int t) CA_INLINE {
-    wait_vmcnt<2 * kDmaPerWave * (DIST - 1 - LEAD)>();  // this wave's loads landed
+    if (loader) wait_vmcnt<2 * kDmaPerWave * (DIST - 1 - LEAD)>();  // this wave's loads landed
     __builtin_amdgcn_s_barrier();                      // ... and every wave's
     issue(t + DIST);
   };
   int t = 0;
   if (PIPE) {
-    wait_vmcnt<2 * kDmaPerWave * (kStages - 2)>();  // tile 0 landed (this wave's part)
+    if (loader) wait_vmcnt<2 * kDmaPerWave * (kStages - 2)>();  // tile 0 landed (this wave's part)
     __builtin_amdgcn_s_barrier();                   // ... and every wave's
     if (w_tiles > 0) {
       phase_a(0, T_{}, F_{});             // S^T(0)
@@ -711,15 +717,17 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_work, int paired) {
-  const QTileWork wk = prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, paired);
+    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
+  const QTileWork wk =
+      prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
 #pragma clang loop unroll(disable)
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
     prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(Q, K, V, O, S, Hq, Hkv, scale_log2,
-                                                              wk.bh, pass ? wk.qt1 : wk.qt0);
+                                                              pass ? wk.bh1 : wk.bh0,
+                                                              pass ? wk.qt1 : wk.qt0);
   }
 }
 
@@ -729,21 +737,17 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 #ifndef CA_PF_PIPE
 #define CA_PF_PIPE 0
 #endif
-#ifndef CA_PF_BM
-#define CA_PF_BM 256
-#endif
-template <typename Tr, bool CAUSAL>
-static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o,
-                                      int B, int Hq, int Hkv, int S, float scale,
-                                      hipStream_t stream) {
-  constexpr int NH = CA_PF_NH;
-  constexpr bool PIPE = CA_PF_PIPE;
-  constexpr int BM = CA_PF_BM;
-  // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
-  constexpr int kLdsPerWg = 160 * 1024 / pf_wg_per_cu(BM, NH);
 #ifndef CA_PF_MAXSTAGES
 #define CA_PF_MAXSTAGES 4
 #endif
+template <typename Tr, bool CAUSAL, int BM>
+static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const void* v, void* o,
+                                         int B, int Hq, int Hkv, int S, float scale,
+                                         hipStream_t stream) {
+  constexpr int NH = CA_PF_NH;
+  constexpr bool PIPE = CA_PF_PIPE;
+  // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
+  constexpr int kLdsPerWg = 160 * 1024 / pf_wg_per_cu(BM, NH);
   constexpr int STAGES = kLdsPerWg / pf128::kStageB > CA_PF_MAXSTAGES ? CA_PF_MAXSTAGES
                                                                       : kLdsPerWg / pf128::kStageB;
   static_assert(STAGES >= (PIPE ? 3 : 2), "LDS ring too short for the schedule");
@@ -758,14 +762,36 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, (int)grid, paired);
+                       n_qt, B * Hq, (int)grid, paired);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, (int)grid, paired);
+                       n_qt, B * Hq, (int)grid, paired);
   }
   return hipGetLastError();
+}
+
+// Workgroup height: 384 query rows (12 waves, three per SIMD, which hides
+// more of each wave's LDS and MFMA latency: +4-6 % at S = 3072) when 384-row
+// tiles cover S exactly, or for a non-causal launch with at most ~5 % padding
+// rows, and the grid still gives every CU two workgroups; 256 rows (8 waves)
+// otherwise. A partial last tile costs a causal launch more (its idle waves
+// walk the longest key range): at S = 4096 causal 384 rows measure 3 % below
+// 256.
+template <typename Tr, bool CAUSAL>
+static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o,
+                                      int B, int Hq, int Hkv, int S, float scale,
+                                      hipStream_t stream) {
+#ifdef CA_PF_BM
+  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+#else
+  const long long n384 = (S + 383) / 384;
+  const bool fits = (S % 384 == 0) || (!CAUSAL && n384 * 384 * 20 <= (long long)S * 21);
+  const bool tall = fits && (long long)B * Hq * n384 >= 2LL * device_cus();
+  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
+              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+#endif
 }
 
 template <typename Tr, int D, bool CAUSAL>
@@ -784,8 +810,8 @@ static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, 
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
                      dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, (int)grid,
-                     paired);
+                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, B * Hq,
+                     (int)grid, paired);
   return hipGetLastError();
 }
 

@@ -121,11 +121,12 @@ def test_paged_f32_nan_tail_does_not_leak(dev):
 @pytest.mark.parametrize("head_dim", [64, 128])
 def test_causal_paired_query_tiles_f32(dev, head_dim):
     """A causal grid big enough that each workgroup takes two query tiles of a
-    head (n_qt-1-p and p): 15 tiles of 128 rows, sampled heads."""
-    q, k, v = qkv(2, 32, 1900, head_dim, F32, dev, hkv=8)
+    head (n_qt-1-p and p; the middle tiles of two heads): 15 tiles of 128
+    rows, sampled heads."""
+    q, k, v = qkv(4, 32, 1900, head_dim, F32, dev, hkv=8)
     out = cuda_llm.flash_attention(q, k, v, is_causal=True)
     torch.cuda.synchronize()
-    for (bi, hi) in [(0, 0), (1, 17), (1, 31)]:
+    for (bi, hi) in [(0, 0), (3, 17), (3, 31)]:
         kh = hi // 4
         ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
                                to_np(v[bi:bi + 1, kh:kh + 1]), is_causal=True, dtype=np.float64)

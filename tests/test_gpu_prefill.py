@@ -120,15 +120,20 @@ def test_baseline_c2_shapes(dev, cfg):
 
 
 @pytest.mark.parametrize("dtype,d,b,hq,hkv,s", [
-    (torch.bfloat16, 128, 1, 32, 8, 3800),   # 15 query tiles of 256: 7 pairs + a lone middle tile
-    (torch.float16, 128, 2, 32, 32, 4096),   # 16 tiles: 8 pairs
-    (torch.bfloat16, 64, 2, 32, 8, 1900),    # 15 tiles of 128
+    (torch.bfloat16, 128, 2, 32, 8, 3072),   # 8 query tiles of 384 rows: 4 pairs per head
+    (torch.float16, 128, 2, 32, 32, 3456),   # 9 tiles of 384: 4 pairs + middle tiles of 2 heads
+    (torch.bfloat16, 128, 2, 32, 8, 3800),   # 15 tiles of 256 (ragged): 7 pairs + middle tiles
+    (torch.float16, 128, 2, 32, 32, 4096),   # 16 tiles of 256: 8 pairs
+    (torch.bfloat16, 128, 7, 7, 1, 2800),    # 11 tiles of 256, 49 heads: one lone middle tile
+    (torch.bfloat16, 64, 4, 32, 8, 1900),    # 15 tiles of 128
 ])
 def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
-    """Causal grids big enough that each workgroup takes two query tiles of a
-    head (tiles n_qt-1-p and p, for equal work per workgroup on a 256-CU
-    device): sampled heads against the oracle, every head through row 0
-    (which sees key 0 only) and through finiteness."""
+    """Causal grids big enough that each workgroup takes two query tiles
+    (tiles n_qt-1-p and p of a head; for an odd n_qt the middle tiles of two
+    heads), for equal work per workgroup on a 256-CU device: sampled heads
+    (including the last head, whose middle tile may be alone) against the
+    oracle, every head through row 0 (which sees key 0 only) and through
+    finiteness."""
     q, k, v = qkv(b, hq, s, d, dtype, dev, hkv=hkv)
     out = cuda_llm.flash_attention(q, k, v, is_causal=True)
     torch.cuda.synchronize()
@@ -140,3 +145,20 @@ def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
         assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_16BIT, name=f"head {bi},{hi}")
     kv0 = v[:, :, 0].float().repeat_interleave(hq // hkv, dim=1)
     assert (out[:, :, 0].float() - kv0).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("s", [1536, 4096])
+def test_tall_workgroups_noncausal(dev, s):
+    """Non-causal grids that take 384-row workgroups (12 waves, three per
+    SIMD): S = 1536 (4 full tiles) and S = 4096 (11 tiles, the last one
+    partial)."""
+    b, hq, hkv = (4, 32, 8) if s == 1536 else (2, 32, 8)
+    q, k, v = qkv(b, hq, s, 128, torch.bfloat16, dev, hkv=hkv)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=False)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    for (bi, hi) in [(0, 0), (b - 1, 13), (b - 1, hq - 1)]:
+        kh = hi // (hq // hkv)
+        ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
+                               to_np(v[bi:bi + 1, kh:kh + 1]))
+        assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_16BIT, name=f"head {bi},{hi}")
