@@ -326,6 +326,9 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 #ifndef CA_PF_AG
 #define CA_PF_AG 0
 #endif
+#ifndef CA_PF_PRIO
+#define CA_PF_PRIO 1
+#endif
 #ifndef CA_PF_KDEPTH
 #define CA_PF_KDEPTH 1
 #endif
@@ -340,7 +343,7 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __device__ CA_INLINE void prefill_d128_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int bh, int qt) {
+    int Hkv, float scale_log2, int bh, int qt, int q_shift) {
   using namespace pf128;
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
@@ -359,7 +362,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
 
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
-  const int q0 = qt * kBM;
+  const int q0 = qt * kBM - q_shift;  // tile 0 may start before row 0 (rows < 0 are padding)
   const uint16_t* Qp = Q + (size_t)(b * Hq + h) * S * D;
   uint16_t* Op = O + (size_t)(b * Hq + h) * S * D;
   const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
@@ -379,7 +382,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   for (int nb = 0; nb < NH; ++nb) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-      if (myq[nb] < S) {
+      if (myq[nb] >= 0 && myq[nb] < S) {
         qv[nb][ks] = *(const vec8*)(Qp + (size_t)myq[nb] * D + 16 * ks + 8 * hl);
       } else {
 #pragma unroll
@@ -395,7 +398,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   const int n_tiles = (kv_end + kBN - 1) / kBN;
   // tiles this wave computes on (it still loads and synchronises for all)
   const int w_end = CAUSAL ? min(kv_end, qw0 + kRW) : kv_end;
-  const int w_tiles = (qw0 < S) ? (w_end + kBN - 1) / kBN : 0;
+  const int w_tiles = (qw0 + kRW > 0 && qw0 < S) ? (w_end + kBN - 1) / kBN : 0;
 
   // HBM -> LDS with buffer loads over the keys this workgroup needs
   // ([0, kv_end) of the (b, kv head) slice; rows past it read as zero, so
@@ -537,6 +540,9 @@ __device__ CA_INLINE void prefill_d128_qtile(
         for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[mb][nb][r] = 0.f;
+      // MFMA blocks run at raised wave priority, so a wave's MFMAs win issue
+      // over the partner wave's softmax VALU (+1-2.5 % measured)
+      if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(1);
       const uint32_t ka = stage(tn) + kofs;
       // K fragments of KD k-steps in flight ahead of the MFMAs (ring of KD + 1)
       constexpr int KD = CA_PF_KDEPTH;
@@ -566,6 +572,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(0);
     } else if (EXP) {
 #pragma unroll
       for (int p = 0; p < 16 * NH; ++p) exp_pair(p);
@@ -585,6 +592,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb) tm[nb][0] = tm[nb][1] = kMaskVal;
     if (PV) {
+      if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(1);
       const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
       // V^T fragments of VD k-steps in flight ahead of the MFMAs (ring of VD + 1)
       constexpr int VD = CA_PF_VDEPTH;
@@ -620,6 +628,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(0);
     } else if (NEXT) {
 #pragma unroll
       for (int p = 0; p < 16 * NH; ++p) take_pair(p, k0n, mask_tag);
@@ -696,7 +705,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   for (int nb = 0; nb < NH; ++nb) {
     const float l_tot = pair32_sum(l_run[nb]);
     const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
-    if (myq[nb] < S) {
+    if (myq[nb] >= 0 && myq[nb] < S) {
 #pragma unroll
       for (int ob = 0; ob < 4; ++ob) {
 #pragma unroll
@@ -717,7 +726,7 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
+    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
@@ -725,9 +734,8 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
-    prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(Q, K, V, O, S, Hq, Hkv, scale_log2,
-                                                              pass ? wk.bh1 : wk.bh0,
-                                                              pass ? wk.qt1 : wk.qt0);
+    prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(
+        Q, K, V, O, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift);
   }
 }
 
@@ -752,6 +760,10 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
                                                                       : kLdsPerWg / pf128::kStageB;
   static_assert(STAGES >= (PIPE ? 3 : 2), "LDS ring too short for the schedule");
   const int n_qt = (S + BM - 1) / BM;
+  // the padding rows of a ragged S go before row 0, in whole key tiles (so a
+  // wave's causal diagonal still lies in one key tile): the partial tile is
+  // the first one, whose causal key walk is the shortest
+  const int q_shift = (n_qt * BM - S) / pf128::kBN * pf128::kBN;
   int paired = 0;
   const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, pf_wg_per_cu(BM, NH), &paired);
   if (grid == 0) return hipSuccess;
@@ -762,23 +774,20 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, B * Hq, (int)grid, paired);
+                       n_qt, B * Hq, (int)grid, paired, q_shift);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
-                       n_qt, B * Hq, (int)grid, paired);
+                       n_qt, B * Hq, (int)grid, paired, q_shift);
   }
   return hipGetLastError();
 }
 
 // Workgroup height: 384 query rows (12 waves, three per SIMD, which hides
 // more of each wave's LDS and MFMA latency: +4-6 % at S = 3072) when 384-row
-// tiles cover S exactly, or for a non-causal launch with at most ~5 % padding
-// rows, and the grid still gives every CU two workgroups; 256 rows (8 waves)
-// otherwise. A partial last tile costs a causal launch more (its idle waves
-// walk the longest key range): at S = 4096 causal 384 rows measure 3 % below
-// 256.
+// tiles cover S with at most ~5 % padding rows and the grid still gives every
+// CU two workgroups; 256 rows (8 waves) otherwise.
 template <typename Tr, bool CAUSAL>
 static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o,
                                       int B, int Hq, int Hkv, int S, float scale,
@@ -787,7 +796,7 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
   return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
 #else
   const long long n384 = (S + 383) / 384;
-  const bool fits = (S % 384 == 0) || (!CAUSAL && n384 * 384 * 20 <= (long long)S * 21);
+  const bool fits = n384 * 384 * 20 <= (long long)S * 21;
   const bool tall = fits && (long long)B * Hq * n384 >= 2LL * device_cus();
   return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
               : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
