@@ -443,7 +443,7 @@ void decode_split_kernel(
 // V pages linear [D][16].
 // ---------------------------------------------------------------------------
 #ifndef CA_DEC_SPLIT_OUTER
-#define CA_DEC_SPLIT_OUTER 1
+#define CA_DEC_SPLIT_OUTER 2
 #endif
 // Cache policy of the page loads: "nt" (every byte is read once per launch,
 // so it is streamed rather than retained).
@@ -497,7 +497,14 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 
   const int lane = threadIdx.x;
   int w = blockIdx.x;
-#if CA_DEC_SPLIT_OUTER
+#if CA_DEC_SPLIT_OUTER == 2
+  // split index outermost, counted from each sequence's end: the waves of
+  // splits before a sequence's start (none exist) come first and retire at
+  // once, and every sequence's last (partial) split is in the final group
+  const int per_split = (int)(gridDim.x / max_splits);
+  const int from_end = max_splits - 1 - w / per_split;
+  w %= per_split;
+#elif CA_DEC_SPLIT_OUTER
   // split index outermost: every sequence's first splits come first and the
   // waves of splits past a sequence's end gather at the tail of the grid
   const int per_split = (int)(gridDim.x / max_splits);
@@ -517,7 +524,12 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
   const int n_splits = max(1, (n_pages + kPagesPerWave - 1) / kPagesPerWave);
+#if CA_DEC_SPLIT_OUTER == 2
+  const int split = n_splits - 1 - from_end;
+  if (split < 0) return;
+#else
   if (split >= n_splits) return;
+#endif
 
   const int l16 = lane & 15, grp = lane >> 4;
   const int p_begin = split * kPagesPerWave;
