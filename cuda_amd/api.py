@@ -13,7 +13,8 @@ Differences from the reference, all widening what is accepted:
     (tests/test_kernels_misc.py:42-64), and also accept float8_e4m3fn tensors;
   * a sequence with context length 0 yields zeros instead of an unwritten row.
 float32 q/k/v are accepted where the reference instantiates float (prefill,
-flash_decode, paged decode). Not supported: autograd through flash_attention.
+flash_decode, paged decode). ``flash_attention`` is differentiable (README.md:
+66-71) through ``flash_attention_backward`` (fp16 / bf16; float32 raises).
 """
 import ctypes
 import math
@@ -24,6 +25,7 @@ from . import _lib
 
 __all__ = [
     "flash_attention", "flash_attention_forward", "flash_attention_v3_hopper",
+    "flash_attention_forward_lse", "flash_attention_backward",
     "fused_gqa_forward", "flash_decode", "async_flash_decode", "paged_attention",
     "paged_attention_forward", "fp8_paged_attention", "fp8_paged_attention_forward",
     "fused_microscaled_attention", "mx_scales_to_e8m0",
@@ -72,12 +74,7 @@ def _workspace(nbytes, device):
 # ---------------------------------------------------------------------------
 # Prefill
 # ---------------------------------------------------------------------------
-def flash_attention_forward(q, k, v, is_causal=False, softmax_scale=None):
-    """O = softmax(Q K^T * scale [+ causal]) V.
-
-    q: [B, Hq, S, D]; k, v: [B, Hkv, S, D] (Hkv == Hq in the reference; any
-    divisor of Hq here). Reference: fused_softmax_binding.cpp:49-103.
-    """
+def _prefill_checks(q, k, v):
     _check(q.is_cuda and k.is_cuda and v.is_cuda, "Inputs must be on CUDA")
     _check(q.is_contiguous() and k.is_contiguous() and v.is_contiguous(),
            "Inputs must be contiguous")
@@ -90,6 +87,16 @@ def flash_attention_forward(q, k, v, is_causal=False, softmax_scale=None):
            "(or K/V with a number of heads dividing Q's)")
     _check(q.dtype == k.dtype == v.dtype, "Q, K, V must have the same dtype")
     _check(d in (64, 128), "Only head_dim 64 and 128 are currently supported")
+
+
+def flash_attention_forward(q, k, v, is_causal=False, softmax_scale=None):
+    """O = softmax(Q K^T * scale [+ causal]) V.
+
+    q: [B, Hq, S, D]; k, v: [B, Hkv, S, D] (Hkv == Hq in the reference; any
+    divisor of Hq here). Reference: fused_softmax_binding.cpp:49-103.
+    """
+    _prefill_checks(q, k, v)
+    b, hq, s, d = q.shape
     dt = _dtype_code(q, "FlashAttention")
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
     out = torch.empty_like(q)
@@ -98,7 +105,86 @@ def flash_attention_forward(q, k, v, is_causal=False, softmax_scale=None):
     return out
 
 
-flash_attention = flash_attention_forward
+def flash_attention_forward_lse(q, k, v, is_causal=False, softmax_scale=None):
+    """(O, LSE): the prefill forward plus the natural-log logsumexp of every
+    row of scaled, masked scores, LSE [B, Hq, S] float32 (-inf for a row with
+    no visible key). No reference counterpart: the reference's forward returns
+    O only; its backward takes this LSE (fused_softmax_binding.cpp:367-376),
+    which its tests build with ref_lse (tests/_utils.py:56-64)."""
+    _prefill_checks(q, k, v)
+    b, hq, s, d = q.shape
+    dt = _dtype_code(q, "FlashAttention")
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    out = torch.empty_like(q)
+    lse = torch.empty(b, hq, s, dtype=torch.float32, device=q.device)
+    _lib.call("ca_flash_attention_fwd_lse", dt, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+              b, hq, k.shape[1], s, d, _scale(softmax_scale, d), int(bool(is_causal)), _stream())
+    return out, lse
+
+
+def flash_attention_backward(dout, q, k, v, out, lse, is_causal=False, softmax_scale=None):
+    """[dq, dk, dv] of O = softmax(Q K^T * scale [+ causal]) V, given the
+    forward output ``out``, its gradient ``dout`` and the forward's
+    natural-log row logsumexp ``lse`` [B, Hq, S] (fused_softmax_binding.cpp:
+    367-433; math flash_attention_bwd_kernel.cuh:9-19). q, out, dout: [B, Hq,
+    S, D]; k, v: [B, Hkv, S, D] (GQA: dk, dv sum over the q heads of a kv
+    head). fp16 / bf16; lse is converted to contiguous float32 as the
+    reference does."""
+    _check(dout.is_cuda and q.is_cuda and k.is_cuda and v.is_cuda and out.is_cuda,
+           "Inputs must be on CUDA")
+    _check(lse.is_cuda, "LSE tensor must be on CUDA")
+    _check(q.dim() == 4, "Expected 4D tensor: [batch, num_heads, seq_len, head_dim]")
+    b, hq, s, d = q.shape
+    _check(k.dim() == 4 and v.dim() == 4 and k.shape == v.shape and k.shape[0] == b
+           and k.shape[2] == s and k.shape[3] == d and hq % k.shape[1] == 0,
+           "K, V must be [batch, num_kv_heads, seq_len, head_dim] with num_kv_heads dividing "
+           "Q's heads")
+    _check(dout.shape == q.shape and out.shape == q.shape, "dout and out must have Q's shape")
+    _check(lse.shape == (b, hq, s), "lse must be [batch, num_heads, seq_len]")
+    _check(q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype,
+           "q, k, v, out and dout must have the same dtype")
+    _check(d in (64, 128), "Only head_dim 64 and 128 are currently supported")
+    _check(q.dtype in (torch.float16, torch.bfloat16),
+           "Unsupported scalar type for FlashAttention Backward. Supported: Float16, BFloat16.")
+    dt = _DT[q.dtype]
+    q, k, v, out, dout = (_aligned(t.contiguous()) for t in (q, k, v, out, dout))
+    lse = lse.to(torch.float32).contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws, nbytes = _workspace(int(_lib.load().ca_flash_attention_bwd_workspace_bytes(b, hq, s)),
+                            q.device)
+    _lib.call("ca_flash_attention_bwd", dt, _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout),
+              _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv), b, hq, k.shape[1], s, d,
+              _scale(softmax_scale, d), int(bool(is_causal)), _ptr(ws), nbytes, _stream())
+    return [dq, dk, dv]
+
+
+class _FlashAttention(torch.autograd.Function):
+    """Autograd node: forward with LSE, backward through flash_attention_backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, is_causal, softmax_scale):
+        out, lse = flash_attention_forward_lse(q, k, v, is_causal, softmax_scale)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.is_causal, ctx.softmax_scale = is_causal, softmax_scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(dout.contiguous(), q, k, v, out, lse,
+                                              ctx.is_causal, ctx.softmax_scale)
+        return dq, dk, dv, None, None
+
+
+def flash_attention(q, k, v, is_causal=False, softmax_scale=None):
+    """README's ``cllm.flash_attention`` (README.md:66-71): the prefill forward,
+    differentiable with respect to q, k and v when any of them requires grad
+    (then the forward also keeps its LSE for the backward kernels)."""
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v)):
+        return _FlashAttention.apply(q, k, v, is_causal, softmax_scale)
+    return flash_attention_forward(q, k, v, is_causal=is_causal, softmax_scale=softmax_scale)
+
+
 flash_attention_v3_hopper = flash_attention_forward
 
 

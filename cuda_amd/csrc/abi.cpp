@@ -79,11 +79,10 @@ size_t ca_decode_workspace_bytes(int num_seqs, int num_q_heads, int head_dim, in
   return ca::decode_workspace_bytes(num_seqs, num_q_heads, head_dim, max_tokens);
 }
 
-ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, const void* v,
-                                 void* o, int batch, int num_q_heads, int num_kv_heads,
-                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
-                                 void* stream) {
-  const char* what = "flash_attention";
+static ca_status prefill_entry(const char* what, ca_dtype dtype, const void* q, const void* k,
+                               const void* v, void* o, float* lse, int batch, int num_q_heads,
+                               int num_kv_heads, int seq_len, int head_dim, float softmax_scale,
+                               int is_causal, void* stream) {
   ca_status st;
   if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
@@ -95,9 +94,65 @@ ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, c
     return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
   if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
     return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
-  return from_hip(ca::launch_prefill((int)dtype, q, k, v, o, batch, num_q_heads, num_kv_heads,
-                                     seq_len, head_dim, softmax_scale, is_causal != 0,
-                                     (hipStream_t)stream),
+  return from_hip(ca::launch_prefill((int)dtype, q, k, v, o, lse, batch, num_q_heads,
+                                     num_kv_heads, seq_len, head_dim, softmax_scale,
+                                     is_causal != 0, (hipStream_t)stream),
+                  what);
+}
+
+ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                 void* o, int batch, int num_q_heads, int num_kv_heads,
+                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
+                                 void* stream) {
+  return prefill_entry("flash_attention", dtype, q, k, v, o, nullptr, batch, num_q_heads,
+                       num_kv_heads, seq_len, head_dim, softmax_scale, is_causal, stream);
+}
+
+ca_status ca_flash_attention_fwd_lse(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                     void* o, float* lse, int batch, int num_q_heads,
+                                     int num_kv_heads, int seq_len, int head_dim,
+                                     float softmax_scale, int is_causal, void* stream) {
+  const char* what = "flash_attention (with lse)";
+  if (!lse && batch > 0 && seq_len > 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: null lse pointer", what);
+  return prefill_entry(what, dtype, q, k, v, o, lse, batch, num_q_heads, num_kv_heads, seq_len,
+                       head_dim, softmax_scale, is_causal, stream);
+}
+
+size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int seq_len) {
+  if (batch <= 0 || num_q_heads <= 0 || seq_len <= 0) return 0;
+  return ca::bwd_workspace_bytes(batch, num_q_heads, seq_len);
+}
+
+ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                 const void* o, const void* dout, const float* lse, void* dq,
+                                 void* dk, void* dv, int batch, int num_q_heads, int num_kv_heads,
+                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "flash_attention_backward";
+  ca_status st;
+  if (dtype == CA_F32)
+    return fail(CA_UNSUPPORTED, "%s: float32 is not supported (use bf16/fp16)", what);
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (batch < 0 || seq_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0 || seq_len == 0) return CA_OK;
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
+  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  const size_t need = ca::bwd_workspace_bytes(batch, num_q_heads, seq_len);
+  if (workspace_bytes < need || !workspace)
+    return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
+                workspace_bytes);
+  return from_hip(ca::launch_flash_bwd((int)dtype, q, k, v, o, dout, lse, dq, dk, dv, batch,
+                                       num_q_heads, num_kv_heads, seq_len, head_dim,
+                                       softmax_scale, is_causal != 0, workspace,
+                                       (hipStream_t)stream),
                   what);
 }
 

@@ -1,0 +1,488 @@
+// Flash-attention backward for gfx950 (bf16/fp16 MFMA, fp32 accumulation).
+//
+// Computes dQ, dK, dV of O = softmax(Q K^T * scale [+ causal mask]) V from Q,
+// K, V, O, dO and the forward's natural-log row logsumexp LSE: the contract
+// of dispatch_flash_attention_v2_backward (kernels_api.h:65-69), math of
+// flash_attention_bwd_kernel.cuh:9-19 and 96-214:
+//   D_i = rowsum(dO * O),  P = exp(S * scale - LSE_i),  dP = dO V^T,
+//   dS = P (dP - D_i) * scale,  dQ = dS K,  dK = dS^T Q,  dV = P^T dO,
+// with P = dS = 0 for masked entries (key > query when causal) and for keys
+// or queries past S. GQA (Hkv < Hq, kv head = h / (Hq / Hkv)): dK and dV of a
+// kv head are summed over its q heads.
+//
+// Three launches and no atomics, so the result does not depend on timing:
+//   bwd_rowdot_kernel  D = rowsum(dO * O) into a [B, Hq, S] fp32 workspace;
+//   bwd_dq_kernel      query-outer: 4 waves x 32 queries of one (b, h); key
+//                      tiles of 64 staged in LDS; per tile S^T = K Q^T,
+//                      dP^T = V dO^T, dS^T, dQ^T += K^T dS^T;
+//   bwd_dkv_kernel     key-outer: 4 waves x 32 keys of one (b, kv head); query
+//                      tiles of 64 (Q, dO, LSE, D) staged in LDS, for every q
+//                      head of the kv head; per tile S = Q K^T, dP = dO V^T,
+//                      dS, dV^T += dO^T P, dK^T += Q^T dS.
+// Operand layouts are those of the forward kernels (prefill.hip): the 32-row
+// A operand of the first product of a tile reads its rows in the order
+// rho(i) = i with bits 2 and 3 swapped, which puts row 16 (r/8) + 8 h + r%8
+// into accumulator register r of lane half h. Those 8-register runs are
+// exactly the 16-bit B operand (dV^T, dK^T, forward PV) or A operand (dQ) of
+// the next product's k-steps, so P and dS go from accumulators to operands
+// without leaving registers. The transposed operands (K^T, Q^T, dO^T) come
+// from row-major LDS tiles through ds_read_b64_tr_b16.
+#include "common.h"
+#include "launch.h"
+
+namespace ca {
+namespace {
+
+constexpr int kBwdWaves = 4;    // waves per workgroup (32 rows each)
+constexpr int kBwdTile = 64;    // keys (dq kernel) or queries (dkv kernel) per LDS tile
+
+__device__ __forceinline__ int rho32(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// D[row] = sum_d dO[row][d] * O[row][d] over rows = B * Hq * S (flash_attention_
+// bwd_kernel.cuh:96-108). D / 8 lanes per row, 8 elements each.
+template <typename Tr, int D>
+__global__ __launch_bounds__(256) void bwd_rowdot_kernel(const uint16_t* __restrict__ O,
+                                                         const uint16_t* __restrict__ dO,
+                                                         float* __restrict__ Dd, long long rows) {
+  using vec8 = typename Tr::vec8;
+  constexpr int L = D / 8;
+  const long long t = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long row = t / L;
+  const int c = (int)(t % L);
+  float acc = 0.f;
+  if (row < rows) {
+    const vec8 o = *(const vec8*)(O + row * D + 8 * c);
+    const vec8 g = *(const vec8*)(dO + row * D + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)o[e], (float)g[e], acc);
+  }
+#pragma unroll
+  for (int m = L / 2; m >= 1; m >>= 1) acc += __shfl_xor(acc, m, 64);
+  if (row < rows && c == 0) Dd[row] = acc;
+}
+
+// Store the transposed accumulators acc[ob] (rows d = 32 ob + 8 a + 4 h + 0..3,
+// column = this lane's row index l32) as row `row` of a [.., D] 16-bit tensor.
+template <typename Tr, int NOB>
+__device__ __forceinline__ void store_rowT(uint16_t* dst_row, const f32x16 (&acc)[NOB], int hl) {
+  using vec4 = typename Tr::vec4;
+  using vec2 = typename Tr::vec2;
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int d = 32 * ob + 8 * a + 4 * hl;
+      const vec2 lo = Tr::pack2(acc[ob][4 * a], acc[ob][4 * a + 1]);
+      const vec2 hi = Tr::pack2(acc[ob][4 * a + 2], acc[ob][4 * a + 3]);
+      vec4 w;
+      w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
+      *(vec4*)(dst_row + d) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: one workgroup = 128 queries of one (b, h); the key walk of the forward.
+// ---------------------------------------------------------------------------
+template <typename Tr, int D, bool CAUSAL>
+__global__ __launch_bounds__(kBwdWaves * 64) void bwd_dq_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
+    const float* __restrict__ LSE, const float* __restrict__ Dd, uint16_t* __restrict__ dQ,
+    int S, int Hq, int Hkv, float scale, int n_qt, int n_work) {
+  using vec8 = typename Tr::vec8;
+  using vec4 = typename Tr::vec4;
+  using vec2 = typename Tr::vec2;
+  constexpr int BM = 32 * kBwdWaves;
+  constexpr int BN = kBwdTile;
+  constexpr int KS = D + 8;   // row stride (elements): permuted-row b128 reads hit distinct banks
+  constexpr int NKS = D / 16;
+  constexpr int NOB = D / 32;
+  constexpr int CHUNKS = D / 8;
+  constexpr int ROWS_PER_PASS = kBwdWaves * 64 / CHUNKS;
+  constexpr int PASSES = BN / ROWS_PER_PASS;
+  static_assert(PASSES * ROWS_PER_PASS == BN, "tile staging must cover the tile");
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * KS];
+
+  const int work = xcd_remap(blockIdx.x, n_work);
+  const int bh = work / n_qt;
+  const int qt = n_qt - 1 - (work % n_qt);  // longest causal walks first
+  const int b = bh / Hq, h = bh % Hq;
+  const int hk = h / (Hq / Hkv);
+  const int q0 = qt * BM;
+  const size_t qoff = (size_t)(b * Hq + h) * S;
+  const uint16_t* Qp = Q + qoff * D;
+  const uint16_t* dOp = dO + qoff * D;
+  const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
+  const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int qw0 = q0 + 32 * wave;
+  const int myq = qw0 + l32;
+  const bool qvalid = myq < S;
+  const float c2 = scale * kLog2e;
+  // P = 2^(s * c2 - lse2); a query past S gets lse2 = +inf, so P = 0
+  const float lse2 = qvalid ? LSE[qoff + myq] * kLog2e : -kNegInf;
+  const float dd = qvalid ? Dd[qoff + myq] : 0.f;
+
+  vec8 qv[NKS], gv[NKS];  // Q and dO as B operands (column = this lane's query)
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (qvalid) {
+      qv[ks] = *(const vec8*)(Qp + (size_t)myq * D + 16 * ks + 8 * hl);
+      gv[ks] = *(const vec8*)(dOp + (size_t)myq * D + 16 * ks + 8 * hl);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qv[ks][e] = 0; gv[ks][e] = 0; }
+    }
+  }
+
+  const int kv_end = CAUSAL ? min(S, q0 + BM) : S;
+  const int n_tiles = (kv_end + BN - 1) / BN;
+  const int st_row = tid / CHUNKS, st_col = (tid % CHUNKS) * 8;
+  u32x4 kreg[PASSES], vreg[PASSES];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = t * BN + st_row + p * ROWS_PER_PASS;
+      if (row < S) {
+        kreg[p] = *(const u32x4*)(Kp + (size_t)row * D + st_col);
+        vreg[p] = *(const u32x4*)(Vp + (size_t)row * D + st_col);
+      } else {
+        kreg[p] = u32x4{0, 0, 0, 0};
+        vreg[p] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = st_row + p * ROWS_PER_PASS;
+      *(u32x4*)(&Ks[buf][r * KS + st_col]) = kreg[p];
+      *(u32x4*)(&Vs[buf][r * KS + st_col]) = vreg[p];
+    }
+  };
+
+  f32x16 acc[NOB];  // dQ^T
+#pragma unroll
+  for (int i = 0; i < NOB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.f;
+
+  const int krow = rho32(l32);
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (s16 & 3);
+
+  if (n_tiles > 0) gload(0);
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    lstore(buf);
+    __syncthreads();
+    if (t + 1 < n_tiles) gload(t + 1);
+    const int k0 = t * BN;
+    if (CAUSAL && k0 > qw0 + 31) continue;  // tile entirely above this wave's rows
+    const uint16_t* Kb = Ks[buf];
+    const uint16_t* Vb = Vs[buf];
+
+    // S^T = K Q^T and dP^T = V dO^T; register r of half hl <-> key
+    // k0 + 32 mb + 16 (r/8) + 8 hl + r%8, column = this lane's query
+    f32x16 s[2], dp[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { s[mb][r] = 0.f; dp[mb][r] = 0.f; }
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const int off = (32 * mb + krow) * KS + 16 * ks + 8 * hl;
+        s[mb] = Tr::mfma32(*(const vec8*)(Kb + off), qv[ks], s[mb]);
+        dp[mb] = Tr::mfma32(*(const vec8*)(Vb + off), gv[ks], dp[mb]);
+      }
+    }
+    const bool need_mask = CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S);
+    vec8 pb[4];  // dS^T as the B operand of dQ^T += K^T dS^T, k-step kk
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float ds[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int i = 8 * kk + 2 * j + e;  // register index over both blocks: mb = i / 16
+          const int mb = i >> 4, r = i & 15;
+          float p = fast_exp2(__builtin_fmaf(s[mb][r], c2, -lse2));
+          if (need_mask) {
+            const int key = k0 + 32 * mb + 16 * (r >> 3) + 8 * hl + (r & 7);
+            if (key >= S || (CAUSAL && key > myq)) p = 0.f;
+          }
+          ds[e] = p * (dp[mb][r] - dd) * scale;
+        }
+        const vec2 pk = Tr::pack2(ds[0], ds[1]);
+        pb[kk][2 * j] = pk[0];
+        pb[kk][2 * j + 1] = pk[1];
+      }
+    }
+    // dQ^T[d x q] += K^T[d x keys] dS^T[keys x q]
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint16_t* src = Kb + (16 * kk + tr_row) * KS + 32 * ob + tr_col;
+        const vec4 lo = Tr::tr_read((const CA_LDS void*)src);
+        const vec4 hi = Tr::tr_read((const CA_LDS void*)(src + 4 * KS));
+        acc[ob] = Tr::mfma32(cat4<vec8, vec4>(lo, hi), pb[kk], acc[ob]);
+      }
+    }
+  }
+  if (qvalid) store_rowT<Tr, NOB>(dQ + (qoff + myq) * D, acc, hl);
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV: one workgroup = 128 keys of one (b, kv head); query tiles of every
+// q head of the kv head.
+// ---------------------------------------------------------------------------
+template <typename Tr, int D, bool CAUSAL>
+__global__ __launch_bounds__(kBwdWaves * 64) void bwd_dkv_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dO,
+    const float* __restrict__ LSE, const float* __restrict__ Dd, uint16_t* __restrict__ dK,
+    uint16_t* __restrict__ dV, int S, int Hq, int Hkv, float scale, int n_kt, int n_work) {
+  using vec8 = typename Tr::vec8;
+  using vec4 = typename Tr::vec4;
+  using vec2 = typename Tr::vec2;
+  constexpr int BK = 32 * kBwdWaves;  // keys per workgroup
+  constexpr int BQ = kBwdTile;        // queries per LDS tile
+  constexpr int KS = D + 8;
+  constexpr int NKS = D / 16;
+  constexpr int NOB = D / 32;
+  constexpr int CHUNKS = D / 8;
+  constexpr int ROWS_PER_PASS = kBwdWaves * 64 / CHUNKS;
+  constexpr int PASSES = BQ / ROWS_PER_PASS;
+  static_assert(PASSES * ROWS_PER_PASS == BQ, "tile staging must cover the tile");
+
+  __shared__ __attribute__((aligned(16))) uint16_t Qs[2][BQ * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t Gs[2][BQ * KS];  // dO
+  __shared__ __attribute__((aligned(16))) float Ls[2][BQ];          // LSE * log2(e)
+  __shared__ __attribute__((aligned(16))) float Ds[2][BQ];          // D
+
+  const int work = xcd_remap(blockIdx.x, n_work);
+  const int bhk = work / n_kt;
+  const int kt = work % n_kt;  // causal: the first key tiles have the longest query walks
+  const int b = bhk / Hkv, hk = bhk % Hkv;
+  const int G = Hq / Hkv;
+  const int K0 = kt * BK;
+  const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
+  const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int kw0 = K0 + 32 * wave;
+  const int mykey = kw0 + l32;
+  const bool kvalid = mykey < S;
+  const float c2 = scale * kLog2e;
+
+  vec8 kv[NKS], vv[NKS];  // K^T and V^T as B operands (column = this lane's key)
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks) {
+    if (kvalid) {
+      kv[ks] = *(const vec8*)(Kp + (size_t)mykey * D + 16 * ks + 8 * hl);
+      vv[ks] = *(const vec8*)(Vp + (size_t)mykey * D + 16 * ks + 8 * hl);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { kv[ks][e] = 0; vv[ks][e] = 0; }
+    }
+  }
+
+  // query tiles: causal walks start at the tile holding the first key
+  const int t_begin = CAUSAL ? K0 / BQ : 0;
+  const int t_end = (S + BQ - 1) / BQ;
+  const int nt = max(0, t_end - t_begin);
+  const int n_it = G * nt;
+
+  const int st_row = tid / CHUNKS, st_col = (tid % CHUNKS) * 8;
+  u32x4 qreg[PASSES], greg[PASSES];
+  float lreg = 0.f, dreg = 0.f;
+  auto gload = [&](int it) {
+    const int h = hk * G + it / nt;
+    const int q0 = (t_begin + it % nt) * BQ;
+    const size_t qoff = (size_t)(b * Hq + h) * S;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int row = q0 + st_row + p * ROWS_PER_PASS;
+      if (row < S) {
+        qreg[p] = *(const u32x4*)(Q + (qoff + row) * D + st_col);
+        greg[p] = *(const u32x4*)(dO + (qoff + row) * D + st_col);
+      } else {
+        qreg[p] = u32x4{0, 0, 0, 0};
+        greg[p] = u32x4{0, 0, 0, 0};
+      }
+    }
+    if (tid < BQ) {
+      const int row = q0 + tid;
+      lreg = row < S ? LSE[qoff + row] * kLog2e : -kNegInf;  // past S: P = 0
+      dreg = row < S ? Dd[qoff + row] : 0.f;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+      const int r = st_row + p * ROWS_PER_PASS;
+      *(u32x4*)(&Qs[buf][r * KS + st_col]) = qreg[p];
+      *(u32x4*)(&Gs[buf][r * KS + st_col]) = greg[p];
+    }
+    if (tid < BQ) {
+      Ls[buf][tid] = lreg;
+      Ds[buf][tid] = dreg;
+    }
+  };
+
+  f32x16 dk[NOB], dv[NOB];  // dK^T, dV^T
+#pragma unroll
+  for (int i = 0; i < NOB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { dk[i][r] = 0.f; dv[i][r] = 0.f; }
+
+  const int qrow = rho32(l32);
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (s16 & 3);
+
+  if (n_it > 0) gload(0);
+  for (int it = 0; it < n_it; ++it) {
+    const int buf = it & 1;
+    lstore(buf);
+    __syncthreads();
+    if (it + 1 < n_it) gload(it + 1);
+    const int q0 = (t_begin + it % nt) * BQ;
+    const uint16_t* Qb = Qs[buf];
+    const uint16_t* Gb = Gs[buf];
+#pragma unroll
+    for (int qb = 0; qb < BQ / 32; ++qb) {
+      const int qs = q0 + 32 * qb;  // first query of the 32-query block
+      if (CAUSAL && qs + 31 < kw0) continue;  // every query before every key of the wave
+      // S = Q K^T, dP = dO V^T; register r of half hl <-> query
+      // qs + 16 (r/8) + 8 hl + r%8, column = this lane's key
+      f32x16 s, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int off = (32 * qb + qrow) * KS + 16 * ks + 8 * hl;
+        s = Tr::mfma32(*(const vec8*)(Qb + off), kv[ks], s);
+        dp = Tr::mfma32(*(const vec8*)(Gb + off), vv[ks], dp);
+      }
+      const bool need_mask = !kvalid || (CAUSAL && qs < kw0 + 31);
+      vec8 pp[2], pd[2];  // P and dS as B operands, k-step kk = 16 queries
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int qi = 32 * qb + 16 * kk + 8 * hl;  // tile row of register 8 kk
+        float lv[8], dv8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { lv[j] = Ls[buf][qi + j]; dv8[j] = Ds[buf][qi + j]; }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float p[2], ds[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int r = 8 * kk + 2 * j + e;
+            p[e] = fast_exp2(__builtin_fmaf(s[r], c2, -lv[2 * j + e]));
+            if (need_mask) {
+              const int query = q0 + qi + 2 * j + e;
+              if (!kvalid || (CAUSAL && mykey > query)) p[e] = 0.f;
+            }
+            ds[e] = p[e] * (dp[r] - dv8[2 * j + e]) * scale;
+          }
+          const vec2 a = Tr::pack2(p[0], p[1]);
+          const vec2 c = Tr::pack2(ds[0], ds[1]);
+          pp[kk][2 * j] = a[0];
+          pp[kk][2 * j + 1] = a[1];
+          pd[kk][2 * j] = c[0];
+          pd[kk][2 * j + 1] = c[1];
+        }
+      }
+      // dV^T[d x keys] += dO^T P and dK^T[d x keys] += Q^T dS
+#pragma unroll
+      for (int ob = 0; ob < NOB; ++ob) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int off = (32 * qb + 16 * kk + tr_row) * KS + 32 * ob + tr_col;
+          const vec4 glo = Tr::tr_read((const CA_LDS void*)(Gb + off));
+          const vec4 ghi = Tr::tr_read((const CA_LDS void*)(Gb + off + 4 * KS));
+          dv[ob] = Tr::mfma32(cat4<vec8, vec4>(glo, ghi), pp[kk], dv[ob]);
+          const vec4 qlo = Tr::tr_read((const CA_LDS void*)(Qb + off));
+          const vec4 qhi = Tr::tr_read((const CA_LDS void*)(Qb + off + 4 * KS));
+          dk[ob] = Tr::mfma32(cat4<vec8, vec4>(qlo, qhi), pd[kk], dk[ob]);
+        }
+      }
+    }
+  }
+  if (kvalid) {
+    const size_t koff = ((size_t)(b * Hkv + hk) * S + mykey) * D;
+    store_rowT<Tr, NOB>(dK + koff, dk, hl);
+    store_rowT<Tr, NOB>(dV + koff, dv, hl);
+  }
+}
+
+template <typename Tr, int D, bool CAUSAL>
+hipError_t launch_bwd_t(const void* q, const void* k, const void* v, const void* o,
+                        const void* dout, const float* lse, void* dq, void* dk, void* dv, int B,
+                        int Hq, int Hkv, int S, float scale, float* ws, hipStream_t stream) {
+  const long long rows = (long long)B * Hq * S;
+  const long long threads = rows * (D / 8);
+  const long long g0 = (threads + 255) / 256;
+  const int n_qt = (S + 32 * kBwdWaves - 1) / (32 * kBwdWaves);
+  const long long g1 = (long long)B * Hq * n_qt;
+  const long long g2 = (long long)B * Hkv * n_qt;  // key tiles are as tall as query tiles
+  if (g0 > 0x7fffffffLL || g1 > 0x7fffffffLL || g2 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((bwd_rowdot_kernel<Tr, D>), dim3((unsigned)g0), dim3(256), 0, stream,
+                     (const uint16_t*)o, (const uint16_t*)dout, ws, rows);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((bwd_dkv_kernel<Tr, D, CAUSAL>), dim3((unsigned)g2), dim3(kBwdWaves * 64), 0,
+                     stream, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                     (const uint16_t*)dout, lse, ws, (uint16_t*)dk, (uint16_t*)dv, S, Hq, Hkv,
+                     scale, n_qt, (int)g2);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((bwd_dq_kernel<Tr, D, CAUSAL>), dim3((unsigned)g1), dim3(kBwdWaves * 64), 0,
+                     stream, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                     (const uint16_t*)dout, lse, ws, (uint16_t*)dq, S, Hq, Hkv, scale, n_qt,
+                     (int)g1);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t bwd_workspace_bytes(int B, int Hq, int S) { return (size_t)B * Hq * S * sizeof(float); }
+
+hipError_t launch_flash_bwd(int dtype, const void* q, const void* k, const void* v,
+                            const void* o, const void* dout, const float* lse, void* dq, void* dk,
+                            void* dv, int B, int Hq, int Hkv, int S, int D, float scale,
+                            bool causal, void* ws, hipStream_t stream) {
+  if ((long long)B * Hq * S == 0) return hipSuccess;
+  float* w = (float*)ws;
+#define CA_BWD_CASE(TR, DD)                                                                   \
+  if (D == DD)                                                                                \
+    return causal ? launch_bwd_t<TR, DD, true>(q, k, v, o, dout, lse, dq, dk, dv, B, Hq, Hkv, \
+                                               S, scale, w, stream)                           \
+                  : launch_bwd_t<TR, DD, false>(q, k, v, o, dout, lse, dq, dk, dv, B, Hq,     \
+                                                Hkv, S, scale, w, stream);
+  if (dtype == kDtypeBF16) {
+    CA_BWD_CASE(BF16, 64)
+    CA_BWD_CASE(BF16, 128)
+  } else if (dtype == kDtypeF16) {
+    CA_BWD_CASE(F16, 64)
+    CA_BWD_CASE(F16, 128)
+  }
+#undef CA_BWD_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ca

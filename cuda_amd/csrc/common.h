@@ -115,6 +115,14 @@ struct F32 {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Natural-log logsumexp of a softmax row from the online-softmax state: m is
+// the running max of the scaled logits in log2 units, l the row sum of
+// 2^(x - m); an empty row (l == 0) gives -inf. l >= 1 for a non-empty row
+// (its largest term is 2^(max - m) >= 1), so the hardware log2 is accurate.
+__device__ __forceinline__ float row_lse(float m, float l) {
+  return l > 0.f ? (m + __builtin_amdgcn_logf(l)) * 0.6931471805599453f : kNegInf;
+}
+
 __device__ __forceinline__ float max3(float a, float b, float c) {
   return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
 }

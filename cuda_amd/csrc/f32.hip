@@ -32,7 +32,7 @@ namespace ca {
 template <int D, bool CAUSAL>
 __device__ CA_INLINE void prefill_f32_qtile(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int bh, int qt) {
+    float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh, int qt) {
   constexpr int NW = 4;
   constexpr int BM = 32 * NW;
   constexpr int BN = 32;
@@ -181,6 +181,7 @@ __device__ CA_INLINE void prefill_f32_qtile(
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+  if (Lse && hl == 0 && myq < S) Lse[(size_t)(b * Hq + h) * S + myq] = row_lse(m_run, l_tot);
   if (myq < S) {
 #pragma unroll
     for (int ob = 0; ob < NOB; ++ob) {
@@ -198,7 +199,7 @@ __device__ CA_INLINE void prefill_f32_qtile(
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh,
+    float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh,
     int n_work, int paired) {
   const QTileWork wk = prefill_work(xcd_remap(blockIdx.x, n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
@@ -206,13 +207,13 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile restages the LDS buffers: every wave must be done reading them
     if (pass) __syncthreads();
-    prefill_f32_qtile<D, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0,
+    prefill_f32_qtile<D, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0,
                                  pass ? wk.qt1 : wk.qt0);
   }
 }
 
 template <int D, bool CAUSAL>
-static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void* v, void* o,
+static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void* v, void* o, float* lse,
                                        int B, int Hq, int Hkv, int S, float scale,
                                        hipStream_t stream) {
   constexpr int BM = 128;
@@ -222,20 +223,20 @@ static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void*
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream,
-                     (const float*)q, (const float*)k, (const float*)v, (float*)o, S, Hq, Hkv,
+                     (const float*)q, (const float*)k, (const float*)v, (float*)o, lse, S, Hq, Hkv,
                      scale * kLog2e, n_qt, B * Hq, (int)grid, paired);
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, int B,
+hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, float* lse, int B,
                               int Hq, int Hkv, int S, int D, float scale, bool causal,
                               hipStream_t stream) {
   if (D == 64)
-    return causal ? launch_prefill_f32_t<64, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
-                  : launch_prefill_f32_t<64, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+    return causal ? launch_prefill_f32_t<64, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)
+                  : launch_prefill_f32_t<64, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
   if (D == 128)
-    return causal ? launch_prefill_f32_t<128, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
-                  : launch_prefill_f32_t<128, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+    return causal ? launch_prefill_f32_t<128, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)
+                  : launch_prefill_f32_t<128, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
   return hipErrorInvalidValue;
 }
 

@@ -13,13 +13,22 @@ constexpr int kDtypeF32 = 0;
 constexpr int kDtypeF16 = 1;
 constexpr int kDtypeBF16 = 2;
 
+// Prefill; lse (may be null) receives the natural-log row logsumexp [B, Hq, S].
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
-                          int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
-                          hipStream_t stream);
+                          float* lse, int B, int Hq, int Hkv, int S, int D, float scale,
+                          bool causal, hipStream_t stream);
 // float32 prefill (f32.hip)
-hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, int B,
-                              int Hq, int Hkv, int S, int D, float scale, bool causal,
+hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, float* lse,
+                              int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
                               hipStream_t stream);
+
+// Backward (backward.hip): dq, dk, dv from q, k, v, o, dout and the forward's
+// natural-log LSE; ws holds bwd_workspace_bytes (the rowsum(dO * O) terms).
+size_t bwd_workspace_bytes(int B, int Hq, int S);
+hipError_t launch_flash_bwd(int dtype, const void* q, const void* k, const void* v,
+                            const void* o, const void* dout, const float* lse, void* dq, void* dk,
+                            void* dv, int B, int Hq, int Hkv, int S, int D, float scale,
+                            bool causal, void* ws, hipStream_t stream);
 
 // Compute units of the current device (cached per device; 0 if unknown).
 inline int device_cus() {

@@ -39,7 +39,7 @@ namespace ca {
 template <typename Tr, int D, int NW, bool CAUSAL>
 __device__ CA_INLINE void prefill_fwd_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int bh, int qt) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
@@ -221,6 +221,7 @@ __device__ CA_INLINE void prefill_fwd_qtile(
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+  if (Lse && hl == 0 && myq < S) Lse[(size_t)(b * Hq + h) * S + myq] = row_lse(m_run, l_tot);
   if (myq < S) {
 #pragma unroll
     for (int ob = 0; ob < NOB; ++ob) {
@@ -240,7 +241,7 @@ __device__ CA_INLINE void prefill_fwd_qtile(
 template <typename Tr, int D, int NW, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile restages the LDS buffers: every wave must be done reading them
     if (pass) __syncthreads();
-    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, S, Hq, Hkv, scale_log2,
+    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2,
                                          pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0);
   }
 }
@@ -342,7 +343,7 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
 __device__ CA_INLINE void prefill_d128_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int bh, int qt, int q_shift) {
   using namespace pf128;
   using vec8 = typename Tr::vec8;
@@ -705,6 +706,8 @@ __device__ CA_INLINE void prefill_d128_qtile(
   for (int nb = 0; nb < NH; ++nb) {
     const float l_tot = pair32_sum(l_run[nb]);
     const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
+    if (Lse && hl == 0 && myq[nb] >= 0 && myq[nb] < S)
+      Lse[(size_t)(b * Hq + h) * S + myq[nb]] = row_lse(m_run[nb], l_tot);
     if (myq[nb] >= 0 && myq[nb] < S) {
 #pragma unroll
       for (int ob = 0; ob < 4; ++ob) {
@@ -725,7 +728,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
 template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
 __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, int S, int Hq,
+    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
@@ -735,7 +738,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
     prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(
-        Q, K, V, O, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift);
+        Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift);
   }
 }
 
@@ -749,7 +752,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 #define CA_PF_MAXSTAGES 4
 #endif
 template <typename Tr, bool CAUSAL, int BM>
-static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const void* v, void* o,
+static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const void* v, void* o, float* lse,
                                          int B, int Hq, int Hkv, int S, float scale,
                                          hipStream_t stream) {
   constexpr int NH = CA_PF_NH;
@@ -773,12 +776,12 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
   if (sl2 >= 0.f) {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
                        n_qt, B * Hq, (int)grid, paired, q_shift);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, sl2,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
                        n_qt, B * Hq, (int)grid, paired, q_shift);
   }
   return hipGetLastError();
@@ -789,22 +792,22 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
 // tiles cover S with at most ~5 % padding rows and the grid still gives every
 // CU two workgroups; 256 rows (8 waves) otherwise.
 template <typename Tr, bool CAUSAL>
-static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o,
+static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o, float* lse,
                                       int B, int Hq, int Hkv, int S, float scale,
                                       hipStream_t stream) {
 #ifdef CA_PF_BM
-  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
 #else
   const long long n384 = (S + 383) / 384;
   const bool fits = n384 * 384 * 20 <= (long long)S * 21;
   const bool tall = fits && (long long)B * Hq * n384 >= 2LL * device_cus();
-  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, B, Hq, Hkv, S, scale, stream)
-              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, B, Hq, Hkv, S, scale, stream);
+  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)
+              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
 #endif
 }
 
 template <typename Tr, int D, bool CAUSAL>
-static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o,
+static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o, float* lse,
                                    int B, int Hq, int Hkv, int S, float scale,
                                    hipStream_t stream) {
 #ifndef CA_PF_NW
@@ -819,29 +822,29 @@ static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, 
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
                      dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, S, Hq, Hkv, scale * kLog2e, n_qt, B * Hq,
+                     (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, scale * kLog2e, n_qt, B * Hq,
                      (int)grid, paired);
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
+hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
                           hipStream_t stream) {
 #define CA_PREFILL_CASE(TR, DD)                                                          \
   if (D == DD) {                                                                         \
-    return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream) \
-                  : launch_prefill_t<TR, DD, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream); \
+    return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream) \
+                  : launch_prefill_t<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream); \
   }
 #ifndef CA_PF_OLD128
 #define CA_PREFILL_128(TR)                                                                     \
   if (D == 128) {                                                                              \
-    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, B, Hq, Hkv, S, scale, stream)    \
-                  : launch_prefill_d128<TR, false>(q, k, v, o, B, Hq, Hkv, S, scale, stream);  \
+    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)    \
+                  : launch_prefill_d128<TR, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);  \
   }
 #else
 #define CA_PREFILL_128(TR) CA_PREFILL_CASE(TR, 128)
 #endif
-  if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, B, Hq, Hkv, S, D, scale, causal, stream);
+  if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, lse, B, Hq, Hkv, S, D, scale, causal, stream);
   if (dtype == kDtypeBF16) {
     CA_PREFILL_CASE(BF16, 64)
     CA_PREFILL_128(BF16)

@@ -52,6 +52,35 @@ ca_status ca_flash_attention_fwd(ca_dtype dtype, const void* q, const void* k, c
                                  int seq_len, int head_dim, float softmax_scale, int is_causal,
                                  void* stream);
 
+/* Prefill forward that also writes the natural-log row logsumexp of the
+ * scaled, masked scores, lse: [batch, num_q_heads, seq_len] float32 (-inf for
+ * a row with no visible key). No counterpart in the reference: its forward
+ * returns O only, while its backward consumes this LSE
+ * (flash_attention_bwd_kernel.cuh:31, fused_softmax_binding.cpp:367-376;
+ * the reference tests build it with ref_lse, tests/_utils.py:56-64). Same
+ * arguments and checks as ca_flash_attention_fwd. */
+ca_status ca_flash_attention_fwd_lse(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                     void* o, float* lse, int batch, int num_q_heads,
+                                     int num_kv_heads, int seq_len, int head_dim,
+                                     float softmax_scale, int is_causal, void* stream);
+
+/* Backward of the prefill forward: dq, dk, dv from q, k, v, the forward output
+ * o, its gradient dout and the forward's natural-log LSE [batch, num_q_heads,
+ * seq_len] float32. q, o, dout, dq: [batch, num_q_heads, seq_len, head_dim];
+ * k, v, dk, dv: [batch, num_kv_heads, seq_len, head_dim] (GQA: dk, dv sum
+ * over the q heads of a kv head). dtype bf16 or fp16 (float32: CA_UNSUPPORTED).
+ * Replaces dispatch_flash_attention_v2_backward<T> (kernels_api.h:65-69);
+ * dq, dk, dv are written, not accumulated. workspace:
+ * ca_flash_attention_bwd_workspace_bytes(batch, num_q_heads, seq_len). */
+ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, const void* v,
+                                 const void* o, const void* dout, const float* lse, void* dq,
+                                 void* dk, void* dv, int batch, int num_q_heads, int num_kv_heads,
+                                 int seq_len, int head_dim, float softmax_scale, int is_causal,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of the ca_flash_attention_bwd workspace (the rowsum(dout * o) terms). */
+size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int seq_len);
+
 /* Single-token decode over a contiguous cache.
  * q, o: [batch, num_q_heads, 1, head_dim]; k, v: [batch, num_kv_heads, kv_len,
  * head_dim]. Replaces dispatch_async_flash_decode<T> (kernels_api.h:58-62).

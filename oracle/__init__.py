@@ -23,19 +23,23 @@ Pinning (what checks each function; see ``tests/test_oracle.py``):
                                      saturation) and round-trip bounds
   attention_tiled / split_merge      equality with ``attention`` (restatements
                                      of the kernels' blocking)
+  attention_backward                 torch autograd (CPU, fp64) of SDPA,
+                                     central finite differences of
+                                     ``attention`` (fp64), the one-key closed
+                                     form (dq = dk = 0, dv = dout)
 No function is left "parity unpinned" except the MXFP8 *semantics* as a whole:
 the reference declares ``dispatch_fused_microscaled_attention``
 (kernels_api.h:103-108) but ships no kernel, binding or test for it, so the
 oracle follows the OCP MX v1.0 definition instead of a reference vector.
 """
-from .attention import (attention, attention_lse, attention_tiled, decode,
-                        default_scale, split_merge)
+from .attention import (attention, attention_backward, attention_lse, attention_tiled,
+                        decode, default_scale, split_merge)
 from .fp8 import (E4M3_MAX, e4m3_decode, e4m3_encode, e8m0_decode,
                   mx_dequantize, mx_quantize, quantize_per_page_fp8)
 from .paged import gather_paged, make_paged_cache, paged_decode
 
 __all__ = [
-    "attention", "attention_lse", "attention_tiled", "decode", "default_scale",
+    "attention", "attention_backward", "attention_lse", "attention_tiled", "decode", "default_scale",
     "split_merge", "E4M3_MAX", "e4m3_decode", "e4m3_encode", "e8m0_decode",
     "mx_dequantize", "mx_quantize", "quantize_per_page_fp8", "gather_paged",
     "make_paged_cache", "paged_decode",

@@ -11,6 +11,8 @@ Reference anchors
 * default scale      fused_softmax_binding.cpp:69-72  1/sqrt(head_dim)
 * empty softmax row  flash_attention_v2_kernel.cuh:223  l == 0 -> output 0
 * online softmax     flash_attention_v2_kernel.cuh:179-229 (running max / sum)
+* backward           flash_attention_bwd_kernel.cuh:9-19, 96-214 (dQ, dK, dV from
+                     the forward's LSE; D_i = rowsum(dO * O))
 """
 import math
 
@@ -107,6 +109,49 @@ def attention_lse(q, k, is_causal=False, scale=None, dtype=np.float32):
             _, lse[i, h] = _row_attention(q[i, h], k[i, kh], k[i, kh], is_causal,
                                           scale, dtype, 512, want_lse=True)
     return lse
+
+
+def attention_backward(dout, q, k, v, out, lse, is_causal=False, scale=None,
+                       dtype=np.float32):
+    """Gradients (dq, dk, dv) of O = softmax(q k^T * scale + mask) v, given the
+    forward output ``out`` and its natural-log row logsumexp ``lse``.
+
+    Restates the reference backward (flash_attention_bwd_kernel.cuh): D_i =
+    rowsum(dO * O) (:96-108); P = exp(S * scale - LSE_i) (:166-172); dP = dO
+    V^T (:174-181); dS = P (dP - D_i) * scale (:183-184); dQ = dS K
+    (:188-199); dV = P^T dO and dK = dS^T Q (:201-214). Masked entries (key >
+    query when causal) have P = dS = 0 (:160-163). GQA (Hkv < Hq, kv head =
+    h // (Hq / Hkv)): dk and dv of a kv head are the sums over its q heads,
+    the gradient of the repeat_interleave in tests/_utils.py:67-72.
+
+    dout, q, out: [B, Hq, S, D]; k, v: [B, Hkv, S, D]; lse: [B, Hq, S].
+    """
+    dout, q, k, v, out, lse = (np.asarray(x) for x in (dout, q, k, v, out, lse))
+    b, hq, sq, d = q.shape
+    hkv, skv = k.shape[1], k.shape[2]
+    scale = default_scale(d) if scale is None else float(scale)
+    dq = np.zeros(q.shape, dtype=dtype)
+    dk = np.zeros(k.shape, dtype=dtype)
+    dv = np.zeros(v.shape, dtype=dtype)
+    for i in range(b):
+        for h in range(hq):
+            kh = _kv_head(h, hq, hkv)
+            qh, kk, vv = (x.astype(dtype) for x in (q[i, h], k[i, kh], v[i, kh]))
+            do, oh = dout[i, h].astype(dtype), out[i, h].astype(dtype)
+            s = (qh @ kk.T) * dtype(scale)
+            visible = np.ones((sq, skv), dtype=bool)
+            if is_causal:
+                visible = np.arange(skv)[None, :] <= np.arange(sq)[:, None]
+            with np.errstate(invalid="ignore", over="ignore"):
+                p = np.where(visible, np.exp(s - lse[i, h].astype(dtype)[:, None]), 0)
+            p = np.nan_to_num(p, nan=0.0).astype(dtype)
+            d_row = (do * oh).sum(axis=1, keepdims=True)
+            dp = do @ vv.T
+            ds = (p * (dp - d_row) * dtype(scale)).astype(dtype)
+            dq[i, h] = ds @ kk
+            dk[i, kh] += ds.T @ qh
+            dv[i, kh] += p.T @ do
+    return dq, dk, dv
 
 
 def decode(q, k, v, context_lens, scale=None, dtype=np.float32):

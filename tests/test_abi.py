@@ -83,6 +83,32 @@ def test_prefill_rejects_bad_arguments():
     assert _status("ca_flash_attention_fwd", L.CA_BF16, P, P, P, P, 0, 4, 4, 64, 64, 0.1, 0, None) == L.CA_OK
 
 
+def test_backward_entry_points_validate():
+    lib = L.load()
+    assert lib.ca_flash_attention_bwd_workspace_bytes(2, 8, 100) == 2 * 8 * 100 * 4
+    assert lib.ca_flash_attention_bwd_workspace_bytes(0, 8, 100) == 0
+    args = [L.CA_BF16, P, P, P, P, P, P, P, P, P, 1, 4, 2, 64, 64, 0.1, 1, P, 1 << 20, None]
+    f32 = list(args)
+    f32[0] = L.CA_F32
+    assert _status("ca_flash_attention_bwd", *f32) == L.CA_UNSUPPORTED
+    small_ws = list(args)
+    small_ws[18] = 16
+    assert _status("ca_flash_attention_bwd", *small_ws) == L.CA_INVALID_ARGUMENT
+    assert b"workspace" in lib.ca_last_error()
+    bad_heads = list(args)
+    bad_heads[12] = 3
+    assert _status("ca_flash_attention_bwd", *bad_heads) == L.CA_INVALID_ARGUMENT
+    no_lse = list(args)
+    no_lse[6] = None
+    assert _status("ca_flash_attention_bwd", *no_lse) == L.CA_INVALID_ARGUMENT
+    empty = list(args)
+    empty[13] = 0
+    assert _status("ca_flash_attention_bwd", *empty) == L.CA_OK
+    fwd = [L.CA_BF16, P, P, P, P, None, 1, 4, 4, 64, 64, 0.1, 0, None]
+    assert _status("ca_flash_attention_fwd_lse", *fwd) == L.CA_INVALID_ARGUMENT
+    assert b"lse" in lib.ca_last_error()
+
+
 def test_paged_rejects_bad_arguments():
     args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
     bad_page = list(args)

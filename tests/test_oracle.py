@@ -281,3 +281,95 @@ def test_per_page_quantization_matches_reference_recipe():
     ref_codes = (pages / ref_scale[:, :, None, None]).to(torch.float8_e4m3fn).view(torch.uint8)
     np.testing.assert_array_equal(scale, ref_scale.numpy())
     np.testing.assert_array_equal(codes, ref_codes.numpy())
+
+
+# ---------------------------------------------------------------------------
+# backward (flash_attention_bwd_kernel.cuh math)
+# ---------------------------------------------------------------------------
+def _torch_grads(q, k, v, dout, causal, scale=None):
+    """fp64 torch autograd of SDPA with the GQA repeat: an implementation that
+    shares no code with the oracle."""
+    qt, kt, vt = (torch.from_numpy(x).double().requires_grad_() for x in (q, k, v))
+    rep = q.shape[1] // k.shape[1]
+    o = F.scaled_dot_product_attention(qt, kt.repeat_interleave(rep, 1), vt.repeat_interleave(rep, 1),
+                                       is_causal=causal, scale=scale)
+    o.backward(torch.from_numpy(dout).double())
+    return o.detach().numpy(), qt.grad.numpy(), kt.grad.numpy(), vt.grad.numpy()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hq,hkv,s,d", [(2, 2, 64, 64), (2, 2, 100, 64), (4, 2, 37, 128), (3, 1, 5, 16)])
+def test_backward_vs_torch_autograd(causal, hq, hkv, s, d):
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, hq, s, d))
+    k = rng.standard_normal((1, hkv, s, d))
+    v = rng.standard_normal((1, hkv, s, d))
+    dout = rng.standard_normal((1, hq, s, d))
+    o, gq, gk, gv = _torch_grads(q, k, v, dout, causal)
+    lse = oracle.attention_lse(q, k, is_causal=causal, dtype=np.float64)
+    dq, dk, dv = oracle.attention_backward(dout, q, k, v, o, lse, is_causal=causal, dtype=np.float64)
+    for name, a, b in (("dq", dq, gq), ("dk", dk, gk), ("dv", dv, gv)):
+        np.testing.assert_allclose(a, b, atol=1e-10, rtol=0, err_msg=name)
+
+
+def test_backward_custom_scale_vs_torch_autograd():
+    rng = np.random.default_rng(12)
+    q, k, v, dout = (rng.standard_normal((1, 2, 33, 64)) for _ in range(4))
+    o, gq, gk, gv = _torch_grads(q, k, v, dout, True, scale=0.3)
+    lse = oracle.attention_lse(q, k, is_causal=True, scale=0.3, dtype=np.float64)
+    dq, dk, dv = oracle.attention_backward(dout, q, k, v, o, lse, is_causal=True, scale=0.3,
+                                           dtype=np.float64)
+    for a, b in ((dq, gq), (dk, gk), (dv, gv)):
+        np.testing.assert_allclose(a, b, atol=1e-10, rtol=0)
+
+
+def test_backward_vs_finite_differences():
+    """Central differences of the forward oracle, fp64, on a tiny case."""
+    rng = np.random.default_rng(13)
+    q, k, v, dout = (rng.standard_normal((1, 1, 4, 3)) for _ in range(4))
+    for causal in (False, True):
+        o = oracle.attention(q, k, v, is_causal=causal, dtype=np.float64)
+        lse = oracle.attention_lse(q, k, is_causal=causal, dtype=np.float64)
+        grads = oracle.attention_backward(dout, q, k, v, o, lse, is_causal=causal, dtype=np.float64)
+        eps = 1e-6
+        for which, g in zip(range(3), grads):
+            x = [q, k, v][which]
+            num = np.zeros_like(x)
+            for idx in np.ndindex(x.shape):
+                xp, xm = x.copy(), x.copy()
+                xp[idx] += eps
+                xm[idx] -= eps
+                args_p = [q, k, v]
+                args_m = [q, k, v]
+                args_p[which], args_m[which] = xp, xm
+                fp = (oracle.attention(*args_p, is_causal=causal, dtype=np.float64) * dout).sum()
+                fm = (oracle.attention(*args_m, is_causal=causal, dtype=np.float64) * dout).sum()
+                num[idx] = (fp - fm) / (2 * eps)
+            np.testing.assert_allclose(g, num, atol=1e-7, rtol=0)
+
+
+def test_backward_single_key_closed_form():
+    """One key: the softmax is constant 1, so dq = dk = 0 and dv = dout."""
+    rng = np.random.default_rng(14)
+    q, k, v, dout = (rng.standard_normal((2, 2, 1, 64)) for _ in range(4))
+    o = oracle.attention(q, k, v, dtype=np.float64)
+    lse = oracle.attention_lse(q, k, dtype=np.float64)
+    dq, dk, dv = oracle.attention_backward(dout, q, k, v, o, lse, dtype=np.float64)
+    assert np.abs(dq).max() < 1e-12 and np.abs(dk).max() < 1e-12
+    np.testing.assert_allclose(dv, dout, atol=1e-12, rtol=0)
+
+
+def test_planted_backward_mistake_is_caught(monkeypatch):
+    """Dropping the D_i term (a plausible slip) breaks the autograd check."""
+    rng = np.random.default_rng(15)
+    q, k, v, dout = (rng.standard_normal((1, 2, 20, 16)) for _ in range(4))
+    o, gq, _, _ = _torch_grads(q, k, v, dout, True)
+    lse = oracle.attention_lse(q, k, is_causal=True, dtype=np.float64)
+    real = oattn.attention_backward
+
+    def dropped_d(dout_, q_, k_, v_, out_, lse_, **kw):
+        return real(dout_, q_, k_, v_, np.zeros_like(out_), lse_, **kw)
+
+    monkeypatch.setattr(oattn, "attention_backward", dropped_d)
+    dq, _, _ = oattn.attention_backward(dout, q, k, v, o, lse, is_causal=True, dtype=np.float64)
+    assert np.abs(dq - gq).max() > 1e-3
