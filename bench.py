@@ -104,6 +104,26 @@ def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
                         "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal})
 
 
+def w_backward(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
+    """Backward of the C2 prefill (dq, dk, dv from q, k, v, out, dout, lse).
+    Work: five S x S x D products per (b, h) (S, dP, dV, dK, dQ), 2.5x the
+    forward's FLOP count, halved when causal (the same convention)."""
+    import torch
+    import cuda_llm
+    g = _gen()
+    q, k, v, dout = (torch.randn(B, H, S, D, device="cuda", generator=g).to(torch.bfloat16)
+                     for _ in range(4))
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=causal)
+    ms = time_steps(lambda: cuda_llm.flash_attention_backward(dout, q, k, v, out, lse,
+                                                              is_causal=causal), steps, warmup)
+    flops = 2.5 * (2.0 if causal else 4.0) * B * H * S * S * D
+    tf = flops / (ms * 1e-3) / 1e12
+    return dict(ms=ms, value=tf, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_TFLOPS, work=flops,
+                config={"workload": f"C2 bf16 {'causal' if causal else 'non-causal'} prefill backward "
+                                    "(flash_attention_backward)",
+                        "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal})
+
+
 def cpu_prefill(r, seconds):
     """Oracle (numpy fp32) on as many (b, h) heads of the same inputs as fit in
     ~``seconds``; heads are independent, so the rate scales exactly."""
@@ -269,6 +289,7 @@ WORKLOADS = {
     "decode_fp8": lambda s, w: w_decode(s, w, fp8=True),
     "decode_bf16": lambda s, w: w_decode(s, w, fp8=False),
     "mxfp8": w_mxfp8,
+    "backward": w_backward,
     "copy": w_copy,
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
@@ -318,12 +339,14 @@ def main():
                    "decode_fp8": "FP8 paged GQA decode HBM GB/s (C4)",
                    "decode_bf16": "bf16 paged GQA decode HBM GB/s (C3)",
                    "mxfp8": "MXFP8 causal attention TFLOP/s (C5)",
+                   "backward": "prefill backward TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
                    "copy": "device copy GB/s"}[head],
         "value": s["value"], "unit": s["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": s["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": {"prefill": "bf16", "prefill_nc": "bf16", "decode_fp8": "e4m3 KV / bf16 q,out / fp32 softmax",
-                  "decode_bf16": "bf16", "mxfp8": "mxfp8 e4m3+e8m0 / bf16 out", "copy": "bf16"}[head],
+                  "decode_bf16": "bf16", "mxfp8": "mxfp8 e4m3+e8m0 / bf16 out", "backward": "bf16",
+                  "copy": "bf16"}[head],
         "data": "synthetic, seeded (torch generator seed 0), resident in HBM",
         "config": dict(s["config"], parallelism="none (1 GPU)"),
         "roofline": s["roofline"],
@@ -346,7 +369,7 @@ def main():
         del r
         torch.cuda.empty_cache()
         extra = {}
-        for name in ("prefill_nc", "decode_bf16", "mxfp8"):
+        for name in ("prefill_nc", "decode_bf16", "mxfp8", "backward"):
             r = WORKLOADS[name](args.steps, args.warmup)
             log(f"{name}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
             extra[name] = summary(name, r)
