@@ -28,7 +28,7 @@ __all__ = [
     "flash_attention_forward_lse", "flash_attention_backward",
     "fused_gqa_forward", "flash_decode", "async_flash_decode", "paged_attention",
     "paged_attention_forward", "fp8_paged_attention", "fp8_paged_attention_forward",
-    "fused_microscaled_attention", "mx_scales_to_e8m0",
+    "fused_microscaled_attention", "mx_scales_to_e8m0", "paged_kv_append",
 ]
 
 _DT = {torch.bfloat16: _lib.CA_BF16, torch.float16: _lib.CA_F16, torch.float32: _lib.CA_F32}
@@ -311,6 +311,72 @@ def fp8_paged_attention_forward(query, key_cache_fp8, value_cache_fp8, k_scale, 
 
 
 fp8_paged_attention = fp8_paged_attention_forward
+
+
+def paged_kv_append(key, value, key_cache, value_cache, block_tables, context_lens,
+                    new_lens=None, k_scale=None, v_scale=None):
+    """Append new tokens to a paged KV cache in place (the step before paged
+    decode; no reference kernel: its tests build caches in torch, tests/
+    _utils.py:105-133, in the layout the paged decode entry points read).
+
+    key, value: [N, Hkv, T, D] fp16/bf16. Sequence n appends its first
+    ``new_lens[n]`` tokens (default T) at positions ``context_lens[n]`` ..
+    through ``block_tables`` [N, max_blocks]; ``context_lens`` is not updated.
+    Caches [num_blocks, Hkv, D, 16]: of key's dtype, or e4m3 codes (uint8 /
+    int8 / float8_e4m3fn) with float32 ``k_scale``/``v_scale``: per head [Hkv]
+    (new slots quantised with the given scale, saturated to +-448) or per
+    (page, head) [num_blocks, Hkv] (every touched page quantised again with
+    scale = max(amax / 448, 1e-8), written in place; tests/test_kernels_misc.
+    py:52-55 per page). Positions past the table and block ids outside the
+    pool are skipped.
+    """
+    _check(key.is_cuda and value.is_cuda and key_cache.is_cuda and value_cache.is_cuda,
+           "Inputs must be on CUDA")
+    _check(block_tables.is_cuda and context_lens.is_cuda, "Metadata tensors must be on CUDA")
+    _check(key.dim() == 4 and key.shape == value.shape,
+           "key and value must be [num_seqs, num_kv_heads, new_tokens, head_dim]")
+    n, hkv, t, d = key.shape
+    _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape
+           and key_cache.size(1) == hkv and key_cache.size(2) == d and key_cache.size(3) == 16,
+           "caches must be [num_blocks, num_kv_heads, head_dim, 16]")
+    _check(key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "caches must be contiguous (they are written in place)")
+    _check(block_tables.dim() == 2 and block_tables.size(0) == n, "block_tables must be [num_seqs, max_blocks]")
+    _check(context_lens.numel() == n, "context_lens must have num_seqs entries")
+    _check(key.dtype == value.dtype, "key and value must have the same dtype")
+    dt = _dtype_code(key, "paged_kv_append")
+    _check(dt != _lib.CA_F32, "paged_kv_append: key/value must be fp16 or bf16")
+    fp8 = key_cache.dtype in _FP8_CACHE_DTYPES
+    num_blocks = key_cache.size(0)
+    per_block = False
+    if fp8:
+        _check(value_cache.dtype in _FP8_CACHE_DTYPES, "both caches must be FP8")
+        _check(k_scale is not None and v_scale is not None, "FP8 caches need k_scale and v_scale")
+        _check(k_scale.is_cuda and v_scale.is_cuda, "Scale tensors must be on CUDA")
+        _check(k_scale.dtype == torch.float32 and v_scale.dtype == torch.float32
+               and k_scale.is_contiguous() and v_scale.is_contiguous(),
+               "scales must be contiguous float32 (per-page scales are written in place)")
+        per_block = k_scale.dim() == 2
+        if per_block:
+            _check(tuple(k_scale.shape) == (num_blocks, hkv) and tuple(v_scale.shape) == (num_blocks, hkv),
+                   "per-block scales must be [num_blocks, num_kv_heads]")
+        else:
+            _check(k_scale.numel() == hkv and v_scale.numel() == hkv,
+                   "per-head scales must be [num_kv_heads]")
+    else:
+        _check(key_cache.dtype == key.dtype and value_cache.dtype == key.dtype,
+               "16-bit caches must have key's dtype")
+    key, value = (_aligned(x.contiguous()) for x in (key, value))
+    tables = block_tables.to(torch.int32).contiguous()
+    lens = context_lens.to(torch.int32).contiguous()
+    nl = None
+    if new_lens is not None:
+        _check(new_lens.is_cuda and new_lens.numel() == n, "new_lens must be [num_seqs] on CUDA")
+        nl = new_lens.to(torch.int32).contiguous()
+    _lib.call("ca_paged_kv_append", dt, int(fp8), _ptr(key), _ptr(value), _ptr(key_cache),
+              _ptr(value_cache), _ptr(k_scale if fp8 else None), _ptr(v_scale if fp8 else None),
+              int(per_block), _ptr(tables), _ptr(lens), _ptr(nl), n, hkv, d, t,
+              tables.size(1), num_blocks, _stream())
 
 
 # ---------------------------------------------------------------------------

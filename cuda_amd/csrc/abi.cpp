@@ -285,4 +285,36 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
                   what);
 }
 
+ca_status ca_paged_kv_append(ca_dtype dtype, int cache_kind, const void* key, const void* value,
+                             void* key_cache, void* value_cache, float* k_scale, float* v_scale,
+                             int per_block_scales, const int32_t* block_tables,
+                             const int32_t* context_lens, const int32_t* new_lens, int num_seqs,
+                             int num_kv_heads, int head_dim, int max_new_tokens,
+                             int max_blocks_per_seq, int num_blocks, void* stream) {
+  const char* what = "paged_kv_append";
+  ca_status st;
+  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (cache_kind != 0 && cache_kind != 1)
+    return fail(CA_INVALID_ARGUMENT, "%s: unknown cache kind %d", what, cache_kind);
+  if (num_kv_heads <= 0) return fail(CA_INVALID_ARGUMENT, "%s: num_kv_heads must be positive", what);
+  if (num_seqs < 0 || max_new_tokens < 0 || max_blocks_per_seq < 0 || num_blocks < 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (num_seqs == 0 || max_new_tokens == 0 || max_blocks_per_seq == 0) return CA_OK;
+  if (!key || !value || !key_cache || !value_cache || !block_tables || !context_lens)
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(key_cache) || !aligned16(value_cache))
+    return fail(CA_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", what);
+  if (cache_kind == 1 && (!k_scale || !v_scale))
+    return fail(CA_INVALID_ARGUMENT, "%s: FP8 caches need k_scale and v_scale", what);
+  if ((long long)num_seqs * num_kv_heads * max_new_tokens * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  const int kind = cache_kind == 0 ? 0 : (per_block_scales ? 2 : 1);
+  return from_hip(ca::launch_kv_append((int)dtype, kind, key, value, key_cache, value_cache,
+                                       k_scale, v_scale, block_tables, context_lens, new_lens,
+                                       num_seqs, num_kv_heads, head_dim, max_new_tokens,
+                                       max_blocks_per_seq, num_blocks, (hipStream_t)stream),
+                  what);
+}
+
 }  // extern "C"

@@ -90,6 +90,14 @@ hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const vo
                                int B, int Hq, int Hkv, int S, int D, float scale, void* ws,
                                size_t ws_bytes, hipStream_t stream);
 
+// Paged KV-cache append (kv_append.hip). kind: 0 = 16-bit cache of the key
+// dtype, 1 = fp8 e4m3 with per-head scales [Hkv], 2 = fp8 e4m3 with per-page
+// scales [num_blocks, Hkv] (re-quantised over every touched page).
+hipError_t launch_kv_append(int dtype, int kind, const void* key, const void* value, void* kc,
+                            void* vc, float* k_scale, float* v_scale, const int32_t* block_tables,
+                            const int32_t* context_lens, const int32_t* new_lens, int N, int Hkv,
+                            int D, int T, int max_blocks, int num_blocks, hipStream_t stream);
+
 // MXFP8 attention: e4m3 q/k/v [B, H, S, D] with e8m0 scale bytes [B, H, S, D/32].
 hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                         const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,

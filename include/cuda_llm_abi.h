@@ -81,6 +81,31 @@ ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, c
 /* Bytes of the ca_flash_attention_bwd workspace (the rowsum(dout * o) terms). */
 size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int seq_len);
 
+/* Append new tokens to a paged KV cache, in place: the step before paged
+ * decode. key, value: [num_seqs, num_kv_heads, max_new_tokens, head_dim] of
+ * `dtype` (bf16/fp16); sequence n appends its first new_lens[n] tokens
+ * (new_lens NULL: max_new_tokens each) at positions context_lens[n] ..
+ * through block_tables [num_seqs, max_blocks_per_seq]: the token at position
+ * t goes to cache[block_tables[n][t / 16]][h][:, t % 16], the layout of the
+ * paged decode entry points (tests/_utils.py:105-133).
+ *   cache_kind 0: 16-bit caches of `dtype`;
+ *   cache_kind 1: e4m3 code caches (uint8) with float32 scales, per head
+ *     [num_kv_heads] (new slots: e4m3(x / scale), saturated) or, with
+ *     per_block_scales, per (page, kv head) [num_blocks, num_kv_heads]: each
+ *     touched page is quantised again over its valid slots with scale =
+ *     max(amax / 448, 1e-8) (the reference's recipe, tests/
+ *     test_kernels_misc.py:52-55, per page), and its scale is written.
+ * Positions past the table and block ids outside [0, num_blocks) are skipped.
+ * No counterpart in the reference (it builds caches in torch); the format is
+ * the one ca_paged_attention and ca_fp8_paged_attention read. context_lens is
+ * not updated. */
+ca_status ca_paged_kv_append(ca_dtype dtype, int cache_kind, const void* key, const void* value,
+                             void* key_cache, void* value_cache, float* k_scale, float* v_scale,
+                             int per_block_scales, const int32_t* block_tables,
+                             const int32_t* context_lens, const int32_t* new_lens, int num_seqs,
+                             int num_kv_heads, int head_dim, int max_new_tokens,
+                             int max_blocks_per_seq, int num_blocks, void* stream);
+
 /* Single-token decode over a contiguous cache.
  * q, o: [batch, num_q_heads, 1, head_dim]; k, v: [batch, num_kv_heads, kv_len,
  * head_dim]. Replaces dispatch_async_flash_decode<T> (kernels_api.h:58-62).

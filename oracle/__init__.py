@@ -23,6 +23,10 @@ Pinning (what checks each function; see ``tests/test_oracle.py``):
                                      saturation) and round-trip bounds
   attention_tiled / split_merge      equality with ``attention`` (restatements
                                      of the kernels' blocking)
+  paged_append                       make_paged_cache of whole sequences,
+                                     token-by-token == all at once,
+                                     quantize_per_page_fp8 of the built cache,
+                                     the per-head e4m3(x / s) recipe
   attention_backward                 torch autograd (CPU, fp64) of SDPA,
                                      central finite differences of
                                      ``attention`` (fp64), the one-key closed
@@ -36,11 +40,11 @@ from .attention import (attention, attention_backward, attention_lse, attention_
                         decode, default_scale, split_merge)
 from .fp8 import (E4M3_MAX, e4m3_decode, e4m3_encode, e8m0_decode,
                   mx_dequantize, mx_quantize, quantize_per_page_fp8)
-from .paged import gather_paged, make_paged_cache, paged_decode
+from .paged import gather_paged, make_paged_cache, paged_append, paged_decode
 
 __all__ = [
     "attention", "attention_backward", "attention_lse", "attention_tiled", "decode", "default_scale",
     "split_merge", "E4M3_MAX", "e4m3_decode", "e4m3_encode", "e8m0_decode",
     "mx_dequantize", "mx_quantize", "quantize_per_page_fp8", "gather_paged",
-    "make_paged_cache", "paged_decode",
+    "make_paged_cache", "paged_append", "paged_decode",
 ]

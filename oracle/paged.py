@@ -15,6 +15,10 @@ Reference anchors
            v = code * v_scale (the codes are e4m3 here, not int8 — the
            reference test's intended semantics, tests/test_kernels_misc.py:42-64)
 * GQA      tests/_utils.py:67-72     kv head = q head // (Hq / Hkv)
+* append   no reference kernel (the reference builds caches in torch, tests/
+           _utils.py:105-133): token t of sequence n is written at the walk
+           position above; FP8 pages are quantised with the per-page form of
+           tests/test_kernels_misc.py:52-55
 * L <= 0   writes zeros (the reference leaves the output unwritten,
            paged_attention_kernel.cuh:37-38; the l == 0 rule of
            flash_attention_v2_kernel.cuh:223 is applied instead)
@@ -98,3 +102,87 @@ def paged_decode(query, key_cache, value_cache, block_tables, context_lens,
         out[i] = decode(query[i][None], kk, vv, [L], scale=scale, dtype=dtype)[0]
     assert out.shape[1] % hkv == 0
     return out
+
+
+def paged_append(key, value, key_cache, value_cache, block_tables, context_lens, new_lens=None,
+                 k_scale=None, v_scale=None):
+    """Append new tokens to a paged KV cache: the step before paged decode.
+
+    key, value: [N, Hkv, T, D] new tokens; sequence n appends its first
+    ``new_lens[n]`` (default T) tokens at positions context_lens[n] ..
+    context_lens[n] + new_lens[n] - 1, token at position t going to
+    ``cache[block_tables[n][t // 16]][h][:, t % 16]`` (the layout of
+    tests/_utils.py:105-133). Positions past the block table and block ids
+    outside the pool are skipped.
+
+    * 16-bit caches (no scales): the new slots take the tokens as given.
+    * FP8 caches (uint8 e4m3 codes) with per-head scales [Hkv]: the new slots
+      take e4m3(x / s[h]), values beyond +-448 saturated.
+    * FP8 caches with per-(page, head) scales [num_blocks, Hkv]: every page the
+      append touches is quantised again over its valid slots (old slots
+      decoded with the page's old scale, new slots as given), with scale =
+      max(amax / 448, 1e-8) and codes e4m3(x / scale) — the recipe of
+      tests/test_kernels_misc.py:52-55 applied per page, as the C4 benchmark
+      cache is built; the page's unused slots are written as code 0.
+
+    Returns new arrays (key_cache, value_cache, k_scale, v_scale); the scales
+    are None for a 16-bit cache.
+    """
+    from .fp8 import E4M3_MAX, e4m3_encode
+
+    key, value = np.asarray(key), np.asarray(value)
+    kc, vc = np.array(key_cache, copy=True), np.array(value_cache, copy=True)
+    fp8 = k_scale is not None
+    ks = None if k_scale is None else np.array(k_scale, dtype=np.float32, copy=True)
+    vs = None if v_scale is None else np.array(v_scale, dtype=np.float32, copy=True)
+    n_seq, hkv, t_max, d = key.shape
+    page = kc.shape[-1]
+    max_blocks = block_tables.shape[1]
+    num_blocks = kc.shape[0]
+    lens = np.asarray(context_lens).astype(np.int64)
+    news = np.full(n_seq, t_max) if new_lens is None else np.clip(np.asarray(new_lens), 0, t_max)
+
+    def enc(x):
+        x = np.clip(np.asarray(x, dtype=np.float32), -E4M3_MAX, E4M3_MAX)
+        return e4m3_encode(x)
+
+    for n in range(n_seq):
+        lo = max(0, int(lens[n]))
+        hi = min(lo + int(news[n]), max_blocks * page)
+        if lo >= hi:
+            continue
+        for p in range(lo // page, (hi - 1) // page + 1):
+            blk = int(block_tables[n, p])
+            if blk < 0 or blk >= num_blocks:
+                continue
+            p0 = p * page
+            for cache, src, sc in ((kc, key, ks), (vc, value, vs)):
+                for h in range(hkv):
+                    if not fp8:
+                        for s in range(page):
+                            pos = p0 + s
+                            if lo <= pos < hi:
+                                cache[blk, h, :, s] = src[n, h, pos - lo]
+                    elif sc.ndim == 1:
+                        for s in range(page):
+                            pos = p0 + s
+                            if lo <= pos < hi:
+                                cache[blk, h, :, s] = enc(src[n, h, pos - lo].astype(np.float32)
+                                                          / sc[h])
+                    else:
+                        vals = np.zeros((d, page), dtype=np.float32)
+                        old_scale = sc[blk, h]
+                        for s in range(page):
+                            pos = p0 + s
+                            if pos < lo:
+                                vals[:, s] = e4m3_decode(cache[blk, h, :, s]) * old_scale
+                            elif pos < hi:
+                                vals[:, s] = src[n, h, pos - lo].astype(np.float32)
+                        amax = np.abs(vals).max()
+                        scale = np.float32(max(np.float32(amax) / np.float32(E4M3_MAX),
+                                               np.float32(1e-8)))
+                        codes = enc(vals / scale)
+                        valid = (p0 + np.arange(page)) < hi
+                        cache[blk, h] = np.where(valid[None, :], codes, 0).astype(np.uint8)
+                        sc[blk, h] = scale
+    return kc, vc, ks, vs

@@ -109,6 +109,27 @@ def test_backward_entry_points_validate():
     assert b"lse" in lib.ca_last_error()
 
 
+def test_kv_append_validates():
+    lib = L.load()
+    args = [L.CA_BF16, 0, P, P, P, P, None, None, 0, P, P, None, 2, 2, 128, 4, 8, 100, None]
+    bad_kind = list(args)
+    bad_kind[1] = 5
+    assert _status("ca_paged_kv_append", *bad_kind) == L.CA_INVALID_ARGUMENT
+    fp8_no_scale = list(args)
+    fp8_no_scale[1] = 1
+    assert _status("ca_paged_kv_append", *fp8_no_scale) == L.CA_INVALID_ARGUMENT
+    assert b"k_scale" in lib.ca_last_error()
+    f32 = list(args)
+    f32[0] = L.CA_F32
+    assert _status("ca_paged_kv_append", *f32) == L.CA_UNSUPPORTED
+    bad_d = list(args)
+    bad_d[14] = 96
+    assert _status("ca_paged_kv_append", *bad_d) == L.CA_INVALID_ARGUMENT
+    nothing = list(args)
+    nothing[15] = 0
+    assert _status("ca_paged_kv_append", *nothing) == L.CA_OK
+
+
 def test_paged_rejects_bad_arguments():
     args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
     bad_page = list(args)

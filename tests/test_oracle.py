@@ -373,3 +373,126 @@ def test_planted_backward_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(oattn, "attention_backward", dropped_d)
     dq, _, _ = oattn.attention_backward(dout, q, k, v, o, lse, is_causal=True, dtype=np.float64)
     assert np.abs(dq - gq).max() > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# paged append
+# ---------------------------------------------------------------------------
+def _append_case(rng, n=3, hkv=2, d=16, lens=(37, 16, 5), extra=4):
+    t = max(lens)
+    k = rng.standard_normal((n, hkv, t, d)).astype(np.float32)
+    v = rng.standard_normal((n, hkv, t, d)).astype(np.float32)
+    bps = (t + 15) // 16 + extra
+    perm = rng.permutation(n * bps)
+    tables = perm.reshape(n, bps).astype(np.int32)
+    return k, v, tables, np.asarray(lens)
+
+
+def test_append_whole_sequences_equals_make_paged_cache():
+    rng = np.random.default_rng(21)
+    k, v, tables, lens = _append_case(rng, extra=0)
+    n, hkv, t, d = k.shape
+    kc0 = np.zeros((tables.size, hkv, d, 16), np.float32)
+    kc, vc, _, _ = oracle.paged_append(k, v, kc0, kc0, tables, np.zeros(n, np.int32), lens)
+    ref_k, ref_v, _ = oracle.make_paged_cache(k, v, 16, perm=tables.reshape(-1))
+    for i in range(n):
+        for p in range((lens[i] + 15) // 16):
+            blk = tables[i, p]
+            for s in range(16):
+                if p * 16 + s < lens[i]:
+                    np.testing.assert_array_equal(kc[blk, :, :, s], ref_k[blk, :, :, s])
+                    np.testing.assert_array_equal(vc[blk, :, :, s], ref_v[blk, :, :, s])
+
+
+def test_append_token_by_token_equals_all_at_once():
+    rng = np.random.default_rng(22)
+    k, v, tables, lens = _append_case(rng)
+    n, hkv, t, d = k.shape
+    zero = np.zeros((tables.size, hkv, d, 16), np.float32)
+    full_k, full_v, _, _ = oracle.paged_append(k, v, zero, zero, tables, np.zeros(n, np.int32), lens)
+    kc, vc = zero.copy(), zero.copy()
+    for step in range(t):
+        new = (lens > step).astype(np.int32)
+        kc, vc, _, _ = oracle.paged_append(k[:, :, step:step + 1], v[:, :, step:step + 1], kc, vc,
+                                           tables, np.minimum(lens, step), new)
+    np.testing.assert_array_equal(kc, full_k)
+    np.testing.assert_array_equal(vc, full_v)
+
+
+def test_append_fp8_per_page_equals_reference_recipe():
+    """Whole sequences into empty pages == quantize_per_page_fp8 of the paged
+    cache (the reference recipe, per page), unused slots zero."""
+    rng = np.random.default_rng(23)
+    k, v, tables, lens = _append_case(rng, extra=0)
+    n, hkv, t, d = k.shape
+    kz = np.zeros((tables.size, hkv, d, 16), np.uint8)
+    sz = np.ones((tables.size, hkv), np.float32)
+    kc, vc, ks, vs = oracle.paged_append(k, v, kz, kz, tables, np.zeros(n, np.int32), lens,
+                                         k_scale=sz, v_scale=sz)
+    masked_k = k.copy()
+    masked_v = v.copy()
+    for i in range(n):
+        masked_k[i, :, lens[i]:] = 0
+        masked_v[i, :, lens[i]:] = 0
+    pk, pv, _ = oracle.make_paged_cache(masked_k, masked_v, 16, perm=tables.reshape(-1))
+    ck, sk = oracle.quantize_per_page_fp8(pk)
+    cv, sv = oracle.quantize_per_page_fp8(pv)
+    np.testing.assert_array_equal(kc, ck)
+    np.testing.assert_array_equal(vc, cv)
+    used = np.concatenate([tables[i, :(lens[i] + 15) // 16] for i in range(n)])
+    np.testing.assert_array_equal(ks[used], sk[used])  # pages never touched keep their scale
+    np.testing.assert_array_equal(vs[used], sv[used])
+
+
+def test_append_fp8_per_page_incremental_when_first_chunk_holds_the_max():
+    """If a page's first append already holds its largest magnitude, appending
+    the rest later re-derives the same codes: equal to one append, bit-exact."""
+    rng = np.random.default_rng(24)
+    k, v, tables, lens = _append_case(rng, lens=(32, 32, 32), extra=0)
+    k[:, :, 0::16, 0] = 50.0  # slot 0 of every page carries the page max
+    v[:, :, 0::16, 0] = -50.0
+    n, hkv, t, d = k.shape
+    kz = np.zeros((tables.size, hkv, d, 16), np.uint8)
+    sz = np.ones((tables.size, hkv), np.float32)
+    one = oracle.paged_append(k, v, kz, kz, tables, np.zeros(n, np.int32), lens, k_scale=sz, v_scale=sz)
+    a = oracle.paged_append(k[:, :, :5], v[:, :, :5], kz, kz, tables, np.zeros(n, np.int32), None,
+                            k_scale=sz, v_scale=sz)
+    b = oracle.paged_append(k[:, :, 5:], v[:, :, 5:], a[0], a[1], tables, np.full(n, 5, np.int32),
+                            None, k_scale=a[2], v_scale=a[3])
+    for x, y in zip(one, b):
+        np.testing.assert_array_equal(x, y)
+
+
+def test_append_fp8_per_head_equals_reference_recipe():
+    rng = np.random.default_rng(25)
+    k, v, tables, lens = _append_case(rng, extra=0)
+    n, hkv, t, d = k.shape
+    s = np.array([0.01, 0.02], np.float32)
+    kz = np.zeros((tables.size, hkv, d, 16), np.uint8)
+    kc, _, _, _ = oracle.paged_append(k, v, kz, kz, tables, np.zeros(n, np.int32), lens,
+                                      k_scale=s, v_scale=s)
+    for i in range(n):
+        for pos in range(lens[i]):
+            blk, slot = tables[i, pos // 16], pos % 16
+            for h in range(hkv):
+                want = torch.from_numpy(np.clip(k[i, h, pos] / s[h], -448, 448)).to(
+                    torch.float8_e4m3fn).view(torch.uint8).numpy()
+                np.testing.assert_array_equal(kc[blk, h, :, slot], want)
+
+
+def test_append_skips_out_of_range_blocks_and_positions():
+    rng = np.random.default_rng(26)
+    k, v, tables, _ = _append_case(rng, lens=(20, 20, 20), extra=0)
+    n, hkv, t, d = k.shape
+    tables = tables.copy()
+    tables[0, 1] = -1          # invalid block: its tokens are dropped
+    zero = np.zeros((tables.size, hkv, d, 16), np.float32)
+    kc, _, _, _ = oracle.paged_append(k, v, zero, zero, tables, np.array([0, 20, 30]), None)
+    # sequence 0: page 1 (positions 16..31) has block -1 and is dropped
+    np.testing.assert_array_equal(kc[tables[0, 0], :, :, :], k[0, :, :16].transpose(0, 2, 1))
+    # sequence 1 (table of 2 pages = 32 positions): positions 20..31 fit, 32..39 are dropped
+    # sequence 2 starts at 30: positions 30, 31 fit
+    blk = tables[1, 1]
+    np.testing.assert_array_equal(kc[blk, :, :, 4:16], k[1, :, :12].transpose(0, 2, 1))
+    assert np.all(kc[tables[1, 0]] == 0)
+    np.testing.assert_array_equal(kc[tables[2, 1], :, :, 14:16], k[2, :, :2].transpose(0, 2, 1))
