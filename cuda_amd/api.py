@@ -26,7 +26,7 @@ from . import _lib
 __all__ = [
     "flash_attention", "flash_attention_forward", "flash_attention_v3_hopper",
     "flash_attention_forward_lse", "flash_attention_backward",
-    "fused_gqa_forward", "flash_decode", "async_flash_decode", "paged_attention",
+    "fused_gqa_forward", "fused_rope_flash_attention", "flash_decode", "async_flash_decode", "paged_attention",
     "paged_attention_forward", "fp8_paged_attention", "fp8_paged_attention_forward",
     "fused_microscaled_attention", "mx_scales_to_e8m0", "paged_kv_append",
 ]
@@ -191,6 +191,28 @@ flash_attention_v3_hopper = flash_attention_forward
 def fused_gqa_forward(q, k, v, is_causal=True, softmax_scale=None):
     """GQA prefill (fused_softmax_binding.cpp:246-302; default causal)."""
     return flash_attention_forward(q, k, v, is_causal=is_causal, softmax_scale=softmax_scale)
+
+
+def fused_rope_flash_attention(q, k, v, cos_tab, sin_tab, is_causal=True, softmax_scale=None):
+    """Prefill on RoPE-rotated q and k (fused_softmax_binding.cpp:179-241):
+    rotate-half convention, cos_tab / sin_tab [seq_len, head_dim] (converted
+    to contiguous float32 as the reference does); q, k, v as
+    flash_attention_forward (GQA allowed)."""
+    _check(cos_tab.is_cuda and sin_tab.is_cuda, "RoPE tables must be on CUDA")
+    _prefill_checks(q, k, v)
+    b, hq, s, d = q.shape
+    _check(tuple(cos_tab.shape) == (s, d) and tuple(sin_tab.shape) == (s, d),
+           "RoPE tables must be [seq_len, head_dim]")
+    dt = _dtype_code(q, "Fused RoPE Attention")
+    q, k, v = _aligned(q), _aligned(k), _aligned(v)
+    cos_f, sin_f = (t.to(torch.float32).contiguous() for t in (cos_tab, sin_tab))
+    out = torch.empty_like(q)
+    hkv = k.shape[1]
+    ws, nbytes = _workspace(int(_lib.load().ca_rope_workspace_bytes(dt, b, hq, hkv, s, d)), q.device)
+    _lib.call("ca_fused_rope_flash_attention", dt, _ptr(q), _ptr(k), _ptr(v), _ptr(cos_f),
+              _ptr(sin_f), _ptr(out), b, hq, hkv, s, d, _scale(softmax_scale, d),
+              int(bool(is_causal)), _ptr(ws), nbytes, _stream())
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -285,6 +285,45 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
                   what);
 }
 
+size_t ca_rope_workspace_bytes(ca_dtype dtype, int batch, int num_q_heads, int num_kv_heads,
+                               int seq_len, int head_dim) {
+  if (batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || seq_len <= 0 || head_dim <= 0)
+    return 0;
+  return ca::rope_workspace_bytes((int)dtype, batch, num_q_heads, num_kv_heads, seq_len,
+                                  head_dim);
+}
+
+ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const void* k,
+                                        const void* v, const float* cos_tab, const float* sin_tab,
+                                        void* o, int batch, int num_q_heads, int num_kv_heads,
+                                        int seq_len, int head_dim, float softmax_scale,
+                                        int is_causal, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  const char* what = "fused_rope_flash_attention";
+  ca_status st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
+  if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
+  if (batch < 0 || seq_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
+  if (batch == 0 || seq_len == 0) return CA_OK;
+  if (!q || !k || !v || !o || !cos_tab || !sin_tab)
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace))
+    return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
+  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  const size_t need = ca::rope_workspace_bytes((int)dtype, batch, num_q_heads, num_kv_heads,
+                                               seq_len, head_dim);
+  if (workspace_bytes < need || !workspace)
+    return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
+                workspace_bytes);
+  return from_hip(ca::launch_rope_prefill((int)dtype, q, k, v, cos_tab, sin_tab, o, batch,
+                                          num_q_heads, num_kv_heads, seq_len, head_dim,
+                                          softmax_scale, is_causal != 0, workspace,
+                                          (hipStream_t)stream),
+                  what);
+}
+
 ca_status ca_paged_kv_append(ca_dtype dtype, int cache_kind, const void* key, const void* value,
                              void* key_cache, void* value_cache, float* k_scale, float* v_scale,
                              int per_block_scales, const int32_t* block_tables,

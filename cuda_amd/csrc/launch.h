@@ -98,6 +98,13 @@ hipError_t launch_kv_append(int dtype, int kind, const void* key, const void* va
                             const int32_t* context_lens, const int32_t* new_lens, int N, int Hkv,
                             int D, int T, int max_blocks, int num_blocks, hipStream_t stream);
 
+// RoPE + prefill (rope.hip): q and k rotated into ws, then launch_prefill.
+size_t rope_workspace_bytes(int dtype, int B, int Hq, int Hkv, int S, int D);
+hipError_t launch_rope_prefill(int dtype, const void* q, const void* k, const void* v,
+                               const float* cos_tab, const float* sin_tab, void* o, int B, int Hq,
+                               int Hkv, int S, int D, float scale, bool causal, void* ws,
+                               hipStream_t stream);
+
 // MXFP8 attention: e4m3 q/k/v [B, H, S, D] with e8m0 scale bytes [B, H, S, D/32].
 hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                         const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,

@@ -81,6 +81,23 @@ ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, c
 /* Bytes of the ca_flash_attention_bwd workspace (the rowsum(dout * o) terms). */
 size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int seq_len);
 
+/* Prefill forward on RoPE-rotated q and k (rotate-half convention):
+ * x'[c] = x[c] cos[s][c] + r[c] sin[s][c], r = [-x[D/2:], x[:D/2]], for the
+ * token at position s; cos_tab, sin_tab: float32 [seq_len, head_dim]. Shapes,
+ * masking and dtypes as ca_flash_attention_fwd (GQA allowed).
+ * Replaces dispatch_fused_rope_flash_attention<T> (kernels_api.h:44-49).
+ * workspace: ca_rope_workspace_bytes(...) (the rotated q and k). */
+ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const void* k,
+                                        const void* v, const float* cos_tab, const float* sin_tab,
+                                        void* o, int batch, int num_q_heads, int num_kv_heads,
+                                        int seq_len, int head_dim, float softmax_scale,
+                                        int is_causal, void* workspace, size_t workspace_bytes,
+                                        void* stream);
+
+/* Bytes of the ca_fused_rope_flash_attention workspace. */
+size_t ca_rope_workspace_bytes(ca_dtype dtype, int batch, int num_q_heads, int num_kv_heads,
+                               int seq_len, int head_dim);
+
 /* Append new tokens to a paged KV cache, in place: the step before paged
  * decode. key, value: [num_seqs, num_kv_heads, max_new_tokens, head_dim] of
  * `dtype` (bf16/fp16); sequence n appends its first new_lens[n] tokens

@@ -27,6 +27,9 @@ Pinning (what checks each function; see ``tests/test_oracle.py``):
                                      token-by-token == all at once,
                                      quantize_per_page_fp8 of the built cache,
                                      the per-head e4m3(x / s) recipe
+  apply_rope / rope_attention        the complex-number form of the rotation,
+                                     norm preservation, position 0 = identity,
+                                     torch SDPA of the rotated tensors
   attention_backward                 torch autograd (CPU, fp64) of SDPA,
                                      central finite differences of
                                      ``attention`` (fp64), the one-key closed
@@ -36,14 +39,14 @@ the reference declares ``dispatch_fused_microscaled_attention``
 (kernels_api.h:103-108) but ships no kernel, binding or test for it, so the
 oracle follows the OCP MX v1.0 definition instead of a reference vector.
 """
-from .attention import (attention, attention_backward, attention_lse, attention_tiled,
-                        decode, default_scale, split_merge)
+from .attention import (apply_rope, attention, attention_backward, attention_lse,
+                        attention_tiled, decode, default_scale, rope_attention, split_merge)
 from .fp8 import (E4M3_MAX, e4m3_decode, e4m3_encode, e8m0_decode,
                   mx_dequantize, mx_quantize, quantize_per_page_fp8)
 from .paged import gather_paged, make_paged_cache, paged_append, paged_decode
 
 __all__ = [
-    "attention", "attention_backward", "attention_lse", "attention_tiled", "decode", "default_scale",
+    "apply_rope", "rope_attention", "attention", "attention_backward", "attention_lse", "attention_tiled", "decode", "default_scale",
     "split_merge", "E4M3_MAX", "e4m3_decode", "e4m3_encode", "e8m0_decode",
     "mx_dequantize", "mx_quantize", "quantize_per_page_fp8", "gather_paged",
     "make_paged_cache", "paged_append", "paged_decode",

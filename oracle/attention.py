@@ -11,6 +11,7 @@ Reference anchors
 * default scale      fused_softmax_binding.cpp:69-72  1/sqrt(head_dim)
 * empty softmax row  flash_attention_v2_kernel.cuh:223  l == 0 -> output 0
 * online softmax     flash_attention_v2_kernel.cuh:179-229 (running max / sum)
+* RoPE               tests/_utils.py:75-94 (rotate-half tables and rotation)
 * backward           flash_attention_bwd_kernel.cuh:9-19, 96-214 (dQ, dK, dV from
                      the forward's LSE; D_i = rowsum(dO * O))
 """
@@ -152,6 +153,25 @@ def attention_backward(dout, q, k, v, out, lse, is_causal=False, scale=None,
             dk[i, kh] += ds.T @ qh
             dv[i, kh] += p.T @ do
     return dq, dk, dv
+
+
+def apply_rope(x, cos, sin):
+    """Rotate-half RoPE (tests/_utils.py:84-89, ``apply_rope``; kernel
+    fused_rope_flash_attention_kernel.cuh:60-70,98-108): x [..., S, D],
+    cos / sin [S, D] -> x * cos + rot(x) * sin with rot(x) = [-x[D/2:], x[:D/2]],
+    in float32."""
+    x = np.asarray(x, dtype=np.float32)
+    half = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., half:], x[..., :half]], axis=-1)
+    return (x * np.asarray(cos, dtype=np.float32) + rot * np.asarray(sin, dtype=np.float32)).astype(
+        np.float32)
+
+
+def rope_attention(q, k, v, cos, sin, is_causal=True, scale=None, dtype=np.float32):
+    """Attention on RoPE-rotated q and k (tests/_utils.py:92-94,
+    ``ref_rope_attention``)."""
+    return attention(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v, is_causal=is_causal,
+                     scale=scale, dtype=dtype)
 
 
 def decode(q, k, v, context_lens, scale=None, dtype=np.float32):

@@ -109,6 +109,20 @@ def test_backward_entry_points_validate():
     assert b"lse" in lib.ca_last_error()
 
 
+def test_rope_entry_validates():
+    lib = L.load()
+    n = lib.ca_rope_workspace_bytes(L.CA_BF16, 2, 8, 2, 100, 64)
+    assert n == ((2 * 8 * 100 * 64 * 2 + 255) // 256) * 256 + 2 * 2 * 100 * 64 * 2
+    args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 100, 64, 0.1, 1, P, n, None]
+    small = list(args)
+    small[15] = n - 1
+    assert _status("ca_fused_rope_flash_attention", *small) == L.CA_INVALID_ARGUMENT
+    assert b"workspace" in lib.ca_last_error()
+    no_tab = list(args)
+    no_tab[4] = None
+    assert _status("ca_fused_rope_flash_attention", *no_tab) == L.CA_INVALID_ARGUMENT
+
+
 def test_kv_append_validates():
     lib = L.load()
     args = [L.CA_BF16, 0, P, P, P, P, None, None, 0, P, P, None, 2, 2, 128, 4, 8, 100, None]

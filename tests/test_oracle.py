@@ -496,3 +496,53 @@ def test_append_skips_out_of_range_blocks_and_positions():
     np.testing.assert_array_equal(kc[blk, :, :, 4:16], k[1, :, :12].transpose(0, 2, 1))
     assert np.all(kc[tables[1, 0]] == 0)
     np.testing.assert_array_equal(kc[tables[2, 1], :, :, 14:16], k[2, :, :2].transpose(0, 2, 1))
+
+
+# ---------------------------------------------------------------------------
+# RoPE (rotate-half, tests/_utils.py:75-94)
+# ---------------------------------------------------------------------------
+def _rope_tables(s, d, base=10000.0):
+    """cos / sin [S, D] as tests/_utils.py:75-81 builds them."""
+    inv = 1.0 / (base ** (np.arange(0, d, 2, dtype=np.float64) / d))
+    ang = np.outer(np.arange(s, dtype=np.float64), inv)
+    emb = np.concatenate([ang, ang], axis=-1)
+    return np.cos(emb).astype(np.float32), np.sin(emb).astype(np.float32), ang
+
+
+def test_rope_equals_complex_rotation():
+    """Rotate-half RoPE is the complex product (x_c + i x_{c+D/2}) e^{i theta_c}."""
+    rng = np.random.default_rng(31)
+    s, d = 50, 64
+    x = rng.standard_normal((2, 3, s, d)).astype(np.float32)
+    cos, sin, ang = _rope_tables(s, d)
+    got = oracle.apply_rope(x, cos, sin)
+    z = (x[..., : d // 2] + 1j * x[..., d // 2:]) * np.exp(1j * ang)
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    np.testing.assert_allclose(got, want, atol=2e-5, rtol=0)
+
+
+def test_rope_preserves_pair_norms_and_position_zero():
+    rng = np.random.default_rng(32)
+    s, d = 40, 128
+    x = rng.standard_normal((1, 2, s, d)).astype(np.float32)
+    cos, sin, _ = _rope_tables(s, d)
+    y = oracle.apply_rope(x, cos, sin)
+    h = d // 2
+    np.testing.assert_allclose(x[..., :h] ** 2 + x[..., h:] ** 2, y[..., :h] ** 2 + y[..., h:] ** 2,
+                               rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(y[:, :, 0], x[:, :, 0], atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_rope_attention_vs_torch_sdpa(causal):
+    rng = np.random.default_rng(33)
+    s, d = 70, 64
+    q, k, v = (rng.standard_normal((1, 4, s, d)).astype(np.float32) for _ in range(3))
+    cos, sin, _ = _rope_tables(s, d)
+    tq, tk = (torch.from_numpy(x) for x in (q, k))
+    tc, ts = torch.from_numpy(cos), torch.from_numpy(sin)
+    rot = lambda t: torch.cat([-t[..., d // 2:], t[..., : d // 2]], dim=-1)  # noqa: E731
+    ref = F.scaled_dot_product_attention(tq * tc + rot(tq) * ts, tk * tc + rot(tk) * ts,
+                                         torch.from_numpy(v), is_causal=causal)
+    np.testing.assert_allclose(oracle.rope_attention(q, k, v, cos, sin, is_causal=causal),
+                               ref.numpy(), atol=2e-5, rtol=0)
