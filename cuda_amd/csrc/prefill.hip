@@ -327,6 +327,9 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 #ifndef CA_PF_AG
 #define CA_PF_AG 0
 #endif
+#ifndef CA_PF_PVX
+#define CA_PF_PVX 0
+#endif
 #ifndef CA_PF_PRIO
 #define CA_PF_PRIO 1
 #endif
@@ -598,10 +601,13 @@ __device__ CA_INLINE void prefill_d128_qtile(
       // V^T fragments of VD k-steps in flight ahead of the MFMAs (ring of VD + 1)
       constexpr int VD = CA_PF_VDEPTH;
       u32x2 vr[VD + 1][2];
-      // step st: O^T block ob = st / 4, P^T k-step kk = st % 4
+      // step st: O^T block ob, P^T k-step kk; with PVX consecutive MFMAs go
+      // to different accumulators (a lone wave then issues them back to back)
+      auto st_ob = [](int st) CA_INLINE { return CA_PF_PVX ? (st & 3) : (st >> 2); };
+      auto st_kk = [](int st) CA_INLINE { return CA_PF_PVX ? (st >> 2) : (st & 3); };
       auto vread = [&](int st, int buf) CA_INLINE {
-        const uint32_t x = 64 * (st >> 2);
-        switch (st & 3) {
+        const uint32_t x = 64 * st_ob(st);
+        switch (st_kk(st)) {
           case 0: vr[buf][0] = lds_read_tr16<0>(va1 ^ x); vr[buf][1] = lds_read_tr16<0>(va2 ^ x); break;
           case 1: vr[buf][0] = lds_read_tr16<4096>(va1 ^ x); vr[buf][1] = lds_read_tr16<4096>(va2 ^ x); break;
           case 2: vr[buf][0] = lds_read_tr16<8192>(va1 ^ x); vr[buf][1] = lds_read_tr16<8192>(va2 ^ x); break;
@@ -617,7 +623,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
         wait_lgkm_n(2 * (VD < 15 - st ? VD : 15 - st));  // step st landed
         after_wait(vr[cb][0]);
         after_wait(vr[cb][1]);
-        const int ob = st >> 2, kk = st & 3;
+        const int ob = st_ob(st), kk = st_kk(st);
         u32x4 w4 = {vr[cb][0][0], vr[cb][0][1], vr[cb][1][0], vr[cb][1][1]};
         const vec8 a = __builtin_bit_cast(vec8, w4);
 #pragma unroll
