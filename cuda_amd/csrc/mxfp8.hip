@@ -32,11 +32,13 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
   return __uint_as_float(e << 23);
 }
 
+// One query tile (BM rows of head bh): the key walk and the output store.
+// Other waves may still read the LDS tiles when a wave returns.
 template <typename Tr, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
+__device__ CA_INLINE void mxfp8_qtile(
     const uint8_t* __restrict__ Q, const uint8_t* __restrict__ QS, const uint8_t* __restrict__ K,
     const uint8_t* __restrict__ KSc, const uint8_t* __restrict__ V, const uint8_t* __restrict__ VSc,
-    uint16_t* __restrict__ O, int S, int H, float scale_log2, int n_qt) {
+    uint16_t* __restrict__ O, int S, float scale_log2, int bh, int qt) {
   using vec8 = BF16::vec8;
   using vec4 = BF16::vec4;
   using vec2 = BF16::vec2;
@@ -53,9 +55,6 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
   __shared__ __attribute__((aligned(16))) uint32_t Kscl[2][BN];  // 4 e8m0 bytes per key
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * VS];
 
-  const int work = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = work / n_qt;
-  const int qt = n_qt - 1 - (work % n_qt);
   const int q0 = qt * BM;
   const size_t base = (size_t)bh * S;
   const uint8_t* Qp = Q + base * D;
@@ -160,6 +159,7 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
     f32x16 s[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[0][r] = 0.f; s[1][r] = 0.f; }
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int row = 32 * mb + krow;
@@ -173,6 +173,9 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
         s[mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qv[st], s[mb], 0, 0, 0, ksc, 0, qsc[st]);
       }
     }
+    // (the MFMA blocks run at raised wave priority: a wave's MFMAs then win
+    // issue over the other waves' softmax VALU)
+    __builtin_amdgcn_s_setprio(0);
 
     float x[32];
 #pragma unroll
@@ -227,6 +230,7 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
     }
     l_run += psum;
 
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ob = 0; ob < NOB; ++ob) {
 #pragma unroll
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
         o[ob] = BF16::mfma32(cat4<vec8, vec4>(lo, hi), pb[kk], o[ob]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   }
 
   const float l_tot = pair32_sum(l_run);
@@ -259,18 +264,37 @@ __global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
   }
 }
 
+template <typename Tr, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void mxfp8_fwd_kernel(
+    const uint8_t* __restrict__ Q, const uint8_t* __restrict__ QS, const uint8_t* __restrict__ K,
+    const uint8_t* __restrict__ KSc, const uint8_t* __restrict__ V, const uint8_t* __restrict__ VSc,
+    uint16_t* __restrict__ O, int S, float scale_log2, int n_qt, int n_bh, int n_work,
+    int paired) {
+  const QTileWork wk = prefill_work(xcd_remap(blockIdx.x, n_work), n_qt, n_bh, paired);
+  const int n_pass = wk.qt1 < 0 ? 1 : 2;
+#pragma clang loop unroll(disable)
+  for (int pass = 0; pass < n_pass; ++pass) {
+    // the second tile restages the LDS buffers: every wave must be done reading them
+    if (pass) __syncthreads();
+    mxfp8_qtile<Tr, CAUSAL>(Q, QS, K, KSc, V, VSc, O, S, scale_log2, pass ? wk.bh1 : wk.bh0,
+                            pass ? wk.qt1 : wk.qt0);
+  }
+}
+
 hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                         const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,
                         int H, int S, int D, float scale, bool causal, hipStream_t stream) {
   if (D != 128) return hipErrorInvalidValue;
   constexpr int BM = 128;
   const int n_qt = (S + BM - 1) / BM;
-  const long long grid = (long long)n_qt * B * H;
+  int paired = 0;
+  const long long grid = prefill_grid(B, H, n_qt, causal, 2, &paired);
   if (grid == 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const float sl2 = scale * kLog2e;
 #define CA_MX(TR, C)                                                                         \
   hipLaunchKernelGGL((mxfp8_fwd_kernel<TR, C>), dim3((unsigned)grid), dim3(256), 0, stream, q, \
-                     qs, k, ks, v, vs, (uint16_t*)o, S, H, sl2, n_qt);
+                     qs, k, ks, v, vs, (uint16_t*)o, S, sl2, n_qt, B * H, (int)grid, paired);
   if (out_dtype == kDtypeBF16) {
     if (causal) { CA_MX(BF16, true) } else { CA_MX(BF16, false) }
   } else if (out_dtype == kDtypeF16) {
