@@ -34,6 +34,14 @@
 
 namespace ca {
 
+// Head-dim-128 kernel: MFMA blocks run at raised wave priority (s_setprio),
+// so a wave's MFMAs win issue over its partner wave's softmax VALU on the same
+// SIMD (+1-2.5 % measured; the head-dim-64 kernel, whose SIMDs hold waves of
+// independent workgroups, measured 2 % slower with it and does not use it).
+#ifndef CA_PF_PRIO
+#define CA_PF_PRIO 1
+#endif
+
 // One query tile (BM rows of head bh): the whole key walk and the output
 // store. Other waves may still read the LDS tiles when a wave returns.
 template <typename Tr, int D, int NW, bool CAUSAL>
@@ -330,9 +338,6 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 #ifndef CA_PF_PVX
 #define CA_PF_PVX 0
 #endif
-#ifndef CA_PF_PRIO
-#define CA_PF_PRIO 1
-#endif
 #ifndef CA_PF_KDEPTH
 #define CA_PF_KDEPTH 1
 #endif
@@ -544,8 +549,6 @@ __device__ CA_INLINE void prefill_d128_qtile(
         for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) sacc[mb][nb][r] = 0.f;
-      // MFMA blocks run at raised wave priority, so a wave's MFMAs win issue
-      // over the partner wave's softmax VALU (+1-2.5 % measured)
       if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(1);
       const uint32_t ka = stage(tn) + kofs;
       // K fragments of KD k-steps in flight ahead of the MFMAs (ring of KD + 1)
