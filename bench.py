@@ -13,7 +13,8 @@ e4m3 cache with per-(page, kv-head) fp32 scales). Its algorithmic bytes are
 the K/V codes of the context tokens, the scales of the pages read, q, out and
 the block-table entries. "extra" holds the other BASELINE configs (C2'
 non-causal prefill, C3 bf16 paged decode, C5 MXFP8) and a plain copy used to
-calibrate HBM counters.
+calibrate HBM counters. Decode lines also carry the measured streaming-read
+ceiling (``ca_stream_read`` over a 4 GiB buffer) as "measured_read_peak".
 
 Timing: W untimed warm-up steps, then K steps between HIP events recorded on
 the stream the kernels run on (torch's current stream), bracketed by device
@@ -21,7 +22,7 @@ synchronisation. ``cpu_baseline`` times the numpy oracle on a bounded sample
 of the same inputs on this host's cores (a reported baseline only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|copy]
+                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|backward|copy|read]
 """
 import argparse
 import json
@@ -283,6 +284,37 @@ def w_copy(steps, warmup, nbytes=2 << 30):
                 config={"workload": "device copy (HBM counter calibration)", "bytes": nbytes})
 
 
+def w_read(steps, warmup, nbytes=4 << 30):
+    """Streaming-read ceiling: ca_stream_read over a resident buffer (the
+    measured second denominator of the HBM-bound decode lines)."""
+    import ctypes
+    import torch
+    from cuda_amd import _lib
+    x = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").random_(generator=_gen())
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    fn = lambda: _lib.call("ca_stream_read", ctypes.c_void_p(x.data_ptr()), nbytes,
+                           ctypes.c_void_p(sink.data_ptr()), st)
+    ms = time_steps(fn, steps, warmup)
+    return dict(ms=ms, value=nbytes / (ms * 1e-3) / 1e9, unit="GB/s", bound="hbm",
+                peak=PEAK_HBM_GBS, work=nbytes,
+                config={"workload": "streaming read (measured HBM read ceiling)", "bytes": nbytes})
+
+
+_READ_CEILING = {}
+
+
+def read_ceiling(steps, warmup):
+    """Measured streaming-read GB/s, once per process."""
+    import torch
+    if "gbs" not in _READ_CEILING:
+        r = w_read(min(steps, 50), min(warmup, 20))
+        _READ_CEILING["gbs"] = r["value"]
+        log(f"read ceiling: {r['value']:.1f} GB/s")
+        torch.cuda.empty_cache()
+    return _READ_CEILING["gbs"]
+
+
 WORKLOADS = {
     "prefill": lambda s, w: w_prefill(s, w, causal=True),
     "prefill_nc": lambda s, w: w_prefill(s, w, causal=False, S=2048),
@@ -291,17 +323,24 @@ WORKLOADS = {
     "mxfp8": w_mxfp8,
     "backward": w_backward,
     "copy": w_copy,
+    "read": w_read,
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
                "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5"}
 
 
-def summary(name, r):
+def summary(name, r, read_gbs=None):
+    """One result object. For an HBM-bound decode line, `read_gbs` (the
+    measured streaming-read ceiling) is reported beside the nominal peak as a
+    second denominator."""
     out = {"value": round(r["value"], 2), "unit": r["unit"], "ms_per_step": round(r["ms"], 4),
            "config": r["config"],
            "roofline": {"bound": r["bound"], "achieved": round(r["value"], 2), "peak": r["peak"],
                         "unit": r["unit"], "frac": round(r["value"] / r["peak"], 4),
                         "traffic": _traffic(TRAFFIC_KEY.get(name, name))}}
+    if read_gbs:
+        out["roofline"]["measured_read_peak"] = round(read_gbs, 2)
+        out["roofline"]["frac_of_measured"] = round(r["value"] / read_gbs, 4)
     return out
 
 
@@ -332,7 +371,8 @@ def main():
     log(f"{head} ...")
     r = WORKLOADS[head](args.steps, args.warmup)
     log(f"{head}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
-    s = summary(head, r)
+    is_decode = head.startswith("decode")
+    s = summary(head, r, read_ceiling(args.steps, args.warmup) if is_decode else None)
     line = {
         "metric": {"prefill": "prefill TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
                    "prefill_nc": "prefill TFLOP/s (bf16 non-causal, B=4 H=32 S=2048 D=128)",
@@ -340,13 +380,14 @@ def main():
                    "decode_bf16": "bf16 paged GQA decode HBM GB/s (C3)",
                    "mxfp8": "MXFP8 causal attention TFLOP/s (C5)",
                    "backward": "prefill backward TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
-                   "copy": "device copy GB/s"}[head],
+                   "copy": "device copy GB/s",
+                   "read": "streaming read GB/s"}[head],
         "value": s["value"], "unit": s["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": s["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": {"prefill": "bf16", "prefill_nc": "bf16", "decode_fp8": "e4m3 KV / bf16 q,out / fp32 softmax",
                   "decode_bf16": "bf16", "mxfp8": "mxfp8 e4m3+e8m0 / bf16 out", "backward": "bf16",
-                  "copy": "bf16"}[head],
+                  "copy": "bf16", "read": "u32"}[head],
         "data": "synthetic, seeded (torch generator seed 0), resident in HBM",
         "config": dict(s["config"], parallelism="none (1 GPU)"),
         "roofline": s["roofline"],
@@ -361,7 +402,7 @@ def main():
     if args.workload == "all":
         r = WORKLOADS["decode_fp8"](args.steps, args.warmup)
         log(f"decode_fp8: {r['ms']:.4f} ms/step, {r['value']:.1f} GB/s")
-        sec = summary("decode_fp8", r)
+        sec = summary("decode_fp8", r, read_ceiling(args.steps, args.warmup))
         sec["metric"] = "FP8 paged GQA decode HBM GB/s (C4)"
         if not args.no_cpu_baseline:
             sec["cpu_baseline"] = cpu_decode(r, args.cpu_seconds)
@@ -372,7 +413,8 @@ def main():
         for name in ("prefill_nc", "decode_bf16", "mxfp8", "backward"):
             r = WORKLOADS[name](args.steps, args.warmup)
             log(f"{name}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
-            extra[name] = summary(name, r)
+            extra[name] = summary(name, r, read_ceiling(args.steps, args.warmup)
+                                  if name.startswith("decode") else None)
             del r
             torch.cuda.empty_cache()
         line["extra"] = extra

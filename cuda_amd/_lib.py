@@ -29,6 +29,7 @@ SIGNATURES = {
     "ca_fused_rope_flash_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I,
                                            _P, _Z, _P]),
     "ca_rope_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "ca_stream_read": (_I, [_P, _Z, _P, _P]),
     "ca_paged_kv_append": (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                 _I, _P]),
     "ca_flash_decode": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),

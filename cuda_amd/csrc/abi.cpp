@@ -324,6 +324,15 @@ ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const voi
                   what);
 }
 
+ca_status ca_stream_read(const void* p, size_t bytes, void* sink, void* stream) {
+  const char* what = "stream_read";
+  if (bytes == 0) return CA_OK;
+  if (!p || !sink) return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if (!aligned16(p) || bytes % 16)
+    return fail(CA_INVALID_ARGUMENT, "%s: pointer and size must be 16-byte aligned", what);
+  return from_hip(ca::launch_stream_read(p, bytes, sink, (hipStream_t)stream), what);
+}
+
 ca_status ca_paged_kv_append(ca_dtype dtype, int cache_kind, const void* key, const void* value,
                              void* key_cache, void* value_cache, float* k_scale, float* v_scale,
                              int per_block_scales, const int32_t* block_tables,

@@ -105,6 +105,9 @@ hipError_t launch_rope_prefill(int dtype, const void* q, const void* k, const vo
                                int Hkv, int S, int D, float scale, bool causal, void* ws,
                                hipStream_t stream);
 
+// Streaming read of `bytes` (multiple of 16) for the bandwidth ceiling (stream_read.hip).
+hipError_t launch_stream_read(const void* p, size_t bytes, void* sink, hipStream_t stream);
+
 // MXFP8 attention: e4m3 q/k/v [B, H, S, D] with e8m0 scale bytes [B, H, S, D/32].
 hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                         const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,

@@ -98,6 +98,13 @@ ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const voi
 size_t ca_rope_workspace_bytes(ca_dtype dtype, int batch, int num_q_heads, int num_kv_heads,
                                int seq_len, int head_dim);
 
+/* Measurement helper, no counterpart in the reference: reads `bytes` bytes
+ * (a multiple of 16, 16-byte aligned) from device memory at `p` with
+ * streaming loads; `sink` is a 4-byte device word the kernel may write. The
+ * time of this call is the measured streaming-read ceiling that the
+ * HBM-bound decode entry points are compared with. */
+ca_status ca_stream_read(const void* p, size_t bytes, void* sink, void* stream);
+
 /* Append new tokens to a paged KV cache, in place: the step before paged
  * decode. key, value: [num_seqs, num_kv_heads, max_new_tokens, head_dim] of
  * `dtype` (bf16/fp16); sequence n appends its first new_lens[n] tokens

@@ -144,6 +144,13 @@ def test_kv_append_validates():
     assert _status("ca_paged_kv_append", *nothing) == L.CA_OK
 
 
+def test_stream_read_validates():
+    assert _status("ca_stream_read", None, 1024, P, None) == L.CA_INVALID_ARGUMENT
+    assert _status("ca_stream_read", P, 1000, P, None) == L.CA_INVALID_ARGUMENT
+    assert b"aligned" in L.load().ca_last_error()
+    assert _status("ca_stream_read", P, 0, None, None) == L.CA_OK  # nothing to read
+
+
 def test_paged_rejects_bad_arguments():
     args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
     bad_page = list(args)
