@@ -415,7 +415,7 @@ void decode_split_kernel(
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const vec2 pk = Tr::pack2(o[nb][r] * inv, 0.f);
-        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = __builtin_bit_cast(uint16_t, pk[0]);
+        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = (uint16_t)(__builtin_bit_cast(uint32_t, pk) & 0xffffu);
       }
     } else {
       const size_t slot = ((size_t)n * Hq + hq) * max_splits + split;
@@ -792,7 +792,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const vec2 pk = Tr::pack2(o[nb][r] * inv, 0.f);
-        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = __builtin_bit_cast(uint16_t, pk[0]);
+        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = (uint16_t)(__builtin_bit_cast(uint32_t, pk) & 0xffffu);
       }
     } else {
       const size_t sl = ((size_t)n * Hq + hq) * max_splits + split;

@@ -23,7 +23,8 @@ hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void*
                               hipStream_t stream);
 
 // Backward (backward.hip): dq, dk, dv from q, k, v, o, dout and the forward's
-// natural-log LSE; ws holds bwd_workspace_bytes (the rowsum(dO * O) terms).
+// natural-log LSE; ws holds bwd_workspace_bytes (per query row the pair
+// (LSE * log2(e), rowsum(dO * O))).
 size_t bwd_workspace_bytes(int B, int Hq, int S);
 hipError_t launch_flash_bwd(int dtype, const void* q, const void* k, const void* v,
                             const void* o, const void* dout, const float* lse, void* dq, void* dk,

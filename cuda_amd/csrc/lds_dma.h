@@ -99,18 +99,24 @@ __device__ __forceinline__ void dma16(const void* src, CA_LDS void* dst) {
   __builtin_amdgcn_global_load_lds(src, dst, 16, 0, AUX);
 }
 
-// Buffer-resource form: 16 bytes per lane from rsrc at voffset + soffset into
-// LDS at `dst` + 16 * lane. Bytes at or past the resource's size read as zero
-// (no memory access), so a tile that runs past the end of a slice needs no
-// clamping. voffset is per lane, soffset uniform: a loop that walks tiles
-// changes only soffset.
+// Buffer-resource form: 16 bytes per lane from rsrc at byte offset `voffset`
+// into LDS at `dst` + 16 * lane. A lane whose offset is at or past the
+// resource's size reads zeros without a memory access, so a tile that runs
+// past the end of a slice needs no clamping. The whole offset goes in the
+// per-lane operand, which the range check covers (the scalar offset operand
+// is left 0: whether the check includes it is not something to rely on).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   // word 3 = 0x00020000: 32-bit data format, as raw dword loads on gfx9 need
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, CA_LDS void* dst,
-                                          uint32_t voffset, uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, (int)voffset, (int)soffset, 0, 0);
+                                          uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, (int)voffset, 0, 0, 0);
+}
+// 4 bytes per lane (LDS at `dst` + 4 * lane), same range check.
+__device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t rsrc, CA_LDS void* dst,
+                                         uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, (int)voffset, 0, 0, 0);
 }
 
 // Orders later uses of `x` after the preceding wait (the asm "rewrites" it).

@@ -78,7 +78,8 @@ ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, c
                                  int seq_len, int head_dim, float softmax_scale, int is_causal,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
-/* Bytes of the ca_flash_attention_bwd workspace (the rowsum(dout * o) terms). */
+/* Bytes of the ca_flash_attention_bwd workspace: per query row the pair
+ * (lse * log2(e), rowsum(dout * o)), 8 bytes. */
 size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int seq_len);
 
 /* Prefill forward on RoPE-rotated q and k (rotate-half convention):

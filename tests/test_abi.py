@@ -85,7 +85,7 @@ def test_prefill_rejects_bad_arguments():
 
 def test_backward_entry_points_validate():
     lib = L.load()
-    assert lib.ca_flash_attention_bwd_workspace_bytes(2, 8, 100) == 2 * 8 * 100 * 4
+    assert lib.ca_flash_attention_bwd_workspace_bytes(2, 8, 100) == 2 * 8 * 100 * 8
     assert lib.ca_flash_attention_bwd_workspace_bytes(0, 8, 100) == 0
     args = [L.CA_BF16, P, P, P, P, P, P, P, P, P, 1, 4, 2, 64, 64, 0.1, 1, P, 1 << 20, None]
     f32 = list(args)

@@ -163,3 +163,25 @@ def test_backward_float32_unsupported(dev):
     out, lse = cuda_llm.flash_attention_forward_lse(q, k, v)
     with pytest.raises(RuntimeError, match="Supported: Float16, BFloat16"):
         cuda_llm.flash_attention_backward(torch.randn_like(q), q, k, v, out, lse)
+
+
+@pytest.mark.parametrize("b,h,s,is_causal", [(4, 16, 2304, True), (4, 16, 2048, True),
+                                             (2, 8, 1100, False)])
+def test_backward_large_paired_tiles(dev, b, h, s, is_causal):
+    """Grids large enough for the causal launches to pair tiles per workgroup
+    (9 tiles per head: the middle tiles of two heads make one work item); the
+    kernel computes every head, sampled heads are checked against the oracle
+    on the kernel forward's own out and LSE."""
+    g = torch.Generator(device=dev).manual_seed(7)
+    q, k, v = qkv(b, h, s, 128, torch.bfloat16, dev, gen=g)
+    dout = torch.randn(b, h, s, 128, device=dev, generator=g).to(torch.bfloat16)
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal)
+    dq, dk, dv = cuda_llm.flash_attention_backward(dout, q, k, v, out, lse, is_causal=is_causal)
+    torch.cuda.synchronize()
+    for bi, hi in [(0, 0), (b - 1, h - 1), (b // 2, h // 2 - 1)]:
+        sel = lambda t: to_np(t[bi:bi + 1, hi:hi + 1]).astype(np.float64)
+        ref = oracle.attention_backward(sel(dout), sel(q), sel(k), sel(v), sel(out),
+                                        to_np(lse[bi:bi + 1, hi:hi + 1]).astype(np.float64),
+                                        is_causal=is_causal, dtype=np.float64)
+        for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+            _check_grad(a[bi:bi + 1, hi:hi + 1], r, f"{name} b{bi} h{hi}")
