@@ -38,6 +38,9 @@ namespace {
 #define CA_BWD_DMA 1
 #endif
 constexpr bool kBwdDma = CA_BWD_DMA != 0;  // head dim 128: the buffer-load kernels below
+#ifndef CA_BWD_PRIO
+#define CA_BWD_PRIO 0
+#endif
 constexpr int kBwdWaves = 4;    // waves per workgroup (32 rows each)
 constexpr int kBwdTile = 64;    // keys (dq kernel) or queries (dkv kernel) per LDS tile
 
@@ -550,8 +553,7 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
   // HBM -> LDS: load i of this wave covers tile rows 4 (kDma wave + i) + lane/16,
   // the lane fetching the chunk that belongs at position lane % 16; rows at or
   // past kv_end read as zero.
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(Kp, (uint32_t)kv_end * kRowB);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(Vp, (uint32_t)kv_end * kRowB);
+  const uint32_t kv_bytes = (uint32_t)kv_end * kRowB;
   uint32_t dma_off[kDma];
 #pragma unroll
   for (int i = 0; i < kDma; ++i) {
@@ -561,10 +563,12 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
   auto issue = [&](int tt) CA_INLINE {
     unsigned char* dst = lds + (tt % kStages) * kStageB + wave * (kDma * 1024);
     const uint32_t toff = (uint32_t)tt * kTileB;
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc_at(Kp, toff, kv_bytes);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc_at(Vp, toff, kv_bytes);
 #pragma unroll
     for (int i = 0; i < kDma; ++i) {
-      dma16_buf(k_rsrc, (CA_LDS void*)(dst + 1024 * i), dma_off[i] + toff);
-      dma16_buf(v_rsrc, (CA_LDS void*)(dst + kTileB + 1024 * i), dma_off[i] + toff);
+      dma16_buf(k_rsrc, (CA_LDS void*)(dst + 1024 * i), dma_off[i]);
+      dma16_buf(v_rsrc, (CA_LDS void*)(dst + kTileB + 1024 * i), dma_off[i]);
     }
   };
   const uint32_t lds0 = lds_off(lds);
@@ -587,6 +591,7 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
     const uint32_t ka = hb + rofs, va = ka + kTileB;
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
     u32x4 kr[2], vr[2];
     kr[0] = lds_read_b128<0>(ka);
     vr[0] = lds_read_b128<0>(va);
@@ -605,6 +610,7 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
       s = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb]), qv[ks], s);
       dp = Tr::mfma32(__builtin_bit_cast(vec8, vr[cb]), gv[ks], dp);
     }
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
     // dS^T / scale = P (dP - D) as the B operand of dQ^T += K^T dS^T
     vec8 pb[2];
     auto softmax = [&](auto mask_tag) CA_INLINE {
@@ -633,6 +639,7 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
     if (mask) softmax(std::true_type{});
     else softmax(std::false_type{});
     // dQ^T[d x q] += K^T[d x keys] dS^T[keys x q]
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) {
       const vec8 a0 = tr_operand<Tr, 0>(hb, tofs, ob);
@@ -644,6 +651,7 @@ __device__ CA_INLINE void bwd_dq128_tile(const uint16_t* __restrict__ Q,
       acc[ob] = Tr::mfma32(x0, pb[0], acc[ob]);
       acc[ob] = Tr::mfma32(x1, pb[1], acc[ob]);
     }
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
 #pragma unroll
@@ -755,14 +763,13 @@ __device__ CA_INLINE void bwd_dkv128_tile(const uint16_t* __restrict__ Q,
     const int h = hk * G + itc / max(nt, 1);
     const int q0 = past ? S : (t_begin + itc % max(nt, 1)) * BQ;
     const size_t ho = (size_t)(b * Hq + h) * S;
-    const __amdgpu_buffer_rsrc_t qr = make_rsrc(Q + ho * kD, (uint32_t)S * kRowB);
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(dO + ho * kD, (uint32_t)S * kRowB);
-    dma16_buf(qr, (CA_LDS void*)(st + 1024 * wave), (uint32_t)q0 * kRowB + dma_off);
-    dma16_buf(gr, (CA_LDS void*)(st + kTileB + 1024 * wave), (uint32_t)q0 * kRowB + dma_off);
-    if (wave == 0) {
-      const __amdgpu_buffer_rsrc_t lr = make_rsrc(LD + 2 * ho, (uint32_t)S * 8);
-      dma4_buf(lr, (CA_LDS void*)(st + 2 * kTileB), (uint32_t)q0 * 8 + 4 * lane);
-    }
+    const uint32_t qoff = (uint32_t)q0 * kRowB, sz = (uint32_t)S * kRowB;
+    dma16_buf(make_rsrc_at(Q + ho * kD, qoff, sz), (CA_LDS void*)(st + 1024 * wave), dma_off);
+    dma16_buf(make_rsrc_at(dO + ho * kD, qoff, sz), (CA_LDS void*)(st + kTileB + 1024 * wave),
+              dma_off);
+    if (wave == 0)
+      dma4_buf(make_rsrc_at(LD + 2 * ho, (uint32_t)q0 * 8, (uint32_t)S * 8),
+               (CA_LDS void*)(st + 2 * kTileB), 4 * lane);
   };
   const uint32_t lds0 = lds_off(lds);
   const uint32_t rofs = row_ofs(rho32(l32), hl);  // Q / dO rows (A operands)
@@ -785,6 +792,7 @@ __device__ CA_INLINE void bwd_dkv128_tile(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
     const uint32_t qa = sb + rofs, ga = qa + kTileB;
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
     u32x4 qr[2], gr[2], vr[2];
     qr[0] = lds_read_b128<0>(qa);
     gr[0] = lds_read_b128<0>(ga);
@@ -806,6 +814,7 @@ __device__ CA_INLINE void bwd_dkv128_tile(const uint16_t* __restrict__ Q,
       s = Tr::mfma32(__builtin_bit_cast(vec8, qr[cb]), kv[ks], s);
       dp = Tr::mfma32(__builtin_bit_cast(vec8, gr[cb]), __builtin_bit_cast(vec8, vr[cb]), dp);
     }
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
     // P and dS / scale = P (dP - D) as B operands, k-step kk = 16 queries
     vec8 pp[2], pd[2];
     auto softmax = [&](auto mask_tag) CA_INLINE {
@@ -849,6 +858,7 @@ __device__ CA_INLINE void bwd_dkv128_tile(const uint16_t* __restrict__ Q,
     if (mask) softmax(std::true_type{});
     else softmax(std::false_type{});
     // dV^T[d x keys] += dO^T P and dK^T[d x keys] += Q^T dS
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ob = 0; ob < 4; ++ob) {
       const vec8 g0 = tr_operand<Tr, 0>(sb + kTileB, tofs, ob);
@@ -866,6 +876,7 @@ __device__ CA_INLINE void bwd_dkv128_tile(const uint16_t* __restrict__ Q,
       dv[ob] = Tr::mfma32(a1, pp[1], dv[ob]);
       dk[ob] = Tr::mfma32(b1, pd[1], dk[ob]);
     }
+    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
 #pragma unroll

@@ -119,6 +119,17 @@ __device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t rsrc, CA_LDS voi
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, (int)voffset, 0, 0, 0);
 }
 
+// Resource over bytes [off, size) of `base` (none when off >= size): a tile
+// walk moves the resource rather than the per-lane offsets, which costs
+// scalar instructions only. The arguments are wave-uniform; readfirstlane
+// says so to the compiler, which would otherwise compute the clamped size in
+// a vector register and wrap every load in a loop over distinct resources.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_at(const void* base, uint32_t off,
+                                                               uint32_t size) {
+  const uint32_t left = __builtin_amdgcn_readfirstlane(size > off ? size - off : 0u);
+  return make_rsrc((const char*)base + off, left);
+}
+
 // Orders later uses of `x` after the preceding wait (the asm "rewrites" it).
 template <typename T>
 __device__ __forceinline__ void after_wait(T& x) {

@@ -413,9 +413,9 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // ([0, kv_end) of the (b, kv head) slice; rows past it read as zero, so
   // partial and trailing tiles need no clamp). Load i of this wave covers
   // tile rows 4*(kDmaPerWave*wave + i) + lane/16; the lane fetches the chunk
-  // that belongs at position lane % 16, at its row offset + the tile offset.
-  const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc(Kp, (uint32_t)kv_end * kRowB);
-  const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc(Vp, (uint32_t)kv_end * kRowB);
+  // that belongs at position lane % 16. Tile tt reads through resources that
+  // start at its first row.
+  const uint32_t kv_bytes = (uint32_t)kv_end * kRowB;
   uint32_t dma_off[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
@@ -427,10 +427,12 @@ __device__ CA_INLINE void prefill_d128_qtile(
     if (!loader) return;
     unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
     const uint32_t toff = (uint32_t)tt * kTileB;
+    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc_at(Kp, toff, kv_bytes);
+    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc_at(Vp, toff, kv_bytes);
 #pragma unroll
     for (int i = 0; i < kDmaPerWave; ++i) {
-      dma16_buf(k_rsrc, (CA_LDS void*)(kdst + 1024 * i), dma_off[i] + toff);
-      dma16_buf(v_rsrc, (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i] + toff);
+      dma16_buf(k_rsrc, (CA_LDS void*)(kdst + 1024 * i), dma_off[i]);
+      dma16_buf(v_rsrc, (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i]);
     }
   };
 
