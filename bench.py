@@ -60,14 +60,16 @@ def time_steps(fn, steps, warmup):
 
 
 def _traffic(key):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    """HBM bytes per step measured by rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by the copy-kernel calibration), committed in
-    profiles/traffic.json."""
+    profiles/traffic.json; `key` names one kernel's entry or a tuple of the
+    entries of a multi-kernel step."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
+    keys = key if isinstance(key, tuple) else (key,)
     try:
         with open(path) as f:
-            t = json.load(f)[key]
-        return float(t["fetch_bytes"]) + float(t["write_bytes"])
+            t = json.load(f)
+        return sum(float(t[k]["fetch_bytes"]) + float(t[k]["write_bytes"]) for k in keys)
     except (OSError, KeyError, ValueError, TypeError):
         return None
 
@@ -326,7 +328,8 @@ WORKLOADS = {
     "read": w_read,
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
-               "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5"}
+               "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5",
+               "backward": ("backward_c2_dkv", "backward_c2_dq")}
 
 
 def summary(name, r, read_gbs=None):
