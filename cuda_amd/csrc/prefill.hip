@@ -44,6 +44,9 @@ namespace ca {
 #ifndef CA_PF_MDEPTH
 #define CA_PF_MDEPTH 4
 #endif
+#ifndef CA_PF_STALE
+#define CA_PF_STALE 1
+#endif
 #ifndef CA_PF_PRIO
 #define CA_PF_PRIO 1
 #endif
@@ -370,6 +373,9 @@ __device__ CA_INLINE void prefill_d128_qtile(
   constexpr int kNW = kBM / kRW;                 // waves per workgroup
   // waves that issue the HBM -> LDS loads: all of them when they divide the
   // 16 1-KB loads of a tile evenly, else the first 8
+  // row max only on a wave's first tile (stale_softmax); 8-wave tiles (at
+  // three waves per SIMD its rare path leaves too few registers)
+  constexpr bool STALE = CA_PF_STALE != 0 && !PIPE && kNW == 8;
   // ping-pong schedule (see the tile walk): 8 waves, two per SIMD
   constexpr bool PP = CA_PF_PP && !PIPE && NH == 1 && kNW == 8 && kStages == 4;
   constexpr int kLoaders = PP ? kNW / 2 : (kTileB / 1024) % kNW == 0 ? kNW : 8;
@@ -493,7 +499,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // accumulators into sv (masked if MASK; a masked logit becomes the value
   // whose exponential is 0) and fold it into the row max
   float tm[NH][2];  // two partial row maxima (independent dependency chains)
-  auto take_pair = [&](int p, int k0, auto mask_tag) CA_INLINE {
+  auto copy_pair = [&](int p, int k0, auto mask_tag) CA_INLINE {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int nb = p >> 4, i0 = 2 * (p & 15);
 #pragma unroll
@@ -507,9 +513,16 @@ __device__ CA_INLINE void prefill_d128_qtile(
       if (PIPE) CA_DEVICE_ASM("" : "+v"(x));  // a real VGPR copy: the accumulators are reused
       sv[nb][i] = x;
     }
+  };
+  auto fold_max = [&](int p) CA_INLINE {
+    const int nb = p >> 4, i0 = 2 * (p & 15);
     float& m = tm[nb][(p >> 1) & 1];
     m = POS ? __builtin_fmaxf(__builtin_fmaxf(m, sv[nb][i0]), sv[nb][i0 + 1])   // one v_max3
             : __builtin_fminf(__builtin_fminf(m, sv[nb][i0]), sv[nb][i0 + 1]);
+  };
+  auto take_pair = [&](int p, int k0, auto mask_tag) CA_INLINE {
+    copy_pair(p, k0, mask_tag);
+    fold_max(p);
   };
   // running max, lazy O rescale, exponent offset for the tile now in sv
   auto settle_max = [&]() CA_INLINE {
@@ -542,6 +555,40 @@ __device__ CA_INLINE void prefill_d128_qtile(
     }
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb) msub[nb] = (m_run[nb] == kNegInf) ? 0.f : m_run[nb];
+  };
+
+  // Softmax step of a tile after the wave's first, without its row max: the
+  // exponentials are taken against the running max as it stands. They may
+  // exceed 1 by far without harm as long as P stays representable in the
+  // operand type of the PV MFMA (bf16: up to 2^48, with O and l far below
+  // the float range; fp16: up to 2^15, its largest power of two below
+  // 65504), so the max only has to be recomputed, O and l rescaled and the
+  // exponentials taken again when some lane's tile sum passes that bound (or
+  // is not finite). Saves the max3 tree and lane swap of every other tile.
+  constexpr float kStaleMax = std::is_same<Tr, BF16>::value ? 0x1p48f : 0x1p15f;
+  auto exp_all = [&]() CA_INLINE {
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) psum[nb][0] = psum[nb][1] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16 * NH; ++p) exp_pair(p);
+  };
+  auto stale_softmax = [&](int tn, auto mask_tag) CA_INLINE {
+#pragma unroll
+    for (int p = 0; p < 16 * NH; ++p) copy_pair(p, tn * kBN, mask_tag);
+    exp_all();
+    bool big = false;
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) big |= !(psum[nb][0] + psum[nb][1] <= kStaleMax);
+    if (__builtin_expect(wave_any(big), 0)) {
+#pragma unroll
+      for (int nb = 0; nb < NH; ++nb) tm[nb][0] = tm[nb][1] = kMaskVal;
+#pragma unroll
+      for (int p = 0; p < 16 * NH; ++p) fold_max(p);
+      settle_max();
+      exp_all();
+    }
+#pragma unroll
+    for (int nb = 0; nb < NH; ++nb) l_run[nb] += psum[nb][0] + psum[nb][1];
   };
 
   // Ping-pong MFMA block (NH = 1): O^T += V(t)^T P^T (16 steps, if PV) then
@@ -815,6 +862,34 @@ __device__ CA_INLINE void prefill_d128_qtile(
       phase_b(t, -1, T_{}, F_{}, F_{});
       ++t;
     }
+  } else if (STALE) {
+    // the wave's first tile takes the full max; later tiles stale_softmax
+    if (w_tiles > 1) {
+      sync(0);
+      phase_a(0, T_{}, F_{});
+      phase_b(-1, 0, F_{}, T_{}, F_{});
+      phase_a(-1, F_{}, T_{});
+      phase_b(0, -1, T_{}, F_{}, F_{});
+      t = 1;
+    }
+    for (; t + 1 < w_tiles; ++t) {
+      sync(t);
+      phase_a(t, T_{}, F_{});
+      stale_softmax(t, F_{});
+      phase_b(t, -1, T_{}, F_{}, F_{});
+    }
+    if (t + 1 == w_tiles) {  // the wave's last tile, masked
+      sync(t);
+      phase_a(t, T_{}, F_{});
+      if (t == 0) {
+        phase_b(-1, t, F_{}, T_{}, T_{});
+        phase_a(-1, F_{}, T_{});
+      } else {
+        stale_softmax(t, T_{});
+      }
+      phase_b(t, -1, T_{}, F_{}, F_{});
+      ++t;
+    }
   } else {
     for (; t + 1 < w_tiles; ++t) {
       sync(t);
@@ -921,10 +996,12 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
   return hipGetLastError();
 }
 
-// Workgroup height: 384 query rows (12 waves, three per SIMD, which hides
-// more of each wave's LDS and MFMA latency: +4-6 % at S = 3072) when 384-row
-// tiles cover S with at most ~5 % padding rows and the grid still gives every
-// CU two workgroups; 256 rows (8 waves) otherwise.
+// Workgroup height: 256 query rows (8 waves, two per SIMD). 384 rows (12
+// waves, three per SIMD) measured +4-6 % at S = 3072 before the stale-max
+// softmax, which only the 8-wave kernel can afford in registers and which
+// gains more; the 384-row choice (when such tiles cover S with at most ~5 %
+// padding and the grid gives every CU two workgroups) remains for builds
+// without it.
 template <typename Tr, bool CAUSAL>
 static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o, float* lse,
                                       int B, int Hq, int Hkv, int S, float scale,
@@ -934,7 +1011,7 @@ static hipError_t launch_prefill_d128(const void* q, const void* k, const void* 
 #else
   const long long n384 = (S + 383) / 384;
   const bool fits = n384 * 384 * 20 <= (long long)S * 21;
-  const bool tall = fits && (long long)B * Hq * n384 >= 2LL * device_cus();
+  const bool tall = !CA_PF_STALE && fits && (long long)B * Hq * n384 >= 2LL * device_cus();
   return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)
               : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
 #endif

@@ -78,6 +78,33 @@ def test_custom_scale_and_large_logits(dev):
         assert_close(to_np(out), ref, **TOL_16BIT, name=f"large logits causal={causal}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("is_causal", [False, True])
+@pytest.mark.parametrize("profile", ["ramp", "jump"])
+def test_running_max_growth(dev, dtype, is_causal, profile):
+    """Logits that grow along the keys. Tiles after a wave's first take their
+    exponentials against the running max as it stands; a tile whose sums
+    pass the bound of the P operand type (bf16 2^48, fp16 2^15; ramp: about
+    +33 log2 units per 64-key tile) or overflow to infinity (jump: +130 log2
+    units at key 512) takes the full max, rescales O and l, and takes the
+    exponentials again."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    b, h, s, d = 1, 2, 1024, 128
+    u = torch.randn(d, device=dev, generator=g)
+    u = u / u.norm()
+    j = torch.arange(s, device=dev, dtype=torch.float32)
+    amp = 0.5 * j if profile == "ramp" else torch.where(j < 512, torch.ones_like(j),
+                                                         torch.full_like(j, 130.0))
+    k = (amp[:, None] * u + 0.1 * torch.randn(b, h, s, d, device=dev, generator=g)).to(dtype)
+    q = (8 * u + 0.1 * torch.randn(b, h, s, d, device=dev, generator=g)).to(dtype)
+    v = torch.randn(b, h, s, d, device=dev, generator=g).to(dtype)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=is_causal)
+    assert_close(to_np(out), ref, **TOL_16BIT, name=f"{profile} causal={is_causal}")
+
+
 def test_every_row_written(dev):
     """Output pre-filled with NaN through the C ABI: every row must be written."""
     import cuda_amd._lib as L
@@ -149,9 +176,9 @@ def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
 
 @pytest.mark.parametrize("s", [1536, 4096])
 def test_tall_workgroups_noncausal(dev, s):
-    """Non-causal grids that take 384-row workgroups (12 waves, three per
-    SIMD): S = 1536 (4 full tiles) and S = 4096 (11 tiles, the last one
-    partial)."""
+    """Large non-causal grids: S = 1536 and S = 4096 (the shapes that take
+    384-row workgroups in builds without the stale-max softmax; 256-row
+    workgroups with it, the last tile partial at S = 1536 + 256k)."""
     b, hq, hkv = (4, 32, 8) if s == 1536 else (2, 32, 8)
     q, k, v = qkv(b, hq, s, 128, torch.bfloat16, dev, hkv=hkv)
     out = cuda_llm.flash_attention(q, k, v, is_causal=False)
