@@ -147,14 +147,20 @@ __device__ CA_INLINE void mxfp8_qtile(
   const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (s16 & 3);
 
-  if (n_tiles > 0) gload(0);
-  for (int t = 0; t < n_tiles; ++t) {
+  // One key tile. The wave's first tile (t = 0, never skipped) takes the row
+  // max; later tiles take their exponentials against the running max as it
+  // stands, and only a tile whose bf16 weights sum past 2^48 in some lane
+  // (or overflow) recomputes them after a full max and rescale: the weights
+  // may exceed 1 by far while they stay representable in bf16 and O, l far
+  // below the float range.
+  auto step = [&](int t, auto first_tag) CA_INLINE {
+    constexpr bool FIRST = decltype(first_tag)::value;
     const int buf = t & 1;
     lstore(buf);
     __syncthreads();
     if (t + 1 < n_tiles) gload(t + 1);
     const int k0 = t * BN;
-    if (CAUSAL && k0 > qw0 + 31) continue;
+    if (CAUSAL && k0 > qw0 + 31) return;
 
     f32x16 s[2];
 #pragma unroll
@@ -177,55 +183,66 @@ __device__ CA_INLINE void mxfp8_qtile(
     // issue over the other waves' softmax VALU)
     __builtin_amdgcn_s_setprio(0);
 
-    float x[32];
+    // masked logits (bounds, causal diagonal) become the value whose scaled
+    // image is -inf, once, on the tiles that need it
+    if (CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S)) {
+      const float mask_s = scale_log2 >= 0.f ? kNegInf : -kNegInf;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[mb * 16 + r] = s[mb][r] * scale_log2;
-    const bool need_mask = CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S);
-    if (need_mask) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 32 * mb + 16 * (r >> 3) + 8 * hl + (r & 7);
-          const bool masked = (key >= S) || (CAUSAL && key > myq);
-          if (masked) x[mb * 16 + r] = kNegInf;
-        }
+      for (int i = 0; i < 32; ++i) {
+        const int key = k0 + 32 * (i >> 4) + 16 * ((i >> 3) & 1) + 8 * hl + (i & 7);
+        if ((key >= S) || (CAUSAL && key > myq)) s[i >> 4][i & 15] = mask_s;
+      }
     }
-    float tmax = x[0];
+    // the tile's row max (log2 units) into the running max; O and l rescaled
+    auto full_max = [&]() CA_INLINE {
+      float tmax = kNegInf;
 #pragma unroll
-    for (int i = 1; i < 32; ++i) tmax = __builtin_fmaxf(tmax, x[i]);
-    tmax = pair32_max(tmax);
-    const bool need = tmax > m_run + 8.0f;
-    if (wave_any(need)) {
-      const float m_new = __builtin_fmaxf(m_run, tmax);
-      const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+      for (int i = 0; i < 32; ++i) tmax = __builtin_fmaxf(tmax, s[i >> 4][i & 15] * scale_log2);
+      tmax = pair32_max(tmax);
+      if (wave_any(tmax > m_run + 8.0f)) {
+        const float m_new = __builtin_fmaxf(m_run, tmax);
+        const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
 #pragma unroll
-      for (int i = 0; i < NOB; ++i)
+        for (int i = 0; i < NOB; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-      l_run *= alpha;
-      m_run = m_new;
-    }
-    const float msub = (m_run == kNegInf) ? 0.f : m_run;
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+        l_run *= alpha;
+        m_run = m_new;
+      }
+    };
     float psum = 0.f;
     vec8 pb[4];
+    // P = 2^(s scale_log2 - m) as the PV B operand; the row sum uses the
+    // bf16-rounded weights that enter PV (one dot2 with ones per pair), so
+    // o / l is an exact weighted mean of V under slightly perturbed weights:
+    // with MX data |v| reaches ~16 and the unrounded sum would put the P
+    // rounding error (up to 2^-9 relative) straight into |o|
+    auto weights = [&]() CA_INLINE {
+      const float msub = (m_run == kNegInf) ? 0.f : m_run;
+      const bf16x2 ones = {(__bf16)1.f, (__bf16)1.f};
+      psum = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int b0 = (kk >> 1) * 16 + (kk & 1) * 8;
+      for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p0 = fast_exp2(x[b0 + 2 * j] - msub);
-        const float p1 = fast_exp2(x[b0 + 2 * j + 1] - msub);
-        const vec2 pk = BF16::pack2(p0, p1);
-        // the row sum uses the bf16-rounded weights that enter PV, so o / l is
-        // an exact weighted mean of V under slightly perturbed weights; with
-        // MX data |v| reaches ~16 and the unrounded sum would put the P
-        // rounding error (up to 2^-9 relative) straight into |o|
-        psum += (float)pk[0] + (float)pk[1];
-        pb[kk][2 * j] = pk[0];
-        pb[kk][2 * j + 1] = pk[1];
+        for (int j = 0; j < 4; ++j) {
+          const int i0 = (kk >> 1) * 16 + (kk & 1) * 8 + 2 * j;
+          const float p0 = fast_exp2(__builtin_fmaf(s[i0 >> 4][i0 & 15], scale_log2, -msub));
+          const float p1 = fast_exp2(__builtin_fmaf(s[(i0 + 1) >> 4][(i0 + 1) & 15], scale_log2, -msub));
+          const vec2 pk = BF16::pack2(p0, p1);
+          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), ones, psum, false);
+          pb[kk][2 * j] = pk[0];
+          pb[kk][2 * j + 1] = pk[1];
+        }
+      }
+    };
+    if (FIRST) {
+      full_max();
+      weights();
+    } else {
+      weights();
+      if (__builtin_expect(wave_any(!(psum <= 0x1p48f)), 0)) {
+        full_max();
+        weights();
       }
     }
     l_run += psum;
@@ -242,7 +259,12 @@ __device__ CA_INLINE void mxfp8_qtile(
       }
     }
     __builtin_amdgcn_s_setprio(0);
+  };
+  if (n_tiles > 0) {
+    gload(0);
+    step(0, std::true_type{});
   }
+  for (int t = 1; t < n_tiles; ++t) step(t, std::false_type{});
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;

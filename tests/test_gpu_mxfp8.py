@@ -51,6 +51,37 @@ def test_mx_vs_oracle(dev, s, causal):
     assert_close(to_np(out), ref, **TOL_FP8, name=f"mx S={s}")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("profile", ["ramp", "jump"])
+def test_mx_running_max_growth(dev, causal, profile):
+    """Logits that grow along the keys: tiles after a wave's first take their
+    weights against the running max as it stands, and a tile whose bf16
+    weights sum past 2^48 (ramp: about +33 log2 units per 64-key tile) or
+    overflow (jump: +130 log2 units at key 512) takes the full max, rescale
+    and weights again. The MX block scales carry the growing key norms."""
+    g = torch.Generator(device="cpu").manual_seed(12)
+    b, h, s, d = 1, 2, 1024, 128
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    j = torch.arange(s, dtype=torch.float32)
+    amp = 0.5 * j if profile == "ramp" else torch.where(j < 512, torch.ones_like(j),
+                                                         torch.full_like(j, 130.0))
+    raw = {"k": amp[:, None] * u + 0.1 * torch.randn(b, h, s, d, generator=g),
+           "q": 8 * u + 0.1 * torch.randn(b, h, s, d, generator=g),
+           "v": torch.randn(b, h, s, d, generator=g)}
+    x = {}
+    for n, t in raw.items():
+        codes, sc = oracle.mx_quantize(t.numpy())
+        x[n] = torch.from_numpy(codes).to(dev)
+        x[n + "_scale"] = torch.from_numpy(sc).to(dev)
+    out = _run(x, causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    dq = _ref(x)
+    ref = oracle.attention(dq["q"], dq["k"], dq["v"], is_causal=causal)
+    assert_close(to_np(out), ref, **TOL_FP8, name=f"mx {profile} causal={causal}")
+
+
 def test_mx_scale_formats_agree(dev):
     """e8m0 bytes, float8_e8m0fnu and float powers of two give identical output."""
     x = mx_inputs(1, 2, 130, 128, dev, seed=3)
