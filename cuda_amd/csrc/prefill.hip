@@ -141,14 +141,18 @@ __device__ CA_INLINE void prefill_fwd_qtile(
   const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (s16 & 3);
 
-  if (n_tiles > 0) gload(0);
-  for (int t = 0; t < n_tiles; ++t) {
+  // One key tile. The wave's first tile (t = 0, never skipped) takes the row
+  // max; later tiles take their exponentials against the running max as it
+  // stands (see stale_softmax of the head-dim-128 kernel for the bound).
+  constexpr float kStaleMax = std::is_same<Tr, BF16>::value ? 0x1p48f : 0x1p15f;
+  auto step = [&](int t, auto first_tag) CA_INLINE {
+    constexpr bool FIRST = decltype(first_tag)::value;
     const int buf = t & 1;
     lstore(buf);
     __syncthreads();
     if (t + 1 < n_tiles) gload(t + 1);
     const int k0 = t * BN;
-    if (CAUSAL && k0 > qw0 + 31) continue;  // tile entirely above this wave's rows
+    if (CAUSAL && k0 > qw0 + 31) return;  // tile entirely above this wave's rows
 
     const uint16_t* Kb = Ks[buf];
     const uint16_t* Vb = Vs[buf];
@@ -181,44 +185,58 @@ __device__ CA_INLINE void prefill_fwd_qtile(
           if (masked) s[mb][r] = mv;
         }
     }
-    float tm;
-    if (pos) {
-      tm = max3(s[0][0], s[0][1], s[0][2]);
+    auto full_max = [&]() CA_INLINE {
+      float tm;
+      if (pos) {
+        tm = max3(s[0][0], s[0][1], s[0][2]);
 #pragma unroll
-      for (int i = 3; i < 31; i += 2) tm = max3(tm, s[i >> 4][i & 15], s[(i + 1) >> 4][(i + 1) & 15]);
-      tm = __builtin_fmaxf(tm, s[1][15]);
-    } else {
-      tm = s[0][0];
+        for (int i = 3; i < 31; i += 2) tm = max3(tm, s[i >> 4][i & 15], s[(i + 1) >> 4][(i + 1) & 15]);
+        tm = __builtin_fmaxf(tm, s[1][15]);
+      } else {
+        tm = s[0][0];
 #pragma unroll
-      for (int i = 1; i < 32; ++i) tm = __builtin_fminf(tm, s[i >> 4][i & 15]);
-    }
-    float tmax = pair32_max(tm * scale_log2);
-    const bool need = tmax > m_run + 8.0f;
-    if (wave_any(need)) {
-      const float m_new = __builtin_fmaxf(m_run, tmax);
-      const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+        for (int i = 1; i < 32; ++i) tm = __builtin_fminf(tm, s[i >> 4][i & 15]);
+      }
+      const float tmax = pair32_max(tm * scale_log2);
+      if (wave_any(tmax > m_run + 8.0f)) {
+        const float m_new = __builtin_fmaxf(m_run, tmax);
+        const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
 #pragma unroll
-      for (int i = 0; i < NOB; ++i)
+        for (int i = 0; i < NOB; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-      l_run *= alpha;
-      m_run = m_new;
-    }
-    const float msub = (m_run == kNegInf) ? 0.f : m_run;
+          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+        l_run *= alpha;
+        m_run = m_new;
+      }
+    };
     float psum = 0.f;
     vec8 pb[4];
+    auto weights = [&]() CA_INLINE {
+      const float msub = (m_run == kNegInf) ? 0.f : m_run;
+      psum = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const int base = (kk >> 1) * 16 + (kk & 1) * 8;
+      for (int kk = 0; kk < 4; ++kk) {
+        const int base = (kk >> 1) * 16 + (kk & 1) * 8;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i0 = base + 2 * j, i1 = i0 + 1;
-        const float p0 = fast_exp2(__builtin_fmaf(s[i0 >> 4][i0 & 15], scale_log2, -msub));
-        const float p1 = fast_exp2(__builtin_fmaf(s[i1 >> 4][i1 & 15], scale_log2, -msub));
-        psum += p0 + p1;
-        const vec2 pk = Tr::pack2(p0, p1);
-        pb[kk][2 * j] = pk[0];
-        pb[kk][2 * j + 1] = pk[1];
+        for (int j = 0; j < 4; ++j) {
+          const int i0 = base + 2 * j, i1 = i0 + 1;
+          const float p0 = fast_exp2(__builtin_fmaf(s[i0 >> 4][i0 & 15], scale_log2, -msub));
+          const float p1 = fast_exp2(__builtin_fmaf(s[i1 >> 4][i1 & 15], scale_log2, -msub));
+          psum += p0 + p1;
+          const vec2 pk = Tr::pack2(p0, p1);
+          pb[kk][2 * j] = pk[0];
+          pb[kk][2 * j + 1] = pk[1];
+        }
+      }
+    };
+    if (FIRST) {
+      full_max();
+      weights();
+    } else {
+      weights();
+      if (__builtin_expect(wave_any(!(psum <= kStaleMax)), 0)) {
+        full_max();
+        weights();
       }
     }
     l_run += psum;
@@ -234,7 +252,12 @@ __device__ CA_INLINE void prefill_fwd_qtile(
         o[ob] = Tr::mfma32(a, pb[kk], o[ob]);
       }
     }
+  };
+  if (n_tiles > 0) {
+    gload(0);
+    step(0, std::true_type{});
   }
+  for (int t = 1; t < n_tiles; ++t) step(t, std::false_type{});
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
@@ -256,7 +279,8 @@ __device__ CA_INLINE void prefill_fwd_qtile(
 }
 
 template <typename Tr, int D, int NW, bool CAUSAL>
-__global__ __launch_bounds__(NW * 64, 2) void prefill_fwd_kernel(
+// (at least 3 workgroups per CU: three waves per SIMD, <= 168 registers)
+__global__ __launch_bounds__(NW * 64, 3) void prefill_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
