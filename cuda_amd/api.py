@@ -14,7 +14,8 @@ Differences from the reference, all widening what is accepted:
   * a sequence with context length 0 yields zeros instead of an unwritten row.
 float32 q/k/v are accepted where the reference instantiates float (prefill,
 flash_decode, paged decode). ``flash_attention`` is differentiable (README.md:
-66-71) through ``flash_attention_backward`` (fp16 / bf16; float32 raises).
+66-71) through ``flash_attention_backward`` (fp16 / bf16 / float32, as the
+reference instantiates it).
 """
 import ctypes
 import math
@@ -128,8 +129,8 @@ def flash_attention_backward(dout, q, k, v, out, lse, is_causal=False, softmax_s
     natural-log row logsumexp ``lse`` [B, Hq, S] (fused_softmax_binding.cpp:
     367-433; math flash_attention_bwd_kernel.cuh:9-19). q, out, dout: [B, Hq,
     S, D]; k, v: [B, Hkv, S, D] (GQA: dk, dv sum over the q heads of a kv
-    head). fp16 / bf16; lse is converted to contiguous float32 as the
-    reference does."""
+    head). fp16 / bf16 / float32; lse is converted to contiguous float32 as
+    the reference does."""
     _check(dout.is_cuda and q.is_cuda and k.is_cuda and v.is_cuda and out.is_cuda,
            "Inputs must be on CUDA")
     _check(lse.is_cuda, "LSE tensor must be on CUDA")
@@ -144,8 +145,9 @@ def flash_attention_backward(dout, q, k, v, out, lse, is_causal=False, softmax_s
     _check(q.dtype == k.dtype == v.dtype == out.dtype == dout.dtype,
            "q, k, v, out and dout must have the same dtype")
     _check(d in (64, 128), "Only head_dim 64 and 128 are currently supported")
-    _check(q.dtype in (torch.float16, torch.bfloat16),
-           "Unsupported scalar type for FlashAttention Backward. Supported: Float16, BFloat16.")
+    _check(q.dtype in _DT,
+           "Unsupported scalar type for FlashAttention Backward. Supported: Float, Float16, "
+           "BFloat16.")
     dt = _DT[q.dtype]
     q, k, v, out, dout = (_aligned(t.contiguous()) for t in (q, k, v, out, dout))
     lse = lse.to(torch.float32).contiguous()

@@ -15,8 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcuda_llm_amd.so")
-SOURCES = ["prefill.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "kv_append.hip",
-           "rope.hip", "stream_read.hip", "abi.cpp"]
+SOURCES = ["prefill.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "backward_f32.hip",
+           "kv_append.hip", "rope.hip", "stream_read.hip", "abi.cpp"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

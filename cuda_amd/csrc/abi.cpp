@@ -131,9 +131,7 @@ ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, c
                                  void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "flash_attention_backward";
   ca_status st;
-  if (dtype == CA_F32)
-    return fail(CA_UNSUPPORTED, "%s: float32 is not supported (use bf16/fp16)", what);
-  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = check_heads(num_q_heads, num_kv_heads, what)) != CA_OK) return st;
   if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
   if (batch < 0 || seq_len < 0) return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);

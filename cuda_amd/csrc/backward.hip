@@ -976,6 +976,10 @@ hipError_t launch_flash_bwd(int dtype, const void* q, const void* k, const void*
                             void* dv, int B, int Hq, int Hkv, int S, int D, float scale,
                             bool causal, void* ws, hipStream_t stream) {
   if ((long long)B * Hq * S == 0) return hipSuccess;
+  if (dtype == kDtypeF32)
+    return launch_flash_bwd_f32((const float*)q, (const float*)k, (const float*)v, (const float*)o,
+                                (const float*)dout, lse, (float*)dq, (float*)dk, (float*)dv, B,
+                                Hq, Hkv, S, D, scale, causal, ws, stream);
   float* w = (float*)ws;
 #define CA_BWD_CASE(TR, DD)                                                                   \
   if (D == DD)                                                                                \

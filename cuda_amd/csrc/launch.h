@@ -31,6 +31,12 @@ hipError_t launch_flash_bwd(int dtype, const void* q, const void* k, const void*
                             void* dv, int B, int Hq, int Hkv, int S, int D, float scale,
                             bool causal, void* ws, hipStream_t stream);
 
+// float32 backward (backward_f32.hip), same contract and workspace
+hipError_t launch_flash_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                                const float* dout, const float* lse, float* dq, float* dk,
+                                float* dv, int B, int Hq, int Hkv, int S, int D, float scale,
+                                bool causal, void* ws, hipStream_t stream);
+
 // Compute units of the current device (cached per device; 0 if unknown).
 inline int device_cus() {
   static int cached[64];

@@ -68,7 +68,7 @@ ca_status ca_flash_attention_fwd_lse(ca_dtype dtype, const void* q, const void* 
  * o, its gradient dout and the forward's natural-log LSE [batch, num_q_heads,
  * seq_len] float32. q, o, dout, dq: [batch, num_q_heads, seq_len, head_dim];
  * k, v, dk, dv: [batch, num_kv_heads, seq_len, head_dim] (GQA: dk, dv sum
- * over the q heads of a kv head). dtype bf16 or fp16 (float32: CA_UNSUPPORTED).
+ * over the q heads of a kv head). dtype float32, fp16 or bf16.
  * Replaces dispatch_flash_attention_v2_backward<T> (kernels_api.h:65-69);
  * dq, dk, dv are written, not accumulated. workspace:
  * ca_flash_attention_bwd_workspace_bytes(batch, num_q_heads, seq_len). */

@@ -88,9 +88,9 @@ def test_backward_entry_points_validate():
     assert lib.ca_flash_attention_bwd_workspace_bytes(2, 8, 100) == 2 * 8 * 100 * 8
     assert lib.ca_flash_attention_bwd_workspace_bytes(0, 8, 100) == 0
     args = [L.CA_BF16, P, P, P, P, P, P, P, P, P, 1, 4, 2, 64, 64, 0.1, 1, P, 1 << 20, None]
-    f32 = list(args)
-    f32[0] = L.CA_F32
-    assert _status("ca_flash_attention_bwd", *f32) == L.CA_UNSUPPORTED
+    bad_dtype = list(args)
+    bad_dtype[0] = 7
+    assert _status("ca_flash_attention_bwd", *bad_dtype) == L.CA_INVALID_ARGUMENT
     small_ws = list(args)
     small_ws[18] = 16
     assert _status("ca_flash_attention_bwd", *small_ws) == L.CA_INVALID_ARGUMENT

@@ -158,11 +158,32 @@ def test_backward_single_key(dev):
     assert torch.allclose(dv.float(), dout.float(), atol=1e-2, rtol=0)
 
 
-def test_backward_float32_unsupported(dev):
-    q, k, v = qkv(1, 2, 64, 64, torch.float32, dev)
-    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v)
-    with pytest.raises(RuntimeError, match="Supported: Float16, BFloat16"):
-        cuda_llm.flash_attention_backward(torch.randn_like(q), q, k, v, out, lse)
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("b,hq,hkv,s", [(1, 2, 2, 64), (1, 2, 2, 100), (2, 4, 1, 300),
+                                        (1, 2, 2, 1)])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_backward_float32(dev, head_dim, b, hq, hkv, s, is_causal):
+    """The float32 instantiation (flash_attention_bwd_instantiations.cu:4):
+    the reference grid plus GQA and S = 1, against the float64 oracle on the
+    same inputs with the float32 forward's out and LSE, to 1e-3."""
+    got, ref = _run_backward(b, hq, hkv, s, head_dim, torch.float32, dev, is_causal, seed=3)
+    for name, a, r in zip(("dq", "dk", "dv"), got, ref):
+        _check_grad(a, r, f"f32 {name}", atol=1e-3, rtol=1e-3, mean_abs=1e-4)
+
+
+def test_autograd_float32(dev):
+    q, k, v = qkv(1, 2, 200, 128, torch.float32, dev)
+    q, k, v = (t.requires_grad_() for t in (q, k, v))
+    out = cuda_llm.flash_attention(q, k, v, is_causal=True)
+    dout = torch.randn_like(out)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    qn, kn, vn, dn = (to_np(t.detach()).astype(np.float64) for t in (q, k, v, dout))
+    on = to_np(out.detach()).astype(np.float64)
+    lse = oracle.attention_lse(qn, kn, is_causal=True, dtype=np.float64)
+    ref = oracle.attention_backward(dn, qn, kn, vn, on, lse, is_causal=True, dtype=np.float64)
+    for name, a, r in zip(("dq", "dk", "dv"), (q.grad, k.grad, v.grad), ref):
+        _check_grad(a, r, f"f32 autograd {name}", atol=1e-3, rtol=1e-3, mean_abs=1e-4)
 
 
 @pytest.mark.parametrize("b,h,s,is_causal", [(4, 16, 2304, True), (4, 16, 2048, True),
