@@ -38,12 +38,6 @@ namespace ca {
 // so a wave's MFMAs win issue over its partner wave's softmax VALU on the same
 // SIMD (+1-2.5 % measured; the head-dim-64 kernel, whose SIMDs hold waves of
 // independent workgroups, measured 2 % slower with it and does not use it).
-#ifndef CA_PF_PP
-#define CA_PF_PP 0
-#endif
-#ifndef CA_PF_MDEPTH
-#define CA_PF_MDEPTH 4
-#endif
 #ifndef CA_PF_STALE
 #define CA_PF_STALE 1
 #endif
@@ -400,9 +394,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // row max only on a wave's first tile (stale_softmax); 8-wave tiles (at
   // three waves per SIMD its rare path leaves too few registers)
   constexpr bool STALE = CA_PF_STALE != 0 && !PIPE && kNW == 8;
-  // ping-pong schedule (see the tile walk): 8 waves, two per SIMD
-  constexpr bool PP = CA_PF_PP && !PIPE && NH == 1 && kNW == 8 && kStages == 4;
-  constexpr int kLoaders = PP ? kNW / 2 : (kTileB / 1024) % kNW == 0 ? kNW : 8;
+  constexpr int kLoaders = (kTileB / 1024) % kNW == 0 ? kNW : 8;
   constexpr int kDmaPerWave = kTileB / 1024 / kLoaders;  // 1 KB loads per loader per tile (K, and V)
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
@@ -615,67 +607,6 @@ __device__ CA_INLINE void prefill_d128_qtile(
     for (int nb = 0; nb < NH; ++nb) l_run[nb] += psum[nb][0] + psum[nb][1];
   };
 
-  // Ping-pong MFMA block (NH = 1): O^T += V(t)^T P^T (16 steps, if PV) then
-  // S^T(tn) = K(tn) Q^T (8 steps, if QK) as one stream of LDS fragments,
-  // MD steps in flight across the PV -> QK boundary (a wave that runs its
-  // MFMAs alone needs its operand reads issued well ahead of use). Each step
-  // reads two fragments: V^T halves (tr16) or the K rows of both key blocks.
-  auto mfma_block = [&](int t, int tn, auto pv_tag, auto qk_tag) CA_INLINE {
-    constexpr bool PV = decltype(pv_tag)::value;
-    constexpr bool QK = decltype(qk_tag)::value;
-    constexpr int S0 = PV ? 0 : 16, S1 = QK ? 24 : 16;
-    constexpr int MD = CA_PF_MDEPTH;
-    const uint32_t va1 = stage(PV ? t : 0) + vofs1, va2 = stage(PV ? t : 0) + vofs2;
-    const uint32_t ka = stage(QK ? tn : 0) + kofs;
-    auto st_ob = [](int st) CA_INLINE { return CA_PF_PVX ? (st & 3) : (st >> 2); };
-    auto st_kk = [](int st) CA_INLINE { return CA_PF_PVX ? (st >> 2) : (st & 3); };
-    u32x4 fr[MD + 1][2];
-    auto rd = [&](int st, int buf) CA_INLINE {
-      if (st < 16) {
-        const uint32_t x = 64 * st_ob(st);
-        u32x2 a, b;
-        switch (st_kk(st)) {
-          case 0: a = lds_read_tr16<0>(va1 ^ x); b = lds_read_tr16<0>(va2 ^ x); break;
-          case 1: a = lds_read_tr16<4096>(va1 ^ x); b = lds_read_tr16<4096>(va2 ^ x); break;
-          case 2: a = lds_read_tr16<8192>(va1 ^ x); b = lds_read_tr16<8192>(va2 ^ x); break;
-          default: a = lds_read_tr16<12288>(va1 ^ x); b = lds_read_tr16<12288>(va2 ^ x); break;
-        }
-        fr[buf][0] = u32x4{a[0], a[1], b[0], b[1]};
-      } else {
-        const uint32_t an = ka ^ (32 * (st - 16));
-        fr[buf][0] = lds_read_b128<0>(an);
-        fr[buf][1] = lds_read_b128<32 * kRowB>(an);
-      }
-    };
-    if (QK) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[mb][0][r] = 0.f;
-    }
-    if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-    for (int st = S0; st < S0 + MD && st < S1; ++st) rd(st, (st - S0) % (MD + 1));
-#pragma unroll
-    for (int st = S0; st < S1; ++st) {
-      const int cb = (st - S0) % (MD + 1);
-      if (st + MD < S1) rd(st + MD, (st + MD - S0) % (MD + 1));
-      // fragments of the steps after st still in flight: two reads each
-      const int ahead = (S1 - 1 - st) < MD ? (S1 - 1 - st) : MD;
-      wait_lgkm_n(2 * ahead);
-      after_wait(fr[cb][0]);
-      if (st >= 16) after_wait(fr[cb][1]);
-      if (st < 16) {
-        o[st_ob(st)][0] = Tr::mfma32(__builtin_bit_cast(vec8, fr[cb][0]), pb[0][st_kk(st)], o[st_ob(st)][0]);
-      } else {
-        const int ks = st - 16;
-        sacc[0][0] = Tr::mfma32(__builtin_bit_cast(vec8, fr[cb][0]), qv[0][ks], sacc[0][0]);
-        sacc[1][0] = Tr::mfma32(__builtin_bit_cast(vec8, fr[cb][1]), qv[0][ks], sacc[1][0]);
-      }
-    }
-    if (CA_PF_PRIO) __builtin_amdgcn_s_setprio(0);
-  };
-
   // Phase A: S^T(tn) = K(tn) Q^T (if QK), with the exponentials of the tile
   // in sv (if EXP) after the MFMAs, one pair each.
   auto phase_a = [&](int tn, auto qk_tag, auto exp_tag) CA_INLINE {
@@ -796,7 +727,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
   using F_ = std::false_type;
   constexpr int DIST = kStages - 1;  // tiles in flight ahead of the one waited for
 #pragma unroll
-  for (int tt = 0; tt < (PP ? 2 : DIST); ++tt) issue(tt);
+  for (int tt = 0; tt < DIST; ++tt) issue(tt);
   // Barrier t: every wave has its loads of tile t + LEAD resident (PIPE: A(t)
   // reads K(t+1)) and is past its last read of tile t - 1, whose slot then
   // takes tile t + DIST.
@@ -807,62 +738,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
     issue(t + DIST);
   };
   int t = 0;
-  if (PP) {
-    // Ping-pong: per tile j, one MFMA block PV(j-1) + QK(j) and one VALU
-    // block (max, rescale, exponentials of tile j), a workgroup barrier before
-    // each. The trailing waves (w >= kNW/2; waves w and w + kNW/2 share a
-    // SIMD) meet one extra barrier first, so they run half a step behind and
-    // each wave's VALU block runs under its SIMD partner's MFMA block. The
-    // leading waves load the tiles, two ahead: before MFMA block j they wait
-    // for tile j (which the trailing waves first read half a step later), and
-    // after that barrier the slot of tile j-2 (last read by the trailing
-    // waves' PV in their MFMA block j-1) is free for tile j+2.
-    // Every wave runs n_tiles + 1 steps of two barriers; the first, the
-    // wave's last (masked) tile and its final PV are peeled out of the loop
-    // so that no accumulator is updated under a condition.
-    const bool trailing = wave >= kNW / 2;
-    if (trailing) __builtin_amdgcn_s_barrier();
-    auto mfma_barrier = [&](int j) CA_INLINE {
-      if (loader) wait_vmcnt<2 * kDmaPerWave>();  // tile j landed (j+1 may be in flight)
-      __builtin_amdgcn_s_barrier();
-      issue(j + 2);
-    };
-    auto valu = [&](int j, auto mask_tag) CA_INLINE {
-      phase_b(-1, j, F_{}, T_{}, mask_tag);  // max of S^T(j), rescale
-      phase_a(-1, F_{}, T_{});               // P(j)
-    };
-    int j = 0;
-    if (w_tiles > 0) {
-      mfma_barrier(0);
-      mfma_block(-1, 0, F_{}, T_{});  // S^T(0)
-      __builtin_amdgcn_s_barrier();
-      if (w_tiles == 1) valu(0, T_{});
-      else valu(0, F_{});
-      for (j = 1; j + 1 < w_tiles; ++j) {
-        mfma_barrier(j);
-        mfma_block(j - 1, j, T_{}, T_{});  // O^T += V(j-1)^T P(j-1)^T, S^T(j)
-        __builtin_amdgcn_s_barrier();
-        valu(j, F_{});
-      }
-      if (j + 1 == w_tiles) {  // the wave's last tile (j >= 1)
-        mfma_barrier(j);
-        mfma_block(j - 1, j, T_{}, T_{});
-        __builtin_amdgcn_s_barrier();
-        valu(j, T_{});
-        ++j;
-      }
-      mfma_barrier(j);  // j == w_tiles: the last PV
-      mfma_block(j - 1, -1, T_{}, F_{});
-      __builtin_amdgcn_s_barrier();
-      ++j;
-    }
-    for (; j <= n_tiles; ++j) {
-      mfma_barrier(j);
-      __builtin_amdgcn_s_barrier();
-    }
-    if (!trailing) __builtin_amdgcn_s_barrier();
-    t = n_tiles;
-  } else if (PIPE) {
+  if (PIPE) {
     if (loader) wait_vmcnt<2 * kDmaPerWave * (kStages - 2)>();  // tile 0 landed (this wave's part)
     __builtin_amdgcn_s_barrier();                   // ... and every wave's
     if (w_tiles > 0) {
