@@ -13,10 +13,18 @@ constexpr int kDtypeF32 = 0;
 constexpr int kDtypeF16 = 1;
 constexpr int kDtypeBF16 = 2;
 
+// RoPE tables (fp32 [S, D], rotate-half) applied to Q as the 16-bit prefill
+// kernels load it; null: no rotation.
+struct RopeQ {
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+};
+
 // Prefill; lse (may be null) receives the natural-log row logsumexp [B, Hq, S].
+// rq (16-bit dtypes only) rotates q on load.
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
                           float* lse, int B, int Hq, int Hkv, int S, int D, float scale,
-                          bool causal, hipStream_t stream);
+                          bool causal, hipStream_t stream, RopeQ rq = RopeQ{});
 // float32 prefill (f32.hip)
 hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, float* lse,
                               int B, int Hq, int Hkv, int S, int D, float scale, bool causal,

@@ -45,13 +45,48 @@ namespace ca {
 #define CA_PF_PRIO 1
 #endif
 
+// Rotate-half RoPE of the Q operand of query row `pos` in registers (the
+// rotation of rope.hip, fused_rope_flash_attention_kernel.cuh:60-70): qv[ks]
+// holds dims 16 ks + 8 hl + e, so dim c < D/2 and its partner c + D/2 sit in
+// k-steps ks and ks + D/32 of the same lane.
+template <typename Tr, int D>
+__device__ __forceinline__ void rope_q(typename Tr::vec8 (&qv)[D / 16], RopeQ rq, int pos, int hl) {
+  using vec2 = typename Tr::vec2;
+  constexpr int H = D / 2, HKS = D / 32;
+  const float* cr = rq.cos + (size_t)pos * D;
+  const float* sr = rq.sin + (size_t)pos * D;
+#pragma unroll
+  for (int ks = 0; ks < HKS; ++ks) {
+    const int c = 16 * ks + 8 * hl;
+    float ca[8], sa[8], cb[8], sb[8];
+#pragma unroll
+    for (int h4 = 0; h4 < 8; h4 += 4) {
+      *(float4*)(ca + h4) = *(const float4*)(cr + c + h4);
+      *(float4*)(sa + h4) = *(const float4*)(sr + c + h4);
+      *(float4*)(cb + h4) = *(const float4*)(cr + c + H + h4);
+      *(float4*)(sb + h4) = *(const float4*)(sr + c + H + h4);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const float a0 = (float)qv[ks][e], a1 = (float)qv[ks][e + 1];
+      const float b0 = (float)qv[ks + HKS][e], b1 = (float)qv[ks + HKS][e + 1];
+      const vec2 lo = Tr::pack2(a0 * ca[e] - b0 * sa[e], a1 * ca[e + 1] - b1 * sa[e + 1]);
+      const vec2 hi = Tr::pack2(b0 * cb[e] + a0 * sb[e], b1 * cb[e + 1] + a1 * sb[e + 1]);
+      qv[ks][e] = lo[0];
+      qv[ks][e + 1] = lo[1];
+      qv[ks + HKS][e] = hi[0];
+      qv[ks + HKS][e + 1] = hi[1];
+    }
+  }
+}
+
 // One query tile (BM rows of head bh): the whole key walk and the output
 // store. Other waves may still read the LDS tiles when a wave returns.
 template <typename Tr, int D, int NW, bool CAUSAL>
 __device__ CA_INLINE void prefill_fwd_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int bh, int qt) {
+    int Hkv, float scale_log2, int bh, int qt, RopeQ rq) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
@@ -94,6 +129,7 @@ __device__ CA_INLINE void prefill_fwd_qtile(
       for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
     }
   }
+  if (rq.cos && myq < S) rope_q<Tr, D>(qv, rq, myq, hl);
 
   const int kv_end = CAUSAL ? min(S, q0 + BM) : S;
   const int n_tiles = (kv_end + BN - 1) / BN;
@@ -277,7 +313,7 @@ template <typename Tr, int D, int NW, bool CAUSAL>
 __global__ __launch_bounds__(NW * 64, 3) void prefill_fwd_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired) {
+    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, RopeQ rq) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(NW * 64, 3) void prefill_fwd_kernel(
     // the second tile restages the LDS buffers: every wave must be done reading them
     if (pass) __syncthreads();
     prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2,
-                                         pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0);
+                                         pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, rq);
   }
 }
 
@@ -379,7 +415,7 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __device__ CA_INLINE void prefill_d128_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int bh, int qt, int q_shift) {
+    int Hkv, float scale_log2, int bh, int qt, int q_shift, RopeQ rq) {
   using namespace pf128;
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
@@ -431,6 +467,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
       CA_DEVICE_ASM("" : "+a"(qv[nb][ks]));  // Q lives in AGPRs (an MFMA operand may)
 #endif
     }
+    if (rq.cos && myq[nb] >= 0 && myq[nb] < S) rope_q<Tr, kD>(qv[nb], rq, myq[nb], hl);
   }
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
@@ -838,7 +875,7 @@ template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STA
 __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift) {
+    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift, RopeQ rq) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
@@ -847,7 +884,8 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
     prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(
-        Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift);
+        Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift,
+        rq);
   }
 }
 
@@ -863,7 +901,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 template <typename Tr, bool CAUSAL, int BM>
 static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const void* v, void* o, float* lse,
                                          int B, int Hq, int Hkv, int S, float scale,
-                                         hipStream_t stream) {
+                                         hipStream_t stream, RopeQ rq) {
   constexpr int NH = CA_PF_NH;
   constexpr bool PIPE = CA_PF_PIPE;
   // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
@@ -886,12 +924,12 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
-                       n_qt, B * Hq, (int)grid, paired, q_shift);
+                       n_qt, B * Hq, (int)grid, paired, q_shift, rq);
   } else {
     hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
-                       n_qt, B * Hq, (int)grid, paired, q_shift);
+                       n_qt, B * Hq, (int)grid, paired, q_shift, rq);
   }
   return hipGetLastError();
 }
@@ -905,22 +943,22 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
 template <typename Tr, bool CAUSAL>
 static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o, float* lse,
                                       int B, int Hq, int Hkv, int S, float scale,
-                                      hipStream_t stream) {
+                                      hipStream_t stream, RopeQ rq) {
 #ifdef CA_PF_BM
-  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
+  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
 #else
   const long long n384 = (S + 383) / 384;
   const bool fits = n384 * 384 * 20 <= (long long)S * 21;
   const bool tall = !CA_PF_STALE && fits && (long long)B * Hq * n384 >= 2LL * device_cus();
-  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)
-              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);
+  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)
+              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
 #endif
 }
 
 template <typename Tr, int D, bool CAUSAL>
 static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o, float* lse,
                                    int B, int Hq, int Hkv, int S, float scale,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, RopeQ rq) {
 #ifndef CA_PF_NW
 #define CA_PF_NW 4
 #endif
@@ -934,23 +972,23 @@ static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, 
   hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
                      dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
                      (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, scale * kLog2e, n_qt, B * Hq,
-                     (int)grid, paired);
+                     (int)grid, paired, rq);
   return hipGetLastError();
 }
 
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
-                          hipStream_t stream) {
+                          hipStream_t stream, RopeQ rq) {
 #define CA_PREFILL_CASE(TR, DD)                                                          \
   if (D == DD) {                                                                         \
-    return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream) \
-                  : launch_prefill_t<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream); \
+    return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq) \
+                  : launch_prefill_t<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
   }
 #ifndef CA_PF_OLD128
 #define CA_PREFILL_128(TR)                                                                     \
   if (D == 128) {                                                                              \
-    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream)    \
-                  : launch_prefill_d128<TR, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream);  \
+    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)  \
+                  : launch_prefill_d128<TR, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
   }
 #else
 #define CA_PREFILL_128(TR) CA_PREFILL_CASE(TR, 128)

@@ -6,12 +6,14 @@
 //   x'[c] = x[c] cos[s][c] + r[c] sin[s][c],  r = [-x[D/2:], x[:D/2]],
 // with fp32 tables cos / sin [S, D].
 //
-// Q and K are rotated once by rope_kernel into a caller-provided workspace
-// (in the input dtype: that is the operand precision of the prefill
-// kernels), then the prefill kernels run on the rotated tensors. Every K row
-// is read by many query tiles, so rotating it once is cheaper than rotating
-// it in every tile that reads it; the pass is HBM-bound: q and k are read and
-// written once (the reference instead rotates inside its attention loop).
+// K is rotated once by rope_kernel into a caller-provided workspace (in the
+// input dtype: that is the operand precision of the prefill kernels): every
+// K row is read by many query tiles, so rotating it once is cheaper than
+// rotating it in every tile that reads it (the pass is HBM-bound: k read and
+// written once). Q is rotated by the 16-bit prefill kernels themselves as
+// they load it into registers (rope_q in prefill.hip); for float32 q is
+// rotated into the workspace as well. (The reference rotates both inside its
+// attention loop.)
 // One thread rotates 8 consecutive dims c .. c+7 of the first half together
 // with their partners c+D/2 .. c+D/2+7.
 #include "common.h"
@@ -95,16 +97,25 @@ size_t elem_bytes(int dtype) { return dtype == kDtypeF32 ? 4 : 2; }
 
 }  // namespace
 
+// float32: rotated q, then k (256-byte aligned); 16-bit: rotated k only.
 size_t rope_workspace_bytes(int dtype, int B, int Hq, int Hkv, int S, int D) {
   const size_t qb = (size_t)B * Hq * S * D * elem_bytes(dtype);
   const size_t kb = (size_t)B * Hkv * S * D * elem_bytes(dtype);
-  return ((qb + 255) & ~(size_t)255) + kb;
+  return dtype == kDtypeF32 ? ((qb + 255) & ~(size_t)255) + kb : kb;
 }
 
 hipError_t launch_rope_prefill(int dtype, const void* q, const void* k, const void* v,
                                const float* cos_tab, const float* sin_tab, void* o, int B, int Hq,
                                int Hkv, int S, int D, float scale, bool causal, void* ws,
                                hipStream_t stream) {
+  if (dtype != kDtypeF32) {
+    hipError_t e = rope(dtype, D, k, ws, cos_tab, sin_tab, (long long)B * Hkv * S, S, stream);
+    if (e != hipSuccess) return e;
+    RopeQ rq;
+    rq.cos = cos_tab;
+    rq.sin = sin_tab;
+    return launch_prefill(dtype, q, ws, v, o, nullptr, B, Hq, Hkv, S, D, scale, causal, stream, rq);
+  }
   const size_t qb = (size_t)B * Hq * S * D * elem_bytes(dtype);
   void* qr = ws;
   void* kr = (char*)ws + ((qb + 255) & ~(size_t)255);

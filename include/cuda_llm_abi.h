@@ -87,7 +87,8 @@ size_t ca_flash_attention_bwd_workspace_bytes(int batch, int num_q_heads, int se
  * token at position s; cos_tab, sin_tab: float32 [seq_len, head_dim]. Shapes,
  * masking and dtypes as ca_flash_attention_fwd (GQA allowed).
  * Replaces dispatch_fused_rope_flash_attention<T> (kernels_api.h:44-49).
- * workspace: ca_rope_workspace_bytes(...) (the rotated q and k). */
+ * workspace: ca_rope_workspace_bytes(...) (the rotated k; for float32 the
+ * rotated q as well: the 16-bit kernels rotate q as they load it). */
 ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const void* k,
                                         const void* v, const float* cos_tab, const float* sin_tab,
                                         void* o, int batch, int num_q_heads, int num_kv_heads,

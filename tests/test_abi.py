@@ -111,8 +111,12 @@ def test_backward_entry_points_validate():
 
 def test_rope_entry_validates():
     lib = L.load()
+    # 16-bit: the rotated k (q is rotated as the prefill loads it); float32:
+    # the rotated q (256-byte aligned), then k
     n = lib.ca_rope_workspace_bytes(L.CA_BF16, 2, 8, 2, 100, 64)
-    assert n == ((2 * 8 * 100 * 64 * 2 + 255) // 256) * 256 + 2 * 2 * 100 * 64 * 2
+    assert n == 2 * 2 * 100 * 64 * 2
+    n32 = lib.ca_rope_workspace_bytes(L.CA_F32, 2, 8, 2, 100, 64)
+    assert n32 == ((2 * 8 * 100 * 64 * 4 + 255) // 256) * 256 + 2 * 2 * 100 * 64 * 4
     args = [L.CA_BF16, P, P, P, P, P, P, 2, 8, 2, 100, 64, 0.1, 1, P, n, None]
     small = list(args)
     small[15] = n - 1
