@@ -207,7 +207,7 @@ def fused_rope_flash_attention(q, k, v, cos_tab, sin_tab, is_causal=True, softma
            "RoPE tables must be [seq_len, head_dim]")
     dt = _dtype_code(q, "Fused RoPE Attention")
     q, k, v = _aligned(q), _aligned(k), _aligned(v)
-    cos_f, sin_f = (t.to(torch.float32).contiguous() for t in (cos_tab, sin_tab))
+    cos_f, sin_f = (_aligned(t.to(torch.float32).contiguous()) for t in (cos_tab, sin_tab))
     out = torch.empty_like(q)
     hkv = k.shape[1]
     ws, nbytes = _workspace(int(_lib.load().ca_rope_workspace_bytes(dt, b, hq, hkv, s, d)), q.device)

@@ -306,7 +306,8 @@ ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const voi
   if (batch == 0 || seq_len == 0) return CA_OK;
   if (!q || !k || !v || !o || !cos_tab || !sin_tab)
     return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace))
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace) ||
+      !aligned16(cos_tab) || !aligned16(sin_tab))
     return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
   if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
     return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);

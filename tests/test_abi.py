@@ -125,6 +125,10 @@ def test_rope_entry_validates():
     no_tab = list(args)
     no_tab[4] = None
     assert _status("ca_fused_rope_flash_attention", *no_tab) == L.CA_INVALID_ARGUMENT
+    odd_tab = list(args)
+    odd_tab[5] = ctypes.c_void_p(16 + 4)  # the tables are read 16 bytes at a time
+    assert _status("ca_fused_rope_flash_attention", *odd_tab) == L.CA_INVALID_ARGUMENT
+    assert b"aligned" in lib.ca_last_error()
 
 
 def test_kv_append_validates():
