@@ -22,7 +22,7 @@ synchronisation. ``cpu_baseline`` times the numpy oracle on a bounded sample
 of the same inputs on this host's cores (a reported baseline only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|backward|copy|read]
+                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|backward|copy|read|refgrid]
 """
 import argparse
 import json
@@ -57,6 +57,37 @@ def time_steps(fn, steps, warmup):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per step
+
+
+def _stream_reader(nbytes):
+    """A call that streams `nbytes` of a resident buffer through ca_stream_read."""
+    import ctypes
+    import torch
+    from cuda_amd import _lib
+    x = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").random_(generator=_gen())
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return lambda: _lib.call("ca_stream_read", ctypes.c_void_p(x.data_ptr()), nbytes,
+                             ctypes.c_void_p(sink.data_ptr()), st)
+
+
+def time_cold(fn, reps=20, flush_bytes=1 << 30):
+    """Median ms of one call of `fn` issued right after a 1 GiB streaming read,
+    which leaves none of fn's inputs in the L2s or the 256 MB MALL."""
+    import torch
+    flush = _stream_reader(flush_bytes)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    torch.cuda.synchronize()
+    for e0, e1 in ev:
+        flush()
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    t = sorted(e0.elapsed_time(e1) for e0, e1 in ev)
+    return t[len(t) // 2]
 
 
 def _traffic(key):
@@ -98,11 +129,15 @@ def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
     import cuda_llm
     g = _gen()
     q, k, v = (torch.randn(B, H, S, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
-    ms = time_steps(lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal), steps, warmup)
+    fn = lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal)
+    ms = time_steps(fn, steps, warmup)
+    cold = time_cold(fn)
     flops = (2.0 if causal else 4.0) * B * H * S * S * D
     tf = flops / (ms * 1e-3) / 1e12
     return dict(ms=ms, value=tf, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_TFLOPS,
                 work=flops, qkv=(q, k, v), causal=causal,
+                cold={"ms_per_step": round(cold, 4), "value": round(flops / (cold * 1e-3) / 1e12, 2),
+                      "note": "median of 20 single calls, each after a 1 GiB streaming read"},
                 config={"workload": f"C2{'' if causal else chr(39)} bf16 {'causal' if causal else 'non-causal'} prefill (flash_attention)",
                         "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal})
 
@@ -289,18 +324,131 @@ def w_copy(steps, warmup, nbytes=2 << 30):
 def w_read(steps, warmup, nbytes=4 << 30):
     """Streaming-read ceiling: ca_stream_read over a resident buffer (the
     measured second denominator of the HBM-bound decode lines)."""
-    import ctypes
-    import torch
-    from cuda_amd import _lib
-    x = torch.empty(nbytes // 4, dtype=torch.int32, device="cuda").random_(generator=_gen())
-    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    fn = lambda: _lib.call("ca_stream_read", ctypes.c_void_p(x.data_ptr()), nbytes,
-                           ctypes.c_void_p(sink.data_ptr()), st)
-    ms = time_steps(fn, steps, warmup)
+    ms = time_steps(_stream_reader(nbytes), steps, warmup)
     return dict(ms=ms, value=nbytes / (ms * 1e-3) / 1e9, unit="GB/s", bound="hbm",
                 peak=PEAK_HBM_GBS, work=nbytes,
                 config={"workload": "streaming read (measured HBM read ceiling)", "bytes": nbytes})
+
+
+def _sdpa_ms(q, k, v, causal, steps, warmup):
+    """torch's own scaled_dot_product_attention on the same inputs, flash
+    backend only (no math fallback); None where torch has no such kernel."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    gqa = q.shape[1] != k.shape[1]
+    try:
+        with sdpa_kernel(SDPBackend.FLASH_ATTENTION):
+            return time_steps(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal,
+                                                                      enable_gqa=gqa),
+                              steps, warmup)
+    except RuntimeError as e:
+        log(f"torch sdpa (flash) unavailable: {str(e).splitlines()[0][:120]}")
+        return None
+
+
+def w_refgrid(steps, warmup):
+    """The reference benchmark's own grid (benchmark_pytorch.py:627-658): fp16,
+    head dim 64, its shapes, table layouts and units (prefill TFLOP/s with
+    2 (causal) or 4 x B H S^2 D, backward 10 B H S^2 D, decode GB/s of K + V
+    bytes N H L D elem 2), run on this build's entry points. Prefill lines
+    also time torch's flash SDPA on the same inputs. The C2 shape closes the
+    grid for the same comparison at head dim 128. Not part of the default run."""
+    import torch
+    import cuda_llm
+    st, wu = min(steps, 100), min(warmup, 50)
+    f16 = torch.float16
+    g = _gen()
+    rows = []
+
+    def randn(*shape, dtype=f16):
+        return torch.randn(*shape, device="cuda", generator=g).to(dtype)
+
+    def add(name, ref, ms, work, unit, sdpa=None, **shape):
+        val = work / (ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+        row = {"case": name, "ref": ref, **shape, "ms": round(ms, 4), "value": round(val, 2),
+               "unit": unit}
+        if sdpa is not None:
+            row["torch_sdpa_ms"] = round(sdpa, 4)
+            row["speedup_vs_torch_sdpa"] = round(sdpa / ms, 2)
+        rows.append(row)
+        log(f"{name} {shape}: {ms:.4f} ms, {val:.1f} {unit}"
+            + (f", torch sdpa {sdpa:.4f} ms" if sdpa else ""))
+
+    def prefill(name, ref, fn, B, Hq, Hkv, S, D, causal, dtype=f16, rope=False):
+        q, k, v = randn(B, Hq, S, D, dtype=dtype), randn(B, Hkv, S, D, dtype=dtype), \
+            randn(B, Hkv, S, D, dtype=dtype)
+        if rope:
+            inv = 1.0 / (10000.0 ** (torch.arange(0, D, 2, device="cuda").float() / D))
+            fr = torch.outer(torch.arange(S, device="cuda").float(), inv)
+            emb = torch.cat((fr, fr), -1)
+            cs, sn = emb.cos().contiguous(), emb.sin().contiguous()
+            ms = time_steps(lambda: fn(q, k, v, cs, sn, is_causal=causal), st, wu)
+            sd = None
+        else:
+            ms = time_steps(lambda: fn(q, k, v, is_causal=causal), st, wu)
+            sd = _sdpa_ms(q, k, v, causal, st, wu)
+        add(name, ref, ms, (2.0 if causal else 4.0) * B * Hq * S * S * D, "TFLOP/s", sd,
+            B=B, Hq=Hq, Hkv=Hkv, S=S, D=D, causal=causal, dtype=str(dtype).split(".")[-1])
+        del q, k, v
+
+    for S in (2048, 4096, 8192):
+        prefill("flash_attention_forward", "benchmark_pytorch.py:636-637",
+                cuda_llm.flash_attention_forward, 2, 32, 32, S, 64, True)
+    for N in (32, 64, 128):
+        nb = 2048 // 16
+        q = randn(N, 32, 64)
+        kc, vc = randn(N * nb, 32, 64, 16), randn(N * nb, 32, 64, 16)
+        tab = torch.arange(N * nb, device="cuda", dtype=torch.int32).view(N, nb)
+        lens = torch.full((N,), 2048, device="cuda", dtype=torch.int32)
+        ms = time_steps(lambda: cuda_llm.paged_attention_forward(q, kc, vc, tab, lens), st, wu)
+        add("paged_attention_forward", "benchmark_pytorch.py:639-641", ms, N * 32 * 2048 * 64 * 2 * 2,
+            "GB/s", N=N, H=32, D=64, context=2048)
+        del q, kc, vc
+    for N in (32, 64, 128):
+        nb = 4096 // 16
+        q = randn(N, 32, 64)
+        # valid e4m3 bytes (0x7f / 0xff are NaN codes), per-(page, head) scale 0.01
+        codes = lambda: (torch.randint(0, 255, (N * nb, 32, 64, 16), device="cuda", generator=g,
+                                       dtype=torch.int32) % 127
+                         + 128 * torch.randint(0, 2, (N * nb, 32, 64, 16), device="cuda",
+                                               generator=g, dtype=torch.int32)).to(torch.uint8)
+        kc, vc = codes(), codes()
+        sc = torch.full((N * nb, 32), 0.01, device="cuda")
+        tab = torch.arange(N * nb, device="cuda", dtype=torch.int32).view(N, nb)
+        lens = torch.full((N,), 4096, device="cuda", dtype=torch.int32)
+        ms = time_steps(lambda: cuda_llm.fp8_paged_attention_forward(q, kc, vc, sc, sc, tab, lens),
+                        st, wu)
+        add("fp8_paged_attention_forward", "benchmark_pytorch.py:643-645", ms,
+            N * 32 * 4096 * 64 * 1 * 2, "GB/s", N=N, H=32, D=64, context=4096)
+        del q, kc, vc
+    for S in (2048, 4096):
+        prefill("fused_rope_flash_attention", "benchmark_pytorch.py:647-649",
+                cuda_llm.fused_rope_flash_attention, 2, 32, 32, S, 64, True, rope=True)
+    for S in (2048, 4096, 8192):
+        prefill("fused_gqa_forward", "benchmark_pytorch.py:651-653",
+                cuda_llm.fused_gqa_forward, 2, 32, 8, S, 64, True)
+    for S in (4096, 8192, 16384):
+        q, k, v = randn(8, 32, 1, 64), randn(8, 32, S, 64), randn(8, 32, S, 64)
+        ms = time_steps(lambda: cuda_llm.async_flash_decode(q, k, v), st, wu)
+        add("async_flash_decode", "benchmark_pytorch.py:655-657", ms, 8 * 32 * S * 64 * 2 * 2,
+            "GB/s", B=8, H=32, S_kv=S, D=64)
+        del q, k, v
+    for S in (2048, 4096):
+        q, k, v, do = (randn(2, 32, S, 64) for _ in range(4))
+        o, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=False)
+        ms = time_steps(lambda: cuda_llm.flash_attention_backward(do, q, k, v, o, lse,
+                                                                  is_causal=False), st, wu)
+        add("flash_attention_backward", "benchmark_pytorch.py:659-661", ms,
+            10.0 * 2 * 32 * S * S * 64, "TFLOP/s", B=2, H=32, S=S, D=64, causal=False)
+        del q, k, v, do, o, lse
+    for S in (4096, 8192, 16384):
+        prefill("flash_attention_v3_hopper", "benchmark_pytorch.py:667-669",
+                cuda_llm.flash_attention_v3_hopper, 2, 32, 32, S, 64, False)
+    prefill("flash_attention (C2)", "BASELINE config C2", cuda_llm.flash_attention, 4, 32, 32, 4096,
+            128, True, dtype=torch.bfloat16)
+    torch.cuda.empty_cache()
+    return rows
 
 
 _READ_CEILING = {}
@@ -326,6 +474,7 @@ WORKLOADS = {
     "backward": w_backward,
     "copy": w_copy,
     "read": w_read,
+    "refgrid": w_refgrid,
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
                "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5",
@@ -341,6 +490,8 @@ def summary(name, r, read_gbs=None):
            "roofline": {"bound": r["bound"], "achieved": round(r["value"], 2), "peak": r["peak"],
                         "unit": r["unit"], "frac": round(r["value"] / r["peak"], 4),
                         "traffic": _traffic(TRAFFIC_KEY.get(name, name))}}
+    if "cold" in r:
+        out["cold"] = r["cold"]
     if read_gbs:
         out["roofline"]["measured_read_peak"] = round(read_gbs, 2)
         out["roofline"]["frac_of_measured"] = round(r["value"] / read_gbs, 4)
@@ -370,6 +521,12 @@ def main():
     torch.cuda.set_device(0)
     props = torch.cuda.get_device_properties(0)
 
+    if args.workload == "refgrid":
+        rows = w_refgrid(args.steps, args.warmup)
+        print(json.dumps({"metric": "reference benchmark grid (benchmark_pytorch.py)", "n_gpus": 1,
+                          "data": "synthetic, seeded", "device": props.name, "rows": rows}),
+              flush=True)
+        return
     head = "prefill" if args.workload == "all" else args.workload
     log(f"{head} ...")
     r = WORKLOADS[head](args.steps, args.warmup)
@@ -394,6 +551,7 @@ def main():
         "data": "synthetic, seeded (torch generator seed 0), resident in HBM",
         "config": dict(s["config"], parallelism="none (1 GPU)"),
         "roofline": s["roofline"],
+        **({"cold": s["cold"]} if "cold" in s else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
     if not args.no_cpu_baseline and head in ("prefill", "prefill_nc", "decode_fp8", "decode_bf16"):

@@ -186,16 +186,17 @@ def test_autograd_float32(dev):
         _check_grad(a, r, f"f32 autograd {name}", atol=1e-3, rtol=1e-3, mean_abs=1e-4)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("b,h,s,is_causal", [(4, 16, 2304, True), (4, 16, 2048, True),
                                              (2, 8, 1100, False)])
-def test_backward_large_paired_tiles(dev, b, h, s, is_causal):
+def test_backward_large_paired_tiles(dev, b, h, s, is_causal, d):
     """Grids large enough for the causal launches to pair tiles per workgroup
     (9 tiles per head: the middle tiles of two heads make one work item); the
     kernel computes every head, sampled heads are checked against the oracle
     on the kernel forward's own out and LSE."""
     g = torch.Generator(device=dev).manual_seed(7)
-    q, k, v = qkv(b, h, s, 128, torch.bfloat16, dev, gen=g)
-    dout = torch.randn(b, h, s, 128, device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = qkv(b, h, s, d, torch.bfloat16, dev, gen=g)
+    dout = torch.randn(b, h, s, d, device=dev, generator=g).to(torch.bfloat16)
     out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal)
     dq, dk, dv = cuda_llm.flash_attention_backward(dout, q, k, v, out, lse, is_causal=is_causal)
     torch.cuda.synchronize()
