@@ -7,10 +7,10 @@
 // 82-83 causal tile bound, 179-229 online softmax, 223 l == 0 -> 0).
 //
 // Work decomposition
-//   one workgroup = NW waves = BM = 32*NW query rows of one (b, h);
+//   one workgroup = 8 waves = 256 query rows of one (b, h);
 //   each wave owns 32 query rows for the whole KV walk;
-//   KV tiles of BN = 64 keys are staged in LDS (double buffered, one barrier
-//   per tile) and shared by the NW waves.
+//   KV tiles of 64 keys travel HBM -> LDS by buffer loads into a ring of 4
+//   tiles (one barrier per tile) shared by the 8 waves.
 // Per wave and KV tile (32x32x16 MFMAs):
 //   S^T[64 keys x 32 q] = K Q^T   (A = K rows from LDS, B = Q from registers)
 //   softmax over keys: keys live in the registers of a lane (16 per 32-key
@@ -34,10 +34,9 @@
 
 namespace ca {
 
-// Head-dim-128 kernel: MFMA blocks run at raised wave priority (s_setprio),
-// so a wave's MFMAs win issue over its partner wave's softmax VALU on the same
-// SIMD (+1-2.5 % measured; the head-dim-64 kernel, whose SIMDs hold waves of
-// independent workgroups, measured 2 % slower with it and does not use it).
+// MFMA blocks run at raised wave priority (s_setprio), so a wave's MFMAs win
+// issue over its partner wave's softmax VALU on the same SIMD (+1-2.5 %
+// measured at head dim 128).
 #ifndef CA_PF_STALE
 #define CA_PF_STALE 1
 #endif
@@ -80,254 +79,8 @@ __device__ __forceinline__ void rope_q(typename Tr::vec8 (&qv)[D / 16], RopeQ rq
   }
 }
 
-// One query tile (BM rows of head bh): the whole key walk and the output
-// store. Other waves may still read the LDS tiles when a wave returns.
-template <typename Tr, int D, int NW, bool CAUSAL>
-__device__ CA_INLINE void prefill_fwd_qtile(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int bh, int qt, RopeQ rq) {
-  using vec8 = typename Tr::vec8;
-  using vec4 = typename Tr::vec4;
-  using vec2 = typename Tr::vec2;
-  constexpr int BM = 32 * NW;
-  constexpr int BN = 64;
-  constexpr int KS = D + 8;    // K row stride (elements): permuted-row b128 reads hit distinct banks
-  constexpr int VS = D + 32;   // V row stride: 4 consecutive rows land 64 B apart mod 256 B (tr16 reads)
-  constexpr int NKS = D / 16;  // QK k-steps
-  constexpr int NOB = D / 32;  // O^T row blocks
-  constexpr int CHUNKS = D / 8;                 // 16-byte chunks per row
-  constexpr int ROWS_PER_PASS = NW * 64 / CHUNKS;
-  constexpr int PASSES = BN / ROWS_PER_PASS;
-  static_assert(PASSES * ROWS_PER_PASS == BN, "tile staging must cover the tile");
-
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BN * VS];
-
-  const int b = bh / Hq, h = bh % Hq;
-  const int hk = h / (Hq / Hkv);
-  const int q0 = qt * BM;
-  const uint16_t* Qp = Q + (size_t)(b * Hq + h) * S * D;
-  uint16_t* Op = O + (size_t)(b * Hq + h) * S * D;
-  const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
-  const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
-
-  const int tid = __builtin_amdgcn_workitem_id_x();
-  const int wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hl = lane >> 5;
-  const int qw0 = q0 + wave * 32;
-  const int myq = qw0 + l32;
-
-  // Q as the B operand of S^T = K Q^T: lane (q = l32, k-group hl)
-  vec8 qv[NKS];
-#pragma unroll
-  for (int ks = 0; ks < NKS; ++ks) {
-    if (myq < S) {
-      qv[ks] = *(const vec8*)(Qp + (size_t)myq * D + 16 * ks + 8 * hl);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
-    }
-  }
-  if (rq.cos && myq < S) rope_q<Tr, D>(qv, rq, myq, hl);
-
-  const int kv_end = CAUSAL ? min(S, q0 + BM) : S;
-  const int n_tiles = (kv_end + BN - 1) / BN;
-
-  const int st_row = tid / CHUNKS, st_col = (tid % CHUNKS) * 8;
-  u32x4 kreg[PASSES], vreg[PASSES];
-  auto gload = [&](int t) {
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int row = t * BN + st_row + p * ROWS_PER_PASS;
-      if (row < S) {
-        kreg[p] = *(const u32x4*)(Kp + (size_t)row * D + st_col);
-        vreg[p] = *(const u32x4*)(Vp + (size_t)row * D + st_col);
-      } else {
-        kreg[p] = u32x4{0, 0, 0, 0};
-        vreg[p] = u32x4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-      const int r = st_row + p * ROWS_PER_PASS;
-      *(u32x4*)(&Ks[buf][r * KS + st_col]) = kreg[p];
-      *(u32x4*)(&Vs[buf][r * VS + st_col]) = vreg[p];
-    }
-  };
-
-  f32x16 o[NOB];
-#pragma unroll
-  for (int i = 0; i < NOB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m_run = kNegInf, l_run = 0.f;
-
-  const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
-  // tr16 source-lane coordinates for the V^T operand
-  const int g16 = lane >> 4, s16 = lane & 15;
-  const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
-  const int tr_col = 16 * (g16 & 1) + 4 * (s16 & 3);
-
-  // One key tile. The wave's first tile (t = 0, never skipped) takes the row
-  // max; later tiles take their exponentials against the running max as it
-  // stands (see stale_softmax of the head-dim-128 kernel for the bound).
-  constexpr float kStaleMax = std::is_same<Tr, BF16>::value ? 0x1p48f : 0x1p15f;
-  auto step = [&](int t, auto first_tag) CA_INLINE {
-    constexpr bool FIRST = decltype(first_tag)::value;
-    const int buf = t & 1;
-    lstore(buf);
-    __syncthreads();
-    if (t + 1 < n_tiles) gload(t + 1);
-    const int k0 = t * BN;
-    if (CAUSAL && k0 > qw0 + 31) return;  // tile entirely above this wave's rows
-
-    const uint16_t* Kb = Ks[buf];
-    const uint16_t* Vb = Vs[buf];
-    f32x16 s[2];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) { s[0][r] = 0.f; s[1][r] = 0.f; }
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const vec8 a = *(const vec8*)(Kb + (32 * mb + krow) * KS + 16 * ks + 8 * hl);
-        s[mb] = Tr::mfma32(a, qv[ks], s[mb]);
-      }
-    }
-
-    // Softmax in the log2 domain with the scale folded into one FMA per
-    // logit: p = 2^(s*c - m). The row max is taken over the raw logits (min
-    // for a negative scale) and scaled once; a masked logit is set to the
-    // value whose scaled image is -inf.
-    const bool need_mask = CAUSAL ? (k0 + BN - 1 > qw0) : (k0 + BN > S);
-    const bool pos = scale_log2 >= 0.f;
-    if (need_mask) {
-      const float mv = pos ? kNegInf : -kNegInf;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + 32 * mb + 16 * (r >> 3) + 8 * hl + (r & 7);
-          const bool masked = (key >= S) || (CAUSAL && key > myq);
-          if (masked) s[mb][r] = mv;
-        }
-    }
-    auto full_max = [&]() CA_INLINE {
-      float tm;
-      if (pos) {
-        tm = max3(s[0][0], s[0][1], s[0][2]);
-#pragma unroll
-        for (int i = 3; i < 31; i += 2) tm = max3(tm, s[i >> 4][i & 15], s[(i + 1) >> 4][(i + 1) & 15]);
-        tm = __builtin_fmaxf(tm, s[1][15]);
-      } else {
-        tm = s[0][0];
-#pragma unroll
-        for (int i = 1; i < 32; ++i) tm = __builtin_fminf(tm, s[i >> 4][i & 15]);
-      }
-      const float tmax = pair32_max(tm * scale_log2);
-      if (wave_any(tmax > m_run + 8.0f)) {
-        const float m_new = __builtin_fmaxf(m_run, tmax);
-        const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
-#pragma unroll
-        for (int i = 0; i < NOB; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-        l_run *= alpha;
-        m_run = m_new;
-      }
-    };
-    float psum = 0.f;
-    vec8 pb[4];
-    auto weights = [&]() CA_INLINE {
-      const float msub = (m_run == kNegInf) ? 0.f : m_run;
-      psum = 0.f;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int base = (kk >> 1) * 16 + (kk & 1) * 8;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i0 = base + 2 * j, i1 = i0 + 1;
-          const float p0 = fast_exp2(__builtin_fmaf(s[i0 >> 4][i0 & 15], scale_log2, -msub));
-          const float p1 = fast_exp2(__builtin_fmaf(s[i1 >> 4][i1 & 15], scale_log2, -msub));
-          psum += p0 + p1;
-          const vec2 pk = Tr::pack2(p0, p1);
-          pb[kk][2 * j] = pk[0];
-          pb[kk][2 * j + 1] = pk[1];
-        }
-      }
-    };
-    if (FIRST) {
-      full_max();
-      weights();
-    } else {
-      weights();
-      if (__builtin_expect(wave_any(!(psum <= kStaleMax)), 0)) {
-        full_max();
-        weights();
-      }
-    }
-    l_run += psum;
-
-#pragma unroll
-    for (int ob = 0; ob < NOB; ++ob) {
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint16_t* src = Vb + (16 * kk + tr_row) * VS + 32 * ob + tr_col;
-        const vec4 lo = Tr::tr_read((const CA_LDS void*)src);
-        const vec4 hi = Tr::tr_read((const CA_LDS void*)(src + 4 * VS));
-        const vec8 a = cat4<vec8, vec4>(lo, hi);
-        o[ob] = Tr::mfma32(a, pb[kk], o[ob]);
-      }
-    }
-  };
-  if (n_tiles > 0) {
-    gload(0);
-    step(0, std::true_type{});
-  }
-  for (int t = 1; t < n_tiles; ++t) step(t, std::false_type{});
-
-  const float l_tot = pair32_sum(l_run);
-  const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
-  if (Lse && hl == 0 && myq < S) Lse[(size_t)(b * Hq + h) * S + myq] = row_lse(m_run, l_tot);
-  if (myq < S) {
-#pragma unroll
-    for (int ob = 0; ob < NOB; ++ob) {
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d = 32 * ob + 8 * a + 4 * hl;
-        const vec2 lo = Tr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
-        const vec2 hi = Tr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
-        vec4 w;
-        w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
-        *(vec4*)(Op + (size_t)myq * D + d) = w;
-      }
-    }
-  }
-}
-
-template <typename Tr, int D, int NW, bool CAUSAL>
-// (at least 3 workgroups per CU: three waves per SIMD, <= 168 registers)
-__global__ __launch_bounds__(NW * 64, 3) void prefill_fwd_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, RopeQ rq) {
-  const QTileWork wk =
-      prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
-  const int n_pass = wk.qt1 < 0 ? 1 : 2;
-#pragma clang loop unroll(disable)
-  for (int pass = 0; pass < n_pass; ++pass) {
-    // the second tile restages the LDS buffers: every wave must be done reading them
-    if (pass) __syncthreads();
-    prefill_fwd_qtile<Tr, D, NW, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2,
-                                         pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, rq);
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Head dim 128 kernel.
+// Head dim 64 and 128 kernel.
 //
 // One workgroup = BM query rows of one (b, h) (BM = 256 or 384), split over
 // its waves: NH = 1 gives BM/32 waves of 32 rows (two or three per SIMD),
@@ -338,22 +91,35 @@ __global__ __launch_bounds__(NW * 64, 3) void prefill_fwd_kernel(
 //
 // K/V tiles of 64 keys travel HBM -> LDS with buffer loads into a ring of
 // kStages tiles (the loaders share every K and V tile; one barrier per
-// tile). Tile layout: 64 rows x 256 bytes, unpadded; the 16-byte chunk c of
-// row r is stored at position c ^ swz(r), swz(r) = 4*(r%4) + (r/4)%4, which
-// makes both read patterns bank-conflict free:
+// tile). Tile layout: 64 rows x 2D bytes, unpadded; the 16-byte chunk c of
+// row r is stored at position c ^ swz(r), which makes both read patterns
+// bank-conflict free:
 //   K, ds_read_b128: a 16-lane group reads one chunk of 16 consecutive rows
-//     -> 16 distinct positions;
+//     -> 16 distinct bank positions;
 //   V, ds_read_b64_tr_b16: a 32-lane group reads chunks 4ob..4ob+3 of 4
-//     consecutive rows 4u..4u+3 -> position quad ob ^ (r%4) differs per row.
+//     consecutive rows 4u..4u+3 -> 16 distinct bank positions.
+// D = 128 (256-byte rows): swz(r) = 4*(r%4) + (r/4)%4, the position quad
+// ob ^ (r%4) differs per row. D = 64 (128-byte rows, two per 256 bytes of
+// banks): swz(r) = 4*((r/2)%2) + (r/4)%4 gives the 8 rows of one parity
+// among 16 consecutive rows 8 distinct chunks, and rows r, r+2 opposite
+// 4-chunk halves. D = 64 builds only the default schedule (NH = 1, no
+// software pipeline).
 // ---------------------------------------------------------------------------
-namespace pf128 {
-constexpr int kD = 128;
-constexpr int kBN = 64;                        // keys per tile
-constexpr int kRowB = kD * 2;                  // bytes per K/V row
-constexpr int kTileB = kBN * kRowB;            // bytes per K (or V) tile
-constexpr int kStageB = 2 * kTileB;            // K tile then V tile
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-}  // namespace pf128
+template <int D>
+struct PfGeom {
+  static_assert(D == 64 || D == 128, "head dim");
+  static constexpr int kBN = 64;                     // keys per tile
+  static constexpr int kRowB = D * 2;                // bytes per K/V row
+  static constexpr int kLpr = kRowB / 16;            // 16-byte chunks per row
+  static constexpr int kRpk = 1024 / kRowB;          // rows per 1-KB load
+  static constexpr int kTileB = kBN * kRowB;         // bytes per K (or V) tile
+  static constexpr int kStageB = 2 * kTileB;         // K tile then V tile
+  static constexpr int kNKS = D / 16;                // QK k-steps
+  static constexpr int kNOB = D / 32;                // O^T row blocks
+  __device__ static __forceinline__ int swz(int r) {
+    return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  }
+};
 
 // acc *= alpha on an accumulator kept in AGPRs, element by element through one
 // VGPR, so the accumulator never needs a VGPR copy (a plain C++ multiply
@@ -411,16 +177,18 @@ constexpr int pf_wg_per_cu(int bm, int nh) {
 // One query tile (kBM rows of head bh) of the workgroup: the whole key walk
 // and the output store. On return every wave has waited for its own HBM ->
 // LDS loads, but other waves may still read the ring.
-template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
-__device__ CA_INLINE void prefill_d128_qtile(
+template <typename Tr, int D, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
+__device__ CA_INLINE void prefill_dma_qtile(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int bh, int qt, int q_shift, RopeQ rq) {
-  using namespace pf128;
+  using Gm = PfGeom<D>;
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
-  constexpr int D = kD;
+  constexpr int kBN = Gm::kBN, kRowB = Gm::kRowB, kTileB = Gm::kTileB, kStageB = Gm::kStageB;
+  constexpr int kNKS = Gm::kNKS, kNOB = Gm::kNOB;
+  static_assert(D == 128 || (NH == 1 && !PIPE && !CA_PF_AG), "D = 64: default schedule only");
   constexpr int kBM = BM;                        // query rows per workgroup
   constexpr int kStages = STAGES;                // K/V tiles in the LDS ring
   constexpr int kRW = 32 * NH;                   // query rows per wave
@@ -452,11 +220,11 @@ __device__ CA_INLINE void prefill_d128_qtile(
   for (int nb = 0; nb < NH; ++nb) myq[nb] = qw0 + 32 * nb + l32;
 
   // Q as the B operand of S^T = K Q^T, one set per 32-query half.
-  vec8 qv[NH][8];
+  vec8 qv[NH][kNKS];
 #pragma unroll
   for (int nb = 0; nb < NH; ++nb) {
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < kNKS; ++ks) {
       if (myq[nb] >= 0 && myq[nb] < S) {
         qv[nb][ks] = *(const vec8*)(Qp + (size_t)myq[nb] * D + 16 * ks + 8 * hl);
       } else {
@@ -467,7 +235,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
       CA_DEVICE_ASM("" : "+a"(qv[nb][ks]));  // Q lives in AGPRs (an MFMA operand may)
 #endif
     }
-    if (rq.cos && myq[nb] >= 0 && myq[nb] < S) rope_q<Tr, kD>(qv[nb], rq, myq[nb], hl);
+    if (rq.cos && myq[nb] >= 0 && myq[nb] < S) rope_q<Tr, D>(qv[nb], rq, myq[nb], hl);
   }
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
@@ -479,15 +247,15 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // HBM -> LDS with buffer loads over the keys this workgroup needs
   // ([0, kv_end) of the (b, kv head) slice; rows past it read as zero, so
   // partial and trailing tiles need no clamp). Load i of this wave covers
-  // tile rows 4*(kDmaPerWave*wave + i) + lane/16; the lane fetches the chunk
-  // that belongs at position lane % 16. Tile tt reads through resources that
-  // start at its first row.
+  // tile rows kRpk*(kDmaPerWave*wave + i) + lane/kLpr; the lane fetches the
+  // chunk that belongs at position lane % kLpr. Tile tt reads through
+  // resources that start at its first row.
   const uint32_t kv_bytes = (uint32_t)kv_end * kRowB;
   uint32_t dma_off[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
-    const int row = 4 * (kDmaPerWave * wave + i) + (lane >> 4);
-    dma_off[i] = row * kRowB + 16 * ((lane & 15) ^ swz(row));
+    const int row = Gm::kRpk * (kDmaPerWave * wave + i) + lane / Gm::kLpr;
+    dma_off[i] = row * kRowB + 16 * ((lane % Gm::kLpr) ^ Gm::swz(row));
   }
   const bool loader = kLoaders == kNW || wave < kLoaders;
   auto issue = [&](int tt) CA_INLINE {
@@ -506,26 +274,28 @@ __device__ CA_INLINE void prefill_d128_qtile(
   // LDS read addresses (bytes from the stage base).
   // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl.
   const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
-  const int fk = swz(krow);
+  const int fk = Gm::swz(krow);
   const uint32_t kofs = krow * kRowB + 32 * (fk >> 1) + 16 * (hl ^ (fk & 1));  // ^ 32*ks
   // V^T: tr16 source lane -> row tr_row (+4 for the second read), logical
   // chunk 4*ob + c0, byte 8*(s16 & 1) of it.
   const int g16 = lane >> 4, s16 = lane & 15;
   const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
   const int c0 = 2 * (g16 & 1) + ((s16 & 3) >> 1);
-  const int fv = swz(tr_row);  // swz(tr_row + 4) == fv + 1
+  // D = 128: swz(tr_row + 4) == swz(tr_row) + 1 (tr_row % 8 < 4)
+  const int fv = Gm::swz(tr_row);
+  const int fv2 = D == 128 ? fv + 1 : Gm::swz(tr_row + 4);
   const uint32_t vofs1 = kTileB + tr_row * kRowB + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
   const uint32_t vofs2 =
-      kTileB + (tr_row + 4) * kRowB + 64 * (fv >> 2) + 16 * (c0 ^ ((fv + 1) & 3)) + 8 * (s16 & 1);
+      kTileB + (tr_row + 4) * kRowB + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
   const uint32_t lds0 = lds_off(lds);
   auto stage = [&](int tt) CA_INLINE { return lds0 + (uint32_t)((tt % kStages) * kStageB); };
 
-  f32x16 o[4][NH];     // O^T accumulators (AGPRs)
+  f32x16 o[kNOB][NH];  // O^T accumulators (AGPRs)
   f32x16 sacc[2][NH];  // S^T accumulators [mb][nb] of the tile being multiplied (AGPRs)
   float sv[NH][32];    // VGPR copy of the S^T being normalised: sv[nb][16mb + r]
   vec8 pb[NH][4];      // P^T, B operand of the O^T MFMAs
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kNOB; ++i)
 #pragma unroll
     for (int nb = 0; nb < NH; ++nb)
 #pragma unroll
@@ -594,7 +364,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
         const float m_new = __builtin_fmaxf(m_run[nb], tmax[nb]);
         const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run[nb] - m_new);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kNOB; ++i) {
 #if CA_PF_AG
           scale_acc(o[i][nb], alpha);
 #else
@@ -671,10 +441,10 @@ __device__ CA_INLINE void prefill_d128_qtile(
 #pragma unroll
       for (int ks = 0; ks < KD; ++ks) kread(ks);
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+      for (int ks = 0; ks < kNKS; ++ks) {
         const int cb = ks % (KD + 1);
-        if (ks + KD < 8) kread(ks + KD);
-        wait_lgkm_n(2 * (KD < 7 - ks ? KD : 7 - ks));  // k-step ks landed
+        if (ks + KD < kNKS) kread(ks + KD);
+        wait_lgkm_n(2 * (KD < kNKS - 1 - ks ? KD : kNKS - 1 - ks));  // k-step ks landed
         after_wait(kr[cb][0]);
         after_wait(kr[cb][1]);
 #pragma unroll
@@ -715,24 +485,26 @@ __device__ CA_INLINE void prefill_d128_qtile(
       u32x2 vr[VD + 1][2];
       // step st: O^T block ob, P^T k-step kk; with PVX consecutive MFMAs go
       // to different accumulators (a lone wave then issues them back to back)
-      auto st_ob = [](int st) CA_INLINE { return CA_PF_PVX ? (st & 3) : (st >> 2); };
-      auto st_kk = [](int st) CA_INLINE { return CA_PF_PVX ? (st >> 2) : (st & 3); };
+      constexpr int NST = 4 * kNOB;  // steps: kNOB O^T blocks x 4 P^T k-steps
+      auto st_ob = [](int st) CA_INLINE { return CA_PF_PVX ? (st % kNOB) : (st >> 2); };
+      auto st_kk = [](int st) CA_INLINE { return CA_PF_PVX ? (st / kNOB) : (st & 3); };
+      constexpr int kKK = 16 * kRowB;  // bytes per P^T k-step of V rows
       auto vread = [&](int st, int buf) CA_INLINE {
         const uint32_t x = 64 * st_ob(st);
         switch (st_kk(st)) {
           case 0: vr[buf][0] = lds_read_tr16<0>(va1 ^ x); vr[buf][1] = lds_read_tr16<0>(va2 ^ x); break;
-          case 1: vr[buf][0] = lds_read_tr16<4096>(va1 ^ x); vr[buf][1] = lds_read_tr16<4096>(va2 ^ x); break;
-          case 2: vr[buf][0] = lds_read_tr16<8192>(va1 ^ x); vr[buf][1] = lds_read_tr16<8192>(va2 ^ x); break;
-          default: vr[buf][0] = lds_read_tr16<12288>(va1 ^ x); vr[buf][1] = lds_read_tr16<12288>(va2 ^ x); break;
+          case 1: vr[buf][0] = lds_read_tr16<kKK>(va1 ^ x); vr[buf][1] = lds_read_tr16<kKK>(va2 ^ x); break;
+          case 2: vr[buf][0] = lds_read_tr16<2 * kKK>(va1 ^ x); vr[buf][1] = lds_read_tr16<2 * kKK>(va2 ^ x); break;
+          default: vr[buf][0] = lds_read_tr16<3 * kKK>(va1 ^ x); vr[buf][1] = lds_read_tr16<3 * kKK>(va2 ^ x); break;
         }
       };
 #pragma unroll
       for (int st = 0; st < VD; ++st) vread(st, st);
 #pragma unroll
-      for (int st = 0; st < 16; ++st) {
+      for (int st = 0; st < NST; ++st) {
         const int cb = st % (VD + 1);
-        if (st + VD < 16) vread(st + VD, (st + VD) % (VD + 1));
-        wait_lgkm_n(2 * (VD < 15 - st ? VD : 15 - st));  // step st landed
+        if (st + VD < NST) vread(st + VD, (st + VD) % (VD + 1));
+        wait_lgkm_n(2 * (VD < NST - 1 - st ? VD : NST - 1 - st));  // step st landed
         after_wait(vr[cb][0]);
         after_wait(vr[cb][1]);
         const int ob = st_ob(st), kk = st_kk(st);
@@ -856,7 +628,7 @@ __device__ CA_INLINE void prefill_d128_qtile(
       Lse[(size_t)(b * Hq + h) * S + myq[nb]] = row_lse(m_run[nb], l_tot);
     if (myq[nb] >= 0 && myq[nb] < S) {
 #pragma unroll
-      for (int ob = 0; ob < 4; ++ob) {
+      for (int ob = 0; ob < kNOB; ++ob) {
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
           const int d = 32 * ob + 8 * a + 4 * hl;
@@ -871,8 +643,8 @@ __device__ CA_INLINE void prefill_d128_qtile(
   }
 }
 
-template <typename Tr, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
-__global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_d128_kernel(
+template <typename Tr, int D, bool CAUSAL, bool POS, int NH, bool PIPE, int BM, int STAGES>
+__global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void prefill_dma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
     int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift, RopeQ rq) {
@@ -883,7 +655,7 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
-    prefill_d128_qtile<Tr, CAUSAL, POS, NH, PIPE, BM, STAGES>(
+    prefill_dma_qtile<Tr, D, CAUSAL, POS, NH, PIPE, BM, STAGES>(
         Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift,
         rq);
   }
@@ -898,22 +670,25 @@ __global__ __launch_bounds__(64 * pf_waves(BM, NH), pf_wg_per_cu(BM, NH)) void p
 #ifndef CA_PF_MAXSTAGES
 #define CA_PF_MAXSTAGES 4
 #endif
-template <typename Tr, bool CAUSAL, int BM>
-static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const void* v, void* o, float* lse,
-                                         int B, int Hq, int Hkv, int S, float scale,
-                                         hipStream_t stream, RopeQ rq) {
-  constexpr int NH = CA_PF_NH;
-  constexpr bool PIPE = CA_PF_PIPE;
-  // LDS ring: as many 32 KB stages as fit next to the other workgroups on the CU
+
+template <typename Tr, int D, bool CAUSAL, int BM>
+static hipError_t launch_prefill_dma_bm(const void* q, const void* k, const void* v, void* o, float* lse,
+                                        int B, int Hq, int Hkv, int S, float scale,
+                                        hipStream_t stream, RopeQ rq) {
+  using Gm = PfGeom<D>;
+  constexpr int NH = D == 128 ? CA_PF_NH : 1;
+  constexpr bool PIPE = D == 128 && CA_PF_PIPE;
+  // LDS ring: as many stages (32 KB at D = 128) as fit next to the other
+  // workgroups on the CU
   constexpr int kLdsPerWg = 160 * 1024 / pf_wg_per_cu(BM, NH);
-  constexpr int STAGES = kLdsPerWg / pf128::kStageB > CA_PF_MAXSTAGES ? CA_PF_MAXSTAGES
-                                                                      : kLdsPerWg / pf128::kStageB;
+  constexpr int STAGES = kLdsPerWg / Gm::kStageB > CA_PF_MAXSTAGES ? CA_PF_MAXSTAGES
+                                                                   : kLdsPerWg / Gm::kStageB;
   static_assert(STAGES >= (PIPE ? 3 : 2), "LDS ring too short for the schedule");
   const int n_qt = (S + BM - 1) / BM;
   // the padding rows of a ragged S go before row 0, in whole key tiles (so a
   // wave's causal diagonal still lies in one key tile): the partial tile is
   // the first one, whose causal key walk is the shortest
-  const int q_shift = (n_qt * BM - S) / pf128::kBN * pf128::kBN;
+  const int q_shift = (n_qt * BM - S) / Gm::kBN * Gm::kBN;
   int paired = 0;
   const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, pf_wg_per_cu(BM, NH), &paired);
   if (grid == 0) return hipSuccess;
@@ -921,12 +696,12 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
   const float sl2 = scale * kLog2e;
   const dim3 block(64 * pf_waves(BM, NH));
   if (sl2 >= 0.f) {
-    hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, true, NH, PIPE, BM, STAGES>),
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, true, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
                        n_qt, B * Hq, (int)grid, paired, q_shift, rq);
   } else {
-    hipLaunchKernelGGL((prefill_d128_kernel<Tr, CAUSAL, false, NH, PIPE, BM, STAGES>),
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, false, NH, PIPE, BM, STAGES>),
                        dim3((unsigned)grid), block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, sl2,
                        n_qt, B * Hq, (int)grid, paired, q_shift, rq);
@@ -940,69 +715,38 @@ static hipError_t launch_prefill_d128_bm(const void* q, const void* k, const voi
 // gains more; the 384-row choice (when such tiles cover S with at most ~5 %
 // padding and the grid gives every CU two workgroups) remains for builds
 // without it.
-template <typename Tr, bool CAUSAL>
-static hipError_t launch_prefill_d128(const void* q, const void* k, const void* v, void* o, float* lse,
-                                      int B, int Hq, int Hkv, int S, float scale,
-                                      hipStream_t stream, RopeQ rq) {
+template <typename Tr, int D, bool CAUSAL>
+static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v, void* o, float* lse,
+                                     int B, int Hq, int Hkv, int S, float scale,
+                                     hipStream_t stream, RopeQ rq) {
 #ifdef CA_PF_BM
-  return launch_prefill_d128_bm<Tr, CAUSAL, CA_PF_BM>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
+  return launch_prefill_dma_bm<Tr, D, CAUSAL, CA_PF_BM>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
 #else
   const long long n384 = (S + 383) / 384;
   const bool fits = n384 * 384 * 20 <= (long long)S * 21;
   const bool tall = !CA_PF_STALE && fits && (long long)B * Hq * n384 >= 2LL * device_cus();
-  return tall ? launch_prefill_d128_bm<Tr, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)
-              : launch_prefill_d128_bm<Tr, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
+  return tall ? launch_prefill_dma_bm<Tr, D, CAUSAL, 384>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)
+              : launch_prefill_dma_bm<Tr, D, CAUSAL, 256>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq);
 #endif
-}
-
-template <typename Tr, int D, bool CAUSAL>
-static hipError_t launch_prefill_t(const void* q, const void* k, const void* v, void* o, float* lse,
-                                   int B, int Hq, int Hkv, int S, float scale,
-                                   hipStream_t stream, RopeQ rq) {
-#ifndef CA_PF_NW
-#define CA_PF_NW 4
-#endif
-  constexpr int NW = CA_PF_NW;  // waves per workgroup (32 query rows each)
-  constexpr int BM = 32 * NW;
-  const int n_qt = (S + BM - 1) / BM;
-  int paired = 0;
-  const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, 2, &paired);
-  if (grid == 0) return hipSuccess;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((prefill_fwd_kernel<Tr, D, NW, CAUSAL>), dim3((unsigned)grid),
-                     dim3(NW * 64), 0, stream, (const uint16_t*)q, (const uint16_t*)k,
-                     (const uint16_t*)v, (uint16_t*)o, lse, S, Hq, Hkv, scale * kLog2e, n_qt, B * Hq,
-                     (int)grid, paired, rq);
-  return hipGetLastError();
 }
 
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,
                           hipStream_t stream, RopeQ rq) {
-#define CA_PREFILL_CASE(TR, DD)                                                          \
-  if (D == DD) {                                                                         \
-    return causal ? launch_prefill_t<TR, DD, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq) \
-                  : launch_prefill_t<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
+#define CA_PREFILL_DMA(TR, DD)                                                                    \
+  if (D == DD) {                                                                                  \
+    return causal ? launch_prefill_dma<TR, DD, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)  \
+                  : launch_prefill_dma<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
   }
-#ifndef CA_PF_OLD128
-#define CA_PREFILL_128(TR)                                                                     \
-  if (D == 128) {                                                                              \
-    return causal ? launch_prefill_d128<TR, true>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq)  \
-                  : launch_prefill_d128<TR, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
-  }
-#else
-#define CA_PREFILL_128(TR) CA_PREFILL_CASE(TR, 128)
-#endif
   if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, lse, B, Hq, Hkv, S, D, scale, causal, stream);
   if (dtype == kDtypeBF16) {
-    CA_PREFILL_CASE(BF16, 64)
-    CA_PREFILL_128(BF16)
+    CA_PREFILL_DMA(BF16, 64)
+    CA_PREFILL_DMA(BF16, 128)
   } else if (dtype == kDtypeF16) {
-    CA_PREFILL_CASE(F16, 64)
-    CA_PREFILL_128(F16)
+    CA_PREFILL_DMA(F16, 64)
+    CA_PREFILL_DMA(F16, 128)
   }
-#undef CA_PREFILL_128
-#undef CA_PREFILL_CASE
+#undef CA_PREFILL_DMA
   return hipErrorInvalidValue;
 }
 

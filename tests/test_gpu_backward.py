@@ -207,3 +207,24 @@ def test_backward_large_paired_tiles(dev, b, h, s, is_causal, d):
                                         is_causal=is_causal, dtype=np.float64)
         for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
             _check_grad(a[bi:bi + 1, hi:hi + 1], r, f"{name} b{bi} h{hi}")
+
+
+def test_backward_reference_benchmark_shape(dev):
+    """The reference benchmark's backward shape (benchmark_pytorch.py:659-661:
+    fp16, B = 2, H = 32, S = 4096, head dim 64, non-causal): every head is
+    computed, two sampled heads are checked against the float64 oracle on the
+    kernel forward's own out and LSE."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    b, h, s, d = 2, 32, 4096, 64
+    q, k, v = qkv(b, h, s, d, torch.float16, dev, gen=g)
+    dout = torch.randn(b, h, s, d, device=dev, generator=g).to(torch.float16)
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=False)
+    dq, dk, dv = cuda_llm.flash_attention_backward(dout, q, k, v, out, lse, is_causal=False)
+    torch.cuda.synchronize()
+    for bi, hi in [(0, 5), (1, 31)]:
+        sel = lambda t: to_np(t[bi:bi + 1, hi:hi + 1]).astype(np.float64)
+        ref = oracle.attention_backward(sel(dout), sel(q), sel(k), sel(v), sel(out),
+                                        to_np(lse[bi:bi + 1, hi:hi + 1]).astype(np.float64),
+                                        is_causal=False, dtype=np.float64)
+        for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+            _check_grad(a[bi:bi + 1, hi:hi + 1], r, f"{name} b{bi} h{hi}")
