@@ -460,6 +460,15 @@ void decode_split_kernel(
 #ifndef CA_RING_16
 #define CA_RING_16 3
 #endif
+// Pages per split of the direct-load decode (64 or 128: one or two page-id
+// registers per lane): 256 KB of K and V per split for both cache kinds
+// (128 fp8 pages, 64 16-bit pages). A split's start (context length,
+// block-table row, scales, filling the ring) is paid once per split: 128
+// fp8 pages measured +3.5 % on C4 over 64, while 128 16-bit pages leave C3
+// too few waves (-3 %).
+#ifndef CA_DMA_PAGES_FP8
+#define CA_DMA_PAGES_FP8 128
+#endif
 // Pages per step and ring depth of the direct-load decode. One page per step
 // keeps a ring slot small (K + V of one page), so more waves fit a CU's LDS
 // and more bytes are in flight per CU; the PV product then runs on 16x16x16
@@ -468,6 +477,9 @@ template <int KIND>
 struct DmaCfg {
   static constexpr int kPagesPerStep = CA_DMA_PPS;
   static constexpr int kRing = KIND == kKindPagedFp8 ? CA_RING_FP8 : CA_RING_16;
+  static constexpr int kPages = KIND == kKindPagedFp8 ? CA_DMA_PAGES_FP8 : kPagesPerWave;
+  // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
+  static_assert(kPages >= kPagesPerWave, "pages per split");
 };
 
 template <typename Tr, int D, int KIND>
@@ -491,7 +503,9 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   constexpr int DPS = 2 * PPS * NDMA;         // loads per step
   constexpr int KRD = FP8 ? NKS : 2 * NKS;    // LDS reads for one page's K^T operands
   static_assert(PPS == 1 || PPS == 2, "pages per step");
-  static_assert(kPagesPerWave % PPS == 0, "whole steps per split");
+  constexpr int kDmaPages = DmaCfg<KIND>::kPages;
+  constexpr int PB = kDmaPages / 64;          // page-id registers per lane
+  static_assert(kDmaPages % 64 == 0 && PB <= 2, "pages per split");
   static_assert((RING - 1) * DPS <= 63, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) unsigned char ring[RING * STAGE];
 
@@ -523,7 +537,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   const int Gc = min(16, Gq - hc * 16);
   const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = max(1, (n_pages + kPagesPerWave - 1) / kPagesPerWave);
+  const int n_splits = max(1, (n_pages + kDmaPages - 1) / kDmaPages);
 #if CA_DEC_SPLIT_OUTER == 2
   const int split = n_splits - 1 - from_end;
   if (split < 0) return;
@@ -532,8 +546,8 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 #endif
 
   const int l16 = lane & 15, grp = lane >> 4;
-  const int p_begin = split * kPagesPerWave;
-  const int p_end = min(p_begin + kPagesPerWave, n_pages);
+  const int p_begin = split * kDmaPages;
+  const int p_end = min(p_begin + kDmaPages, n_pages);
   const int n_steps = (p_end - p_begin + PPS - 1) / PPS;
 
   vec8 qv[NKS];
@@ -549,23 +563,36 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       }
     }
   }
-  int pid_lane = 0;
-  float ksc_lane = 1.f, vsc_lane = 1.f;
-  if (p_begin + lane < p_end) {
-    pid_lane = block_tables[(size_t)n * max_blocks + p_begin + lane];
-    pid_lane = min(max(pid_lane, 0), num_blocks - 1);
-  }
-  if (FP8) {
-    if (per_block) {
-      if (p_begin + lane < p_end) {
-        ksc_lane = k_scale[(size_t)pid_lane * Hkv + hk];
-        vsc_lane = v_scale[(size_t)pid_lane * Hkv + hk];
+  // page ids and per-page scales: lane j of register b holds page
+  // p_begin + 64 b + j; read back for page index i (uniform) with lane_val
+  int pid_lane[PB];
+  float ksc_lane[PB], vsc_lane[PB];
+#pragma unroll
+  for (int pb = 0; pb < PB; ++pb) {
+    const int page = p_begin + 64 * pb + lane;
+    pid_lane[pb] = 0;
+    ksc_lane[pb] = vsc_lane[pb] = 1.f;
+    if (page < p_end) {
+      pid_lane[pb] = block_tables[(size_t)n * max_blocks + page];
+      pid_lane[pb] = min(max(pid_lane[pb], 0), num_blocks - 1);
+    }
+    if (FP8) {
+      if (per_block) {
+        if (page < p_end) {
+          ksc_lane[pb] = k_scale[(size_t)pid_lane[pb] * Hkv + hk];
+          vsc_lane[pb] = v_scale[(size_t)pid_lane[pb] * Hkv + hk];
+        }
+      } else {
+        ksc_lane[pb] = k_scale[hk];
+        vsc_lane[pb] = v_scale[hk];
       }
-    } else {
-      ksc_lane = k_scale[hk];
-      vsc_lane = v_scale[hk];
     }
   }
+  auto lane_val = [&](const auto (&r)[PB], int i) CA_INLINE {
+    const auto v = (PB > 1 && i >= 64) ? r[PB - 1] : r[0];
+    return __builtin_bit_cast(std::remove_const_t<std::remove_reference_t<decltype(r[0])>>,
+                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i & 63));
+  };
 
   // source byte offset of this lane's 16 bytes for load i of a K chunk
   auto k_src = [&](int i) -> int {
@@ -581,7 +608,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       const int page = p_begin + PPS * step + pp;
       const bool valid = step < n_steps && page < p_end;
       const int idx = valid ? PPS * step + pp : 0;
-      const int pid = __builtin_amdgcn_readlane(pid_lane, idx);
+      const int pid = lane_val(pid_lane, idx);
       const size_t chunk = ((size_t)pid * Hkv + hk) * (size_t)CHUNK;
       const unsigned char* kp = (const unsigned char*)Kc + chunk;
       const unsigned char* vp = (const unsigned char*)Vc + chunk;
@@ -690,8 +717,8 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       c[pp] = scale_log2;
       vs[pp] = 1.f;
       if (FP8) {
-        c[pp] *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), PPS * step + pp));
-        vs[pp] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), PPS * step + pp));
+        c[pp] *= lane_val(ksc_lane, PPS * step + pp);
+        vs[pp] = lane_val(vsc_lane, PPS * step + pp);
       }
     }
     float x[4 * PPS];
@@ -809,13 +836,14 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 template <typename Tr, int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
-    const float* __restrict__ ws_lse, void* __restrict__ O, int Hq, int max_splits) {
+    const float* __restrict__ ws_lse, void* __restrict__ O, int Hq, int max_splits,
+    int pages_per_split) {
   constexpr int PER = D / 64;
   const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
   const int lane = threadIdx.x;
   const int Lctx = context_lens ? min(max(0, context_lens[n]), max_tokens) : max_tokens;
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = (n_pages + kPagesPerWave - 1) / kPagesPerWave;
+  const int n_splits = (n_pages + pages_per_split - 1) / pages_per_split;
   if (n_splits <= 1) return;
   const size_t slot0 = ((size_t)n * Hq + hq) * max_splits;
   float M = kNegInf;
@@ -862,7 +890,12 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
                                   float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
   const int max_tokens = (KIND == kKindContig16) ? S_contig : max_blocks * kDecodePage;
   const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  const int max_splits = max(1, (pages + kPagesPerWave - 1) / kPagesPerWave);
+  // the direct-load kernel splits at DmaCfg<KIND>::kPages pages, the others
+  // at kPagesPerWave; the workspace (sized for kPagesPerWave-page splits)
+  // covers both
+  const bool dma = KIND != kKindContig16 && kDecodeDma;
+  const int pps = dma ? DmaCfg<KIND>::kPages : kPagesPerWave;
+  const int max_splits = max(1, (pages + pps - 1) / pps);
   const int Gq = Hq / Hkv;
   const int n_hc = (Gq + 15) / 16;
   const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
@@ -871,7 +904,7 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
   float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
   const long long total_waves = (long long)N * Hkv * n_hc * max_splits;
   if (total_waves == 0) return hipSuccess;
-  if (KIND != kKindContig16 && kDecodeDma) {
+  if (dma) {
     if (total_waves > 0x7fffffffLL) return hipErrorInvalidValue;
     hipLaunchKernelGGL((decode_dma_kernel<Tr, D, KIND>), dim3((unsigned)total_waves), dim3(64), 0,
                        stream, (const uint16_t*)q, kc, vc, k_scale, v_scale, per_block, bt, lens,
@@ -890,7 +923,7 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
   if (e != hipSuccess || max_splits <= 1) return e;
   hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
                      KIND == kKindContig16 ? nullptr : lens, max_tokens, ws_o, ws_lse, out, Hq,
-                     max_splits);
+                     max_splits, pps);
   return hipGetLastError();
 }
 
@@ -1087,7 +1120,8 @@ static hipError_t launch_decode_f32_t(const void* q, const void* kc, const void*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_splits <= 1) return e;
   hipLaunchKernelGGL((decode_merge_kernel<F32, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
-                     PAGED ? lens : nullptr, max_tokens, ws_o, ws_lse, out, Hq, max_splits);
+                     PAGED ? lens : nullptr, max_tokens, ws_o, ws_lse, out, Hq, max_splits,
+                     kPagesPerWave);
   return hipGetLastError();
 }
 

@@ -49,7 +49,7 @@ def test_paged_attention(dev, dtype, head_dim, context_lens):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("hq,hkv", [(32, 8), (8, 1), (16, 16), (40, 2)])
 def test_paged_gqa_and_splits(dev, dtype, hq, hkv):
-    lens = [0, 1, 15, 16, 17, 1023, 1024, 1025, 3000, 5000]
+    lens = [0, 1, 15, 16, 17, 1023, 1024, 1025, 2047, 2048, 2049, 3000, 4097, 5000]
     case = build_paged(lens, hq, hkv, 128, dtype, dev, pool=2000)
     out = _run_paged(case)
     torch.cuda.synchronize()
