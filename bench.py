@@ -43,11 +43,32 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_steps(fn, steps, warmup):
+# Minimum GPU-busy time of the warm-up: the GPU needs ~0.1-0.2 s of load to
+# reach its sustained clock, so a few warm-up launches (the driver's 5) would
+# time the first steps at a ramping clock. The warm-up runs at least `warmup`
+# launches and keeps launching until this much time has passed.
+WARM_SECONDS = 0.25
+WARM_LOG = {}  # workload label -> {"launches": n, "seconds": s} of its last warm-up
+
+
+def time_steps(fn, steps, warmup, label=None):
+    """ms per step of `fn` over `steps` launches between HIP events on the
+    current stream, after a warm-up of at least `warmup` launches and at least
+    WARM_SECONDS of wall time (recorded in WARM_LOG[label])."""
     import torch
+    t0 = time.perf_counter()
+    n = 0
     for _ in range(warmup):
         fn()
+        n += 1
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < WARM_SECONDS:
+        for _ in range(4):
+            fn()
+            n += 1
+        torch.cuda.synchronize()
+    if label:
+        WARM_LOG[label] = {"launches": n, "seconds": round(time.perf_counter() - t0, 3)}
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -117,6 +138,24 @@ def blas_threads():
         return os.cpu_count()
 
 
+def host_info():
+    """CPU model and counts of this host, reported beside every CPU figure."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count()
+    return {"cpu_model": model, "host_cpus": os.cpu_count(), "cpus_available": avail}
+
+
 def _gen(seed=0):
     import torch
     g = torch.Generator(device="cuda")
@@ -133,7 +172,7 @@ def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
     g = _gen()
     q, k, v = (torch.randn(B, H, S, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
     fn = lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal)
-    ms = time_steps(fn, steps, warmup)
+    ms = time_steps(fn, steps, warmup, "prefill" if causal else "prefill_nc")
     cold = time_cold(fn)
     flops = (2.0 if causal else 4.0) * B * H * S * S * D
     tf = flops / (ms * 1e-3) / 1e12
@@ -156,7 +195,8 @@ def w_backward(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
                      for _ in range(4))
     out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=causal)
     ms = time_steps(lambda: cuda_llm.flash_attention_backward(dout, q, k, v, out, lse,
-                                                              is_causal=causal), steps, warmup)
+                                                              is_causal=causal), steps, warmup,
+                    "backward")
     flops = 2.5 * (2.0 if causal else 4.0) * B * H * S * S * D
     tf = flops / (ms * 1e-3) / 1e12
     return dict(ms=ms, value=tf, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_TFLOPS, work=flops,
@@ -186,7 +226,7 @@ def cpu_prefill(r, seconds):
     flops = (2.0 if r["causal"] else 4.0) * S * S * D * done
     return dict(value=flops / el / 1e12, unit="TFLOP/s", cores=blas_threads(), kind="port",
                 sample=f"{done} of {B * H} (b,h) heads of the same inputs, numpy fp32 oracle "
-                       f"(oracle/attention.py), {el:.1f} s")
+                       f"(oracle/attention.py), {el:.1f} s", **host_info())
 
 
 def make_paged(N, Hq, Hkv, D, lens, fp8, pool=None, seed=0):
@@ -248,7 +288,7 @@ def w_decode(steps, warmup, fp8):
                                                           c["tables"], c["lens"])
     else:
         fn = lambda: cuda_llm.paged_attention_forward(c["query"], c["kc"], c["vc"], c["tables"], c["lens"])
-    ms = time_steps(fn, steps, warmup)
+    ms = time_steps(fn, steps, warmup, "decode_fp8" if fp8 else "decode_bf16")
     gbs = c["alg_bytes"] / (ms * 1e-3) / 1e9
     name = "C4 FP8 paged GQA decode" if fp8 else "C3 bf16 paged GQA decode"
     return dict(ms=ms, value=gbs, unit="GB/s", bound="hbm", peak=PEAK_HBM_GBS, work=c["alg_bytes"],
@@ -287,7 +327,7 @@ def cpu_decode(r, seconds):
     bytes_per_token = c["alg_bytes"] / sum(c["lens_host"])
     return dict(value=done_tokens * bytes_per_token / el / 1e9, unit="GB/s", cores=blas_threads(),
                 kind="port", sample=f"{done} of {len(c['lens_host'])} sequences of the same inputs, "
-                                    f"numpy oracle (oracle/paged.py), {el:.1f} s")
+                                    f"numpy oracle (oracle/paged.py), {el:.1f} s", **host_info())
 
 
 def w_mxfp8(steps, warmup, B=1, H=16, S=8192, D=128):
@@ -306,7 +346,7 @@ def w_mxfp8(steps, warmup, B=1, H=16, S=8192, D=128):
         x[n + "s"] = (e + 127).to(torch.uint8)
     fn = lambda: cuda_llm.fused_microscaled_attention(x["q"], x["qs"], x["k"], x["ks"], x["v"], x["vs"],
                                                       is_causal=True)
-    ms = time_steps(fn, steps, warmup)
+    ms = time_steps(fn, steps, warmup, "mxfp8")
     flops = 2.0 * B * H * S * S * D
     return dict(ms=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s", bound="mfma",
                 peak=PEAK_FP8_TFLOPS, work=flops,
@@ -314,11 +354,46 @@ def w_mxfp8(steps, warmup, B=1, H=16, S=8192, D=128):
                         "head_dim": D, "note": "QK on fp8 scaled MFMA, PV on bf16 MFMA"})
 
 
+def w_c1(steps, warmup, B=2, H=8, S=1024, D=64):
+    """C1 (the workload of the reference's ref_attention,
+    tests/_utils.py:48-53): fp32 q, k, v ~ N(0,1) [2, 8, 1024, 64], causal,
+    scale 1/8. The oracle (numpy fp32) runs the whole config on this host's
+    cores, and the fp32 HIP prefill runs it on the GPU; both are checked
+    against each other (max-abs 1e-4, the reference's float32 tolerance)."""
+    import numpy as np
+    import torch
+    import cuda_llm
+    import oracle
+    g = _gen()
+    q, k, v = (torch.randn(B, H, S, D, device="cuda", generator=g) for _ in range(3))
+    fn = lambda: cuda_llm.flash_attention(q, k, v, is_causal=True)
+    ms = time_steps(fn, steps, warmup, "c1")
+    flops = 2.0 * B * H * S * S * D
+    qn, kn, vn = (t.cpu().numpy() for t in (q, k, v))
+    reps, el = 0, 0.0
+    while el < 2.0 or reps < 3:
+        t1 = time.perf_counter()
+        ref = oracle.attention(qn, kn, vn, is_causal=True)
+        el += time.perf_counter() - t1
+        reps += 1
+    err = float(np.abs(fn().cpu().numpy() - ref).max())
+    return dict(ms=ms, value=flops / (ms * 1e-3) / 1e12, unit="TFLOP/s", bound="mfma",
+                peak=157.3, work=flops, max_abs_err_vs_oracle=err,
+                cpu={"value": flops * reps / el / 1e12, "unit": "TFLOP/s", "cores": blas_threads(),
+                     "kind": "port", "sample": f"the whole config, {reps} runs of the numpy fp32 "
+                                               f"oracle (oracle/attention.py), {el:.1f} s",
+                     **host_info()},
+                config={"workload": "C1 fp32 causal prefill (flash_attention)", "batch": B,
+                        "heads": H, "seq_len": S, "head_dim": D, "causal": True,
+                        "note": "GPU: fp32 prefill on v_mfma_f32_32x32x2_f32, priced against the "
+                                "fp32 MFMA peak 157.3 TFLOP/s"})
+
+
 def w_copy(steps, warmup, nbytes=2 << 30):
     import torch
     x = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_()
     y = torch.empty_like(x)
-    ms = time_steps(lambda: y.copy_(x), steps, warmup)
+    ms = time_steps(lambda: y.copy_(x), steps, warmup, "copy")
     return dict(ms=ms, value=2 * nbytes / (ms * 1e-3) / 1e9, unit="GB/s", bound="hbm",
                 peak=PEAK_HBM_GBS, work=2 * nbytes,
                 config={"workload": "device copy (HBM counter calibration)", "bytes": nbytes})
@@ -327,7 +402,7 @@ def w_copy(steps, warmup, nbytes=2 << 30):
 def w_read(steps, warmup, nbytes=4 << 30):
     """Streaming-read ceiling: ca_stream_read over a resident buffer (the
     measured second denominator of the HBM-bound decode lines)."""
-    ms = time_steps(_stream_reader(nbytes), steps, warmup)
+    ms = time_steps(_stream_reader(nbytes), steps, warmup, "read")
     return dict(ms=ms, value=nbytes / (ms * 1e-3) / 1e9, unit="GB/s", bound="hbm",
                 peak=PEAK_HBM_GBS, work=nbytes,
                 config={"workload": "streaming read (measured HBM read ceiling)", "bytes": nbytes})
@@ -475,6 +550,7 @@ WORKLOADS = {
     "decode_bf16": lambda s, w: w_decode(s, w, fp8=False),
     "mxfp8": w_mxfp8,
     "backward": w_backward,
+    "c1": w_c1,
     "copy": w_copy,
     "read": w_read,
     "refgrid": w_refgrid,
@@ -495,6 +571,12 @@ def summary(name, r, read_gbs=None):
                         "traffic": _traffic(TRAFFIC_KEY.get(name, name))}}
     if "cold" in r:
         out["cold"] = r["cold"]
+    if name in WARM_LOG:
+        out["warmup_run"] = WARM_LOG[name]
+    if "cpu" in r:
+        out["cpu_baseline"] = r["cpu"]
+    if "max_abs_err_vs_oracle" in r:
+        out["max_abs_err_vs_oracle"] = r["max_abs_err_vs_oracle"]
     if read_gbs:
         out["roofline"]["measured_read_peak"] = round(read_gbs, 2)
         out["roofline"]["frac_of_measured"] = round(r["value"] / read_gbs, 4)
@@ -544,19 +626,23 @@ def main():
                    "mxfp8": "MXFP8 causal attention TFLOP/s (C5)",
                    "backward": "prefill backward TFLOP/s (bf16 causal, B=4 H=32 S=4096 D=128)",
                    "copy": "device copy GB/s",
-                   "read": "streaming read GB/s"}[head],
+                   "read": "streaming read GB/s",
+                   "c1": "prefill TFLOP/s (fp32 causal, B=2 H=8 S=1024 D=64)"}[head],
         "value": s["value"], "unit": s["unit"], "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": s["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": {"prefill": "bf16", "prefill_nc": "bf16", "decode_fp8": "e4m3 KV / bf16 q,out / fp32 softmax",
                   "decode_bf16": "bf16", "mxfp8": "mxfp8 e4m3+e8m0 / bf16 out", "backward": "bf16",
-                  "copy": "bf16", "read": "u32"}[head],
+                  "copy": "bf16", "read": "u32", "c1": "f32"}[head],
         "data": "synthetic, seeded (torch generator seed 0), resident in HBM",
         "config": dict(s["config"], parallelism="none (1 GPU)"),
         "roofline": s["roofline"],
         **({"cold": s["cold"]} if "cold" in s else {}),
+        **({"warmup_run": s["warmup_run"]} if "warmup_run" in s else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count},
     }
+    if "cpu_baseline" in s:
+        line["cpu_baseline"] = s["cpu_baseline"]
     if not args.no_cpu_baseline and head in ("prefill", "prefill_nc", "decode_fp8", "decode_bf16"):
         log("cpu baseline ...")
         line["cpu_baseline"] = (cpu_prefill if head.startswith("prefill") else cpu_decode)(r, args.cpu_seconds)
@@ -574,7 +660,7 @@ def main():
         del r
         torch.cuda.empty_cache()
         extra = {}
-        for name in ("prefill_nc", "decode_bf16", "mxfp8", "backward"):
+        for name in ("prefill_nc", "decode_bf16", "mxfp8", "backward", "c1"):
             r = WORKLOADS[name](args.steps, args.warmup)
             log(f"{name}: {r['ms']:.4f} ms/step, {r['value']:.1f} {r['unit']}")
             extra[name] = summary(name, r, read_ceiling(args.steps, args.warmup)

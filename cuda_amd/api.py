@@ -62,7 +62,7 @@ def _scale(softmax_scale, head_dim):
 
 
 def _dtype_code(t, what):
-    _check(t.dtype in _DT, f"Unsupported scalar type for {what}. Supported: Float16, BFloat16.")
+    _check(t.dtype in _DT, f"Unsupported scalar type for {what}. Supported: Float, Float16, BFloat16.")
     return _DT[t.dtype]
 
 

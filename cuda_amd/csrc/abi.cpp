@@ -239,7 +239,7 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
                                  size_t workspace_bytes, void* stream) {
   const char* what = "fp8_paged_attention";
   ca_status st;
-  if ((st = check_16bit_dtype(dtype, what)) != CA_OK) return st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
   if ((st = paged_common_checks(what, query, key_cache, value_cache, block_tables, context_lens,
                                 out, num_seqs, num_q_heads, num_kv_heads, head_dim,
                                 max_blocks_per_seq, page_size, num_blocks, workspace,

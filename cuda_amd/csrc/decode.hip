@@ -36,7 +36,7 @@
 
 namespace ca {
 
-enum : int { kKindPaged16 = 0, kKindPagedFp8 = 1, kKindContig16 = 2 };
+enum : int { kKindPaged16 = 0, kKindPagedFp8 = 1 };
 
 template <typename Tr>
 struct Fp8Conv;
@@ -69,50 +69,39 @@ __device__ __forceinline__ T ld_stream(const void* p) {
   return __builtin_nontemporal_load((const T*)p);
 }
 
-template <int D, int KIND>
-struct DecodeGeom {
+// Contiguous-cache decode (flash_decode): one wave per split of kPagesPerWave
+// "pages" of 16 consecutive tokens of one (sequence, kv head, <= 16 q heads).
+// K^T operands come straight from the row-major cache (a lane's 16 bytes are
+// 8 consecutive head-dim elements of one token); V rows go through a
+// wave-private LDS copy [32][D + 16] and are read back transposed. Register
+// double-buffering: the next two pages load while the current two compute.
+template <int D>
+struct ContigGeom {
   static constexpr int NKS = D / 32;  // S^T k-steps (32 d each)
   static constexpr int NB = D / 16;   // PV output blocks (16 d each)
-  // 16-byte chunks per lane of one page: 16-bit [D][16] = D/32, fp8 = D/64;
-  // contiguous: the K^T operand itself, NKS x 16 B per page
-  static constexpr int KREG = KIND == kKindPaged16 ? D / 32 : KIND == kKindPagedFp8 ? D / 64 : NKS;
-  // contiguous V: 16 rows x D of one page as 16-byte chunks per lane
+  // V: 16 rows x D of one page as 16-byte chunks per lane
   static constexpr int VROWREG = (16 * D * 2) / (64 * 16);
-  // wave-private LDS: paged 16-bit K pages [D][16] with a 64-element gap
-  // every 8 rows (conflict-free tr16 reads), fp8 K pages [D][16] bytes,
-  // contiguous V rows [32][D + 16]
-  static constexpr int kPaged16PageElems = D * 16 + (D / 8) * 64;
-  static constexpr int kLdsBytesPerWave = KIND == kKindPaged16 ? 2 * kPaged16PageElems * 2
-                                          : KIND == kKindPagedFp8 ? 2 * D * 16
-                                                                  : 32 * (D + 16) * 2;
+  static constexpr int kLdsBytesPerWave = 32 * (D + 16) * 2;
 };
 
 // Registers of one step (two pages): K and V as loaded from HBM.
-template <int D, int KIND>
-struct StepRegs {
-  using G = DecodeGeom<D, KIND>;
-  u32x4 k[2][G::KREG];
-  u32x2 v16[2][KIND == kKindPaged16 ? G::NB : 1];
-  uint32_t v8[2][KIND == kKindPagedFp8 ? G::NB : 1];
-  u32x4 vrow[2][KIND == kKindContig16 ? G::VROWREG : 1];
+template <int D>
+struct ContigRegs {
+  using G = ContigGeom<D>;
+  u32x4 k[2][G::NKS];
+  u32x4 vrow[2][G::VROWREG];
 };
 
-template <typename Tr, int D, int KIND>
-// waves per SIMD: fp8 steps fit 3 (168 VGPRs), 16-bit steps carry twice the
-// bytes in flight and fit 2
-__global__ __launch_bounds__(kDecodeWgWaves * 64)
-__attribute__((amdgpu_waves_per_eu(KIND == kKindPagedFp8 ? 3 : 2, KIND == kKindPagedFp8 ? 3 : 2)))
+template <typename Tr, int D>
+__global__ __launch_bounds__(kDecodeWgWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void decode_split_kernel(
-    const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
-    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
-    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ Kc, const uint16_t* __restrict__ Vc,
     uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
-    int Hkv, int max_blocks, int num_blocks, int S_contig, int max_splits, int n_hc,
-    long long total_waves, float scale_log2) {
+    int Hkv, int S_contig, int max_splits, int n_hc, long long total_waves, float scale_log2) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
-  using G = DecodeGeom<D, KIND>;
+  using G = ContigGeom<D>;
   constexpr int NKS = G::NKS, NB = G::NB;
   __shared__ __attribute__((aligned(16))) unsigned char lds[kDecodeWgWaves * G::kLdsBytesPerWave];
 
@@ -135,10 +124,7 @@ void decode_split_kernel(
   const int hq0 = hk * Gq + hc * 16;
   const int Gc = min(16, Gq - hc * 16);
 
-  // a context longer than its block-table row is cut to the row (never read
-  // past block_tables[n][max_blocks - 1])
-  const int Lctx = (KIND == kKindContig16) ? S_contig
-                                           : min(max(0, context_lens[n]), max_blocks * kDecodePage);
+  const int Lctx = S_contig;
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
   const int n_splits = max(1, (n_pages + kPagesPerWave - 1) / kPagesPerWave);
   if (split >= n_splits) return;
@@ -162,77 +148,31 @@ void decode_split_kernel(
       }
     }
   }
-
-  // ---- page ids and per-page scales: lane j < kPagesPerWave holds page p_begin + j ----
-  int pid_lane = 0;
-  float ksc_lane = 1.f, vsc_lane = 1.f;
-  if (KIND != kKindContig16) {
-    if (lane < kPagesPerWave && p_begin + lane < p_end) {
-      pid_lane = block_tables[(size_t)n * max_blocks + p_begin + lane];
-      pid_lane = min(max(pid_lane, 0), num_blocks - 1);
-    }
-    if (KIND == kKindPagedFp8) {
-      if (per_block) {
-        if (lane < kPagesPerWave && p_begin + lane < p_end) {
-          ksc_lane = k_scale[(size_t)pid_lane * Hkv + hk];
-          vsc_lane = v_scale[(size_t)pid_lane * Hkv + hk];
-        }
-      } else {
-        ksc_lane = k_scale[hk];
-        vsc_lane = v_scale[hk];
-      }
-    }
-  }
   unsigned char* wlds = lds + wave * G::kLdsBytesPerWave;
+  const size_t base = ((size_t)n * Hkv + hk) * (size_t)S_contig * D;
+  const uint16_t* Kp = Kc + base;
+  const uint16_t* Vp = Vc + base;
 
   // ---- HBM -> registers for one step ----
-  const size_t chunk_elems = (size_t)D * 16;  // one (page, head) chunk
-  auto load_step = [&](StepRegs<D, KIND>& R, int step) {
+  auto load_step = [&](ContigRegs<D>& R, int step) {
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       const int page = p_begin + 2 * step + pp;
       const bool valid = page < p_end;
-      if (KIND == kKindContig16) {
-        const size_t base = ((size_t)n * Hkv + hk) * (size_t)S_contig * D;
-        const uint16_t* Kp = (const uint16_t*)Kc + base;
-        const uint16_t* Vp = (const uint16_t*)Vc + base;
-        const int tok = page * 16 + l16;
+      const int tok = page * 16 + l16;
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks)
-          R.k[pp][ks] = (valid && tok < S_contig)
-                            ? ld_stream<u32x4>(Kp + (size_t)tok * D + 32 * ks + 8 * grp)
+      for (int ks = 0; ks < NKS; ++ks)
+        R.k[pp][ks] = (valid && tok < S_contig)
+                          ? ld_stream<u32x4>(Kp + (size_t)tok * D + 32 * ks + 8 * grp)
+                          : u32x4{0, 0, 0, 0};
+      constexpr int CH = D / 8;
+#pragma unroll
+      for (int i = 0; i < G::VROWREG; ++i) {
+        const int c = lane + 64 * i;
+        const int vt = page * 16 + c / CH;
+        R.vrow[pp][i] = (valid && vt < S_contig)
+                            ? ld_stream<u32x4>(Vp + (size_t)vt * D + (c % CH) * 8)
                             : u32x4{0, 0, 0, 0};
-        constexpr int CH = D / 8;
-#pragma unroll
-        for (int i = 0; i < G::VROWREG; ++i) {
-          const int c = lane + 64 * i;
-          const int vt = page * 16 + c / CH;
-          R.vrow[pp][i] = (valid && vt < S_contig)
-                              ? ld_stream<u32x4>(Vp + (size_t)vt * D + (c % CH) * 8)
-                              : u32x4{0, 0, 0, 0};
-        }
-      } else {
-        const int pid = __builtin_amdgcn_readlane(pid_lane, 2 * step + pp);
-        const size_t chunk = ((size_t)pid * Hkv + hk) * chunk_elems;
-        if (KIND == kKindPaged16) {
-          const uint16_t* Kp = (const uint16_t*)Kc + chunk;
-          const uint16_t* Vp = (const uint16_t*)Vc + chunk;
-#pragma unroll
-          for (int i = 0; i < G::KREG; ++i)
-            R.k[pp][i] = valid ? ld_stream<u32x4>(Kp + (lane + 64 * i) * 8) : u32x4{0, 0, 0, 0};
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-            R.v16[pp][nb] = valid ? ld_stream<u32x2>(Vp + (16 * nb + l16) * 16 + 4 * grp) : u32x2{0, 0};
-        } else {
-          const unsigned char* Kp = (const unsigned char*)Kc + chunk;
-          const unsigned char* Vp = (const unsigned char*)Vc + chunk;
-#pragma unroll
-          for (int i = 0; i < G::KREG; ++i)
-            R.k[pp][i] = valid ? ld_stream<u32x4>(Kp + (lane + 64 * i) * 16) : u32x4{0, 0, 0, 0};
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-            R.v8[pp][nb] = valid ? ld_stream<uint32_t>(Vp + (16 * nb + l16) * 16 + 4 * grp) : 0u;
-        }
       }
     }
   };
@@ -243,24 +183,9 @@ void decode_split_kernel(
   float m_run = kNegInf, l_run = 0.f;
 
   // ---- one step of attention on registers R ----
-  auto compute_step = [&](const StepRegs<D, KIND>& R, int step) {
-    // stage K (paged) or V rows (contiguous) into the wave's LDS
-    if (KIND == kKindPaged16) {
-      uint16_t* kl = (uint16_t*)wlds;
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int i = 0; i < G::KREG; ++i) {
-          const int e = (lane + 64 * i) * 8;  // element offset in the [D][16] page
-          *(u32x4*)(kl + pp * G::kPaged16PageElems + e + (e >> 7) * 64) = R.k[pp][i];
-        }
-    } else if (KIND == kKindPagedFp8) {
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp)
-#pragma unroll
-        for (int i = 0; i < G::KREG; ++i)
-          *(u32x4*)(wlds + pp * D * 16 + (lane + 64 * i) * 16) = R.k[pp][i];
-    } else {
+  auto compute_step = [&](const ContigRegs<D>& R, int step) {
+    // stage the V rows into the wave's LDS
+    {
       uint16_t* vl = (uint16_t*)wlds;
       constexpr int CH = D / 8;
 #pragma unroll
@@ -279,46 +204,20 @@ void decode_split_kernel(
     for (int pp = 0; pp < 2; ++pp) {
       s[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        vec8 a;
-        if (KIND == kKindPaged16) {
-          // tr16: source lane (j = l16/4, c = l16%4) -> row 32ks + 8grp + 4r + j, col 4c
-          const uint16_t* kl = (const uint16_t*)wlds + pp * G::kPaged16PageElems;
-          const int row = 32 * ks + 8 * grp + (l16 >> 2);
-          const int row4 = row + 4;
-          const vec4 lo = Tr::tr_read((const CA_LDS void*)(kl + row * 16 + (row >> 3) * 64 + 4 * (l16 & 3)));
-          const vec4 hi = Tr::tr_read((const CA_LDS void*)(kl + row4 * 16 + (row4 >> 3) * 64 + 4 * (l16 & 3)));
-          a = cat4<vec8, vec4>(lo, hi);
-        } else if (KIND == kKindPagedFp8) {
-          // tr8: source lane (j = l16/2, c = l16%2) -> row 32ks + 8grp + j, col 8c
-          const int row = 32 * ks + 8 * grp + (l16 >> 1);
-          const i32x2 raw = tr8_read((const CA_LDS void*)(wlds + pp * D * 16 + row * 16 + 8 * (l16 & 1)));
-          a = fp8x8_to<Tr>((uint32_t)raw[0], (uint32_t)raw[1]);
-        } else {
-          a = __builtin_bit_cast(vec8, R.k[pp][ks]);
-        }
-        s[pp] = Tr::mfma16(a, qv[ks], s[pp]);
-      }
+      for (int ks = 0; ks < NKS; ++ks)
+        s[pp] = Tr::mfma16(__builtin_bit_cast(vec8, R.k[pp][ks]), qv[ks], s[pp]);
     }
 
     // online softmax over the step's 32 tokens
     const int pageA = p_begin + 2 * step;
-    float cA = scale_log2, cB = scale_log2, vsA = 1.f, vsB = 1.f;
-    if (KIND == kKindPagedFp8) {
-      cA *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), 2 * step));
-      cB *= __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ksc_lane), 2 * step + 1));
-      vsA = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), 2 * step));
-      vsB = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vsc_lane), 2 * step + 1));
-    }
     float x[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      x[r] = s[0][r] * cA;
-      x[4 + r] = s[1][r] * cB;
+      x[r] = s[0][r] * scale_log2;
+      x[4 + r] = s[1][r] * scale_log2;
     }
     // tokens past the context (or the wave's last page) are masked; their V
-    // slots are zeroed too, so stale cache bytes (NaN patterns included) in
-    // a partially filled page cannot reach the PV product
+    // slots are zeroed too
     const bool partial = (pageA + 2) * 16 > Lctx || pageA + 1 >= p_end;
     bool slot_ok[8];
 #pragma unroll
@@ -353,8 +252,8 @@ void decode_split_kernel(
     vec8 pa;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const vec2 ua = Tr::pack2(p[2 * j] * vsA, p[2 * j + 1] * vsA);
-      const vec2 ub = Tr::pack2(p[4 + 2 * j] * vsB, p[4 + 2 * j + 1] * vsB);
+      const vec2 ua = Tr::pack2(p[2 * j], p[2 * j + 1]);
+      const vec2 ub = Tr::pack2(p[4 + 2 * j], p[4 + 2 * j + 1]);
       pa[2 * j] = ua[0];
       pa[2 * j + 1] = ua[1];
       pa[4 + 2 * j] = ub[0];
@@ -364,20 +263,13 @@ void decode_split_kernel(
     // O += P V^T
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      vec8 bv;
-      if (KIND == kKindPaged16) {
-        bv = cat4<vec8, vec4>(__builtin_bit_cast(vec4, R.v16[0][nb]), __builtin_bit_cast(vec4, R.v16[1][nb]));
-      } else if (KIND == kKindPagedFp8) {
-        bv = fp8x8_to<Tr>(R.v8[0][nb], R.v8[1][nb]);
-      } else {
-        // tr16: source lane (j = l16/4, c = l16%4) -> row (16pp + 4grp + j), col 16nb + 4c
-        const uint16_t* vl = (const uint16_t*)wlds;
-        const int row = 4 * grp + (l16 >> 2);
-        const int col = 16 * nb + 4 * (l16 & 3);
-        const vec4 lo = Tr::tr_read((const CA_LDS void*)(vl + row * (D + 16) + col));
-        const vec4 hi = Tr::tr_read((const CA_LDS void*)(vl + (16 + row) * (D + 16) + col));
-        bv = cat4<vec8, vec4>(lo, hi);
-      }
+      // tr16: source lane (j = l16/4, c = l16%4) -> row (16pp + 4grp + j), col 16nb + 4c
+      const uint16_t* vl = (const uint16_t*)wlds;
+      const int row = 4 * grp + (l16 >> 2);
+      const int col = 16 * nb + 4 * (l16 & 3);
+      const vec4 lo = Tr::tr_read((const CA_LDS void*)(vl + row * (D + 16) + col));
+      const vec4 hi = Tr::tr_read((const CA_LDS void*)(vl + (16 + row) * (D + 16) + col));
+      vec8 bv = cat4<vec8, vec4>(lo, hi);
       if (partial) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
@@ -389,7 +281,7 @@ void decode_split_kernel(
   };
 
   // ---- the walk: register sets A and B alternate ----
-  StepRegs<D, KIND> A, B;
+  ContigRegs<D> A, B;
   if (n_steps > 0) load_step(A, 0);
   for (int step = 0; step < n_steps; step += 2) {
     if (step + 1 < n_steps) load_step(B, step + 1);
@@ -442,45 +334,25 @@ void decode_split_kernel(
 // parity so the tr16 reads of lane groups 0/1 and 2/3 hit disjoint banks),
 // V pages linear [D][16].
 // ---------------------------------------------------------------------------
-#ifndef CA_DEC_SPLIT_OUTER
-#define CA_DEC_SPLIT_OUTER 2
-#endif
-// Cache policy of the page loads: "nt" (every byte is read once per launch,
-// so it is streamed rather than retained).
-#ifndef CA_DMA_POLICY
-#define CA_DMA_POLICY 2
-#endif
-
-#ifndef CA_DMA_PPS
-#define CA_DMA_PPS 1
-#endif
-#ifndef CA_RING_FP8
-#define CA_RING_FP8 4
-#endif
-#ifndef CA_RING_16
-#define CA_RING_16 3
-#endif
-// Pages per split of the direct-load decode (64 or 128: one or two page-id
-// registers per lane): 256 KB of K and V per split for both cache kinds
-// (128 fp8 pages, 64 16-bit pages). A split's start (context length,
-// block-table row, scales, filling the ring) is paid once per split: 128
-// fp8 pages measured +3.5 % on C4 over 64, while 128 16-bit pages leave C3
-// too few waves (-3 %).
-#ifndef CA_DMA_PAGES_FP8
-#define CA_DMA_PAGES_FP8 128
-#endif
-// Pages per step and ring depth of the direct-load decode. One page per step
-// keeps a ring slot small (K + V of one page), so more waves fit a CU's LDS
-// and more bytes are in flight per CU; the PV product then runs on 16x16x16
-// MFMAs, whose 4 k-values per lane are exactly the 4 tokens a lane holds.
+// Ring depth (steps of one page, K and V, in flight per wave) and pages per
+// split of the direct-load decode: 256 KB of K and V per split for both
+// cache kinds (128 fp8 pages, two page-id registers per lane; 64 16-bit
+// pages, one). A split's start (context length, block-table row, scales,
+// filling the ring) is paid once per split: 128 fp8 pages measured +3.5 % on
+// C4 over 64, while 128 16-bit pages leave C3 too few waves (-3 %). One page
+// per step keeps a ring slot small (K + V of one page), so more waves fit a
+// CU's LDS and more bytes are in flight per CU; the PV product then runs on
+// 16x16x16 MFMAs, whose 4 k-values per lane are exactly the 4 tokens a lane
+// holds. Page loads use the "nt" cache policy: every cache byte is read
+// once per launch, so it is streamed rather than retained.
 template <int KIND>
 struct DmaCfg {
-  static constexpr int kPagesPerStep = CA_DMA_PPS;
-  static constexpr int kRing = KIND == kKindPagedFp8 ? CA_RING_FP8 : CA_RING_16;
-  static constexpr int kPages = KIND == kKindPagedFp8 ? CA_DMA_PAGES_FP8 : kPagesPerWave;
+  static constexpr int kRing = KIND == kKindPagedFp8 ? 4 : 3;
+  static constexpr int kPages = KIND == kKindPagedFp8 ? 128 : kPagesPerWave;
   // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
   static_assert(kPages >= kPagesPerWave, "pages per split");
 };
+constexpr int kDmaPolicy = 2;  // global_load_lds cache policy bits: nt
 
 template <typename Tr, int D, int KIND>
 __global__ __launch_bounds__(64) void decode_dma_kernel(
@@ -497,12 +369,10 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   constexpr int ELEM = FP8 ? 1 : 2;
   constexpr int CHUNK = D * 16 * ELEM;        // bytes of one (page, head) chunk
   constexpr int NDMA = CHUNK / 1024;          // 16 B x 64 lanes per load
-  constexpr int PPS = DmaCfg<KIND>::kPagesPerStep;
-  constexpr int STAGE = 2 * PPS * CHUNK;      // K and V of the step's pages
+  constexpr int STAGE = 2 * CHUNK;            // K and V of the step's page
   constexpr int RING = DmaCfg<KIND>::kRing;
-  constexpr int DPS = 2 * PPS * NDMA;         // loads per step
+  constexpr int DPS = 2 * NDMA;               // loads per step
   constexpr int KRD = FP8 ? NKS : 2 * NKS;    // LDS reads for one page's K^T operands
-  static_assert(PPS == 1 || PPS == 2, "pages per step");
   constexpr int kDmaPages = DmaCfg<KIND>::kPages;
   constexpr int PB = kDmaPages / 64;          // page-id registers per lane
   static_assert(kDmaPages % 64 == 0 && PB <= 2, "pages per split");
@@ -511,23 +381,12 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 
   const int lane = threadIdx.x;
   int w = blockIdx.x;
-#if CA_DEC_SPLIT_OUTER == 2
   // split index outermost, counted from each sequence's end: the waves of
   // splits before a sequence's start (none exist) come first and retire at
   // once, and every sequence's last (partial) split is in the final group
   const int per_split = (int)(gridDim.x / max_splits);
   const int from_end = max_splits - 1 - w / per_split;
   w %= per_split;
-#elif CA_DEC_SPLIT_OUTER
-  // split index outermost: every sequence's first splits come first and the
-  // waves of splits past a sequence's end gather at the tail of the grid
-  const int per_split = (int)(gridDim.x / max_splits);
-  const int split = w / per_split;
-  w %= per_split;
-#else
-  const int split = w % max_splits;
-  w /= max_splits;
-#endif
   const int hc = w % n_hc;
   w /= n_hc;
   const int hk = w % Hkv;
@@ -538,17 +397,13 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
   const int n_splits = max(1, (n_pages + kDmaPages - 1) / kDmaPages);
-#if CA_DEC_SPLIT_OUTER == 2
   const int split = n_splits - 1 - from_end;
   if (split < 0) return;
-#else
-  if (split >= n_splits) return;
-#endif
 
   const int l16 = lane & 15, grp = lane >> 4;
   const int p_begin = split * kDmaPages;
   const int p_end = min(p_begin + kDmaPages, n_pages);
-  const int n_steps = (p_end - p_begin + PPS - 1) / PPS;
+  const int n_steps = p_end - p_begin;
 
   vec8 qv[NKS];
   {
@@ -603,21 +458,18 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   const unsigned char* dummy = (const unsigned char*)Q;  // 16 valid bytes for padding loads
   auto issue_step = [&](int step, int slot) {
     unsigned char* base = ring + slot * STAGE;
+    const int page = p_begin + step;
+    const bool valid = step < n_steps;
+    const int pid = lane_val(pid_lane, valid ? step : 0);
+    const size_t chunk = ((size_t)pid * Hkv + hk) * (size_t)CHUNK;
+    const unsigned char* kp = (const unsigned char*)Kc + chunk;
+    const unsigned char* vp = (const unsigned char*)Vc + chunk;
+    (void)page;
 #pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
-      const int page = p_begin + PPS * step + pp;
-      const bool valid = step < n_steps && page < p_end;
-      const int idx = valid ? PPS * step + pp : 0;
-      const int pid = lane_val(pid_lane, idx);
-      const size_t chunk = ((size_t)pid * Hkv + hk) * (size_t)CHUNK;
-      const unsigned char* kp = (const unsigned char*)Kc + chunk;
-      const unsigned char* vp = (const unsigned char*)Vc + chunk;
-#pragma unroll
-      for (int i = 0; i < NDMA; ++i) {
-        dma16<CA_DMA_POLICY>(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + pp * 2 * CHUNK + 1024 * i));
-        dma16<CA_DMA_POLICY>(valid ? vp + 1024 * i + 16 * lane : dummy,
-              (CA_LDS void*)(base + pp * 2 * CHUNK + CHUNK + 1024 * i));
-      }
+    for (int i = 0; i < NDMA; ++i) {
+      dma16<kDmaPolicy>(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + 1024 * i));
+      dma16<kDmaPolicy>(valid ? vp + 1024 * i + 16 * lane : dummy,
+                        (CA_LDS void*)(base + CHUNK + 1024 * i));
     }
   };
 
@@ -639,111 +491,88 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegInf, l_run = 0.f;
 
-#pragma unroll
   // RING steps in flight from the start; a slot is refilled as soon as its
   // LDS reads have returned, so RING steps stay in flight during the math
-  for (int s = 0; s < RING; ++s) issue_step(s, s);
+#pragma unroll
+  for (int st = 0; st < RING; ++st) issue_step(st, st);
   int slot = 0;
   for (int step = 0; step < n_steps; ++step) {
     wait_vmcnt<(RING - 1) * DPS>();  // this step's loads are the oldest outstanding
-    const uint32_t sb = ring0 + slot * STAGE;
+    const uint32_t kb = ring0 + slot * STAGE;
+    const uint32_t vb = kb + CHUNK + v_off;
 
     // ---- LDS -> operands ----
-    u32x2 kraw[PPS][KRD];
-    uint32_t v8r[PPS][FP8 ? NB : 1];
-    u32x2 v16r[PPS][FP8 ? 1 : NB];
-#pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
-      const uint32_t kb = sb + pp * 2 * CHUNK;
-      const uint32_t vb = kb + CHUNK + v_off;
-      if (FP8) {
-        const uint32_t a = kb + k_lo;
-        kraw[pp][0] = lds_read_tr8<0>(a);
-        if (NKS > 1) kraw[pp][1 % KRD] = lds_read_tr8<512>(a);
-        if (NKS > 2) kraw[pp][2 % KRD] = lds_read_tr8<1024>(a);
-        if (NKS > 3) kraw[pp][3 % KRD] = lds_read_tr8<1536>(a);
-#define CA_V8(NBI) if (NBI < NB) v8r[pp][NBI % NB] = lds_read_b32<256 * NBI>(vb);
-        CA_V8(0) CA_V8(1) CA_V8(2) CA_V8(3) CA_V8(4) CA_V8(5) CA_V8(6) CA_V8(7)
+    u32x2 kraw[KRD];
+    uint32_t v8r[FP8 ? NB : 1];
+    u32x2 v16r[FP8 ? 1 : NB];
+    if (FP8) {
+      const uint32_t a = kb + k_lo;
+      kraw[0] = lds_read_tr8<0>(a);
+      if (NKS > 1) kraw[1 % KRD] = lds_read_tr8<512>(a);
+      if (NKS > 2) kraw[2 % KRD] = lds_read_tr8<1024>(a);
+      if (NKS > 3) kraw[3 % KRD] = lds_read_tr8<1536>(a);
+#define CA_V8(NBI) if (NBI < NB) v8r[NBI % NB] = lds_read_b32<256 * NBI>(vb);
+      CA_V8(0) CA_V8(1) CA_V8(2) CA_V8(3) CA_V8(4) CA_V8(5) CA_V8(6) CA_V8(7)
 #undef CA_V8
-      } else {
-        const uint32_t alo = kb + k_lo, ahi = kb + k_hi;
-        kraw[pp][0] = lds_read_tr16<0>(alo);
-        kraw[pp][1] = lds_read_tr16<0>(ahi);
-        if (NKS > 1) { kraw[pp][2 % KRD] = lds_read_tr16<1024>(alo); kraw[pp][3 % KRD] = lds_read_tr16<1024>(ahi); }
-        if (NKS > 2) { kraw[pp][4 % KRD] = lds_read_tr16<2048>(alo); kraw[pp][5 % KRD] = lds_read_tr16<2048>(ahi); }
-        if (NKS > 3) { kraw[pp][6 % KRD] = lds_read_tr16<3072>(alo); kraw[pp][7 % KRD] = lds_read_tr16<3072>(ahi); }
-#define CA_V16(NBI) if (NBI < NB) v16r[pp][NBI % NB] = lds_read_b64<512 * NBI>(vb);
-        CA_V16(0) CA_V16(1) CA_V16(2) CA_V16(3) CA_V16(4) CA_V16(5) CA_V16(6) CA_V16(7)
+    } else {
+      const uint32_t alo = kb + k_lo, ahi = kb + k_hi;
+      kraw[0] = lds_read_tr16<0>(alo);
+      kraw[1] = lds_read_tr16<0>(ahi);
+      if (NKS > 1) { kraw[2 % KRD] = lds_read_tr16<1024>(alo); kraw[3 % KRD] = lds_read_tr16<1024>(ahi); }
+      if (NKS > 2) { kraw[4 % KRD] = lds_read_tr16<2048>(alo); kraw[5 % KRD] = lds_read_tr16<2048>(ahi); }
+      if (NKS > 3) { kraw[6 % KRD] = lds_read_tr16<3072>(alo); kraw[7 % KRD] = lds_read_tr16<3072>(ahi); }
+#define CA_V16(NBI) if (NBI < NB) v16r[NBI % NB] = lds_read_b64<512 * NBI>(vb);
+      CA_V16(0) CA_V16(1) CA_V16(2) CA_V16(3) CA_V16(4) CA_V16(5) CA_V16(6) CA_V16(7)
 #undef CA_V16
-      }
     }
     wait_lgkm0();
 #pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
+    for (int i = 0; i < KRD; ++i) after_wait(kraw[i]);
 #pragma unroll
-      for (int i = 0; i < KRD; ++i) after_wait(kraw[pp][i]);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) {
-        if (FP8) after_wait(v8r[pp][i % (FP8 ? NB : 1)]);
-        else after_wait(v16r[pp][i % (FP8 ? 1 : NB)]);
-      }
+    for (int i = 0; i < NB; ++i) {
+      if (FP8) after_wait(v8r[i % (FP8 ? NB : 1)]);
+      else after_wait(v16r[i % (FP8 ? 1 : NB)]);
     }
     issue_step(step + RING, slot);  // the slot's data is in registers now
 
-    // ---- S^T per page ----
-    f32x4 s[PPS];
+    // ---- S^T of the page ----
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
-      s[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        vec8 a;
-        if (FP8) {
-          a = fp8x8_to<Tr>(kraw[pp][ks % KRD][0], kraw[pp][ks % KRD][1]);
-        } else {
-          const u32x4 t = {kraw[pp][(2 * ks) % KRD][0], kraw[pp][(2 * ks) % KRD][1],
-                           kraw[pp][(2 * ks + 1) % KRD][0], kraw[pp][(2 * ks + 1) % KRD][1]};
-          a = __builtin_bit_cast(vec8, t);
-        }
-        s[pp] = Tr::mfma16(a, qv[ks], s[pp]);
+    for (int ks = 0; ks < NKS; ++ks) {
+      vec8 a;
+      if (FP8) {
+        a = fp8x8_to<Tr>(kraw[ks % KRD][0], kraw[ks % KRD][1]);
+      } else {
+        const u32x4 t = {kraw[(2 * ks) % KRD][0], kraw[(2 * ks) % KRD][1],
+                         kraw[(2 * ks + 1) % KRD][0], kraw[(2 * ks + 1) % KRD][1]};
+        a = __builtin_bit_cast(vec8, t);
       }
+      s = Tr::mfma16(a, qv[ks], s);
     }
 
-    // ---- online softmax over the step's 16 * PPS tokens ----
-    const int page0 = p_begin + PPS * step;
-    float c[PPS], vs[PPS];
-#pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
-      c[pp] = scale_log2;
-      vs[pp] = 1.f;
-      if (FP8) {
-        c[pp] *= lane_val(ksc_lane, PPS * step + pp);
-        vs[pp] = lane_val(vsc_lane, PPS * step + pp);
-      }
+    // ---- online softmax over the page's 16 tokens ----
+    const int page0 = p_begin + step;
+    float c = scale_log2, vs = 1.f;
+    if (FP8) {
+      c *= lane_val(ksc_lane, step);
+      vs = lane_val(vsc_lane, step);
     }
-    float x[4 * PPS];
+    float x[4];
 #pragma unroll
-    for (int pp = 0; pp < PPS; ++pp)
+    for (int r = 0; r < 4; ++r) x[r] = s[r] * c;
+    // tokens past the context are masked; their V slots are zeroed too, so
+    // stale cache bytes (NaN patterns included) in a partially filled page
+    // cannot reach the PV product
+    const bool partial = (page0 + 1) * 16 > Lctx;
+    bool slot_ok[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) x[4 * pp + r] = s[pp][r] * c[pp];
-    // tokens past the context (or the wave's last page) are masked; their V
-    // slots are zeroed too, so stale cache bytes (NaN patterns included) in
-    // a partially filled page cannot reach the PV product
-    const bool partial = (page0 + PPS) * 16 > Lctx || page0 + PPS > p_end;
-    bool slot_ok[4 * PPS];
-#pragma unroll
-    for (int pp = 0; pp < PPS; ++pp)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        slot_ok[4 * pp + r] = ((page0 + pp) * 16 + 4 * grp + r < Lctx) && (page0 + pp < p_end);
+    for (int r = 0; r < 4; ++r) slot_ok[r] = page0 * 16 + 4 * grp + r < Lctx;
     if (partial) {
 #pragma unroll
-      for (int i = 0; i < 4 * PPS; ++i)
+      for (int i = 0; i < 4; ++i)
         if (!slot_ok[i]) x[i] = kNegInf;
     }
     float tmax = max3(x[0], x[1], __builtin_fmaxf(x[2], x[3]));
-    if (PPS == 2) tmax = max3(tmax, __builtin_fmaxf(x[4 % (4 * PPS)], x[5 % (4 * PPS)]),
-                              __builtin_fmaxf(x[6 % (4 * PPS)], x[7 % (4 * PPS)]));
     tmax = pair16_max(tmax);
     tmax = pair32_max(tmax);
     const bool need = tmax > m_run + 8.0f;
@@ -756,49 +585,37 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       m_run = m_new;
     }
     const float msub = (m_run == kNegInf) ? 0.f : m_run;
-    float p[4 * PPS];
+    float p[4];
 #pragma unroll
-    for (int i = 0; i < 4 * PPS; ++i) p[i] = fast_exp2(x[i] - msub);
+    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(x[i] - msub);
     float psum = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4 * PPS; ++i) psum += p[i];
+    for (int i = 0; i < 4; ++i) psum += p[i];
     l_run += psum;
-    // P operand (v scale folded in): PPS = 2 -> 8 values = 4 tokens of each
-    // page (16x16x32); PPS = 1 -> the lane's 4 tokens (16x16x16)
-    u32x4 pw;
-#pragma unroll
-    for (int pp = 0; pp < PPS; ++pp) {
-      pw[2 * pp] = __builtin_bit_cast(uint32_t, Tr::pack2(p[4 * pp] * vs[pp], p[4 * pp + 1] * vs[pp]));
-      pw[2 * pp + 1] = __builtin_bit_cast(uint32_t, Tr::pack2(p[4 * pp + 2] * vs[pp], p[4 * pp + 3] * vs[pp]));
-    }
+    // P operand (v scale folded in): the lane's 4 tokens (16x16x16)
+    u32x2 pw;
+    pw[0] = __builtin_bit_cast(uint32_t, Tr::pack2(p[0] * vs, p[1] * vs));
+    pw[1] = __builtin_bit_cast(uint32_t, Tr::pack2(p[2] * vs, p[3] * vs));
 
     // ---- O += P V^T ----
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      u32x4 bw;
-#pragma unroll
-      for (int pp = 0; pp < PPS; ++pp) {
-        if (FP8) {
-          const uint32_t v = v8r[pp][nb % (FP8 ? NB : 1)];
-          bw[2 * pp] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(v));
-          bw[2 * pp + 1] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(v));
-        } else {
-          bw[2 * pp] = v16r[pp][nb % (FP8 ? 1 : NB)][0];
-          bw[2 * pp + 1] = v16r[pp][nb % (FP8 ? 1 : NB)][1];
-        }
+      u32x2 bw;
+      if (FP8) {
+        const uint32_t v = v8r[nb % (FP8 ? NB : 1)];
+        bw[0] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(v));
+        bw[1] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(v));
+      } else {
+        bw[0] = v16r[nb % (FP8 ? 1 : NB)][0];
+        bw[1] = v16r[nb % (FP8 ? 1 : NB)][1];
       }
       if (partial) {
         // zero masked token slots: 16-bit halves of the operand dwords
 #pragma unroll
-        for (int i = 0; i < 4 * PPS; ++i)
+        for (int i = 0; i < 4; ++i)
           if (!slot_ok[i]) bw[i >> 1] &= (i & 1) ? 0x0000ffffu : 0xffff0000u;
       }
-      if (PPS == 2) {
-        o[nb] = Tr::mfma16(__builtin_bit_cast(vec8, pw), __builtin_bit_cast(vec8, bw), o[nb]);
-      } else {
-        const u32x2 a2 = {pw[0], pw[1]}, b2 = {bw[0], bw[1]};
-        o[nb] = Tr::mfma16k16(__builtin_bit_cast(vec4, a2), __builtin_bit_cast(vec4, b2), o[nb]);
-      }
+      o[nb] = Tr::mfma16k16(__builtin_bit_cast(vec4, pw), __builtin_bit_cast(vec4, bw), o[nb]);
     }
     slot = (slot == RING - 1) ? 0 : slot + 1;
   }
@@ -883,19 +700,16 @@ size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
 }
 
 template <typename Tr, int D, int KIND>
-static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
-                                  const float* k_scale, const float* v_scale, int per_block,
-                                  const int32_t* bt, const int32_t* lens, void* out, int N,
-                                  int Hq, int Hkv, int max_blocks, int num_blocks, int S_contig,
-                                  float scale, void* ws, size_t ws_bytes, hipStream_t stream) {
-  const int max_tokens = (KIND == kKindContig16) ? S_contig : max_blocks * kDecodePage;
-  const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  // the direct-load kernel splits at DmaCfg<KIND>::kPages pages, the others
-  // at kPagesPerWave; the workspace (sized for kPagesPerWave-page splits)
-  // covers both
-  const bool dma = KIND != kKindContig16 && kDecodeDma;
-  const int pps = dma ? DmaCfg<KIND>::kPages : kPagesPerWave;
-  const int max_splits = max(1, (pages + pps - 1) / pps);
+static hipError_t launch_paged_decode_t(const void* q, const void* kc, const void* vc,
+                                        const float* k_scale, const float* v_scale, int per_block,
+                                        const int32_t* bt, const int32_t* lens, void* out, int N,
+                                        int Hq, int Hkv, int max_blocks, int num_blocks,
+                                        float scale, void* ws, size_t ws_bytes,
+                                        hipStream_t stream) {
+  const int max_tokens = max_blocks * kDecodePage;
+  // splits of DmaCfg<KIND>::kPages pages; the workspace (sized for
+  // kPagesPerWave-page splits) covers them
+  const int max_splits = max(1, (max_blocks + DmaCfg<KIND>::kPages - 1) / DmaCfg<KIND>::kPages);
   const int Gq = Hq / Hkv;
   const int n_hc = (Gq + 15) / 16;
   const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
@@ -904,43 +718,69 @@ static hipError_t launch_decode_t(const void* q, const void* kc, const void* vc,
   float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
   const long long total_waves = (long long)N * Hkv * n_hc * max_splits;
   if (total_waves == 0) return hipSuccess;
-  if (dma) {
-    if (total_waves > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((decode_dma_kernel<Tr, D, KIND>), dim3((unsigned)total_waves), dim3(64), 0,
-                       stream, (const uint16_t*)q, kc, vc, k_scale, v_scale, per_block, bt, lens,
-                       (uint16_t*)out, ws_o, ws_lse, Hq, Hkv, max_blocks, num_blocks, max_splits,
-                       n_hc, scale * kLog2e);
-  } else {
-    const long long grid = (total_waves + kDecodeWgWaves - 1) / kDecodeWgWaves;
-    if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((decode_split_kernel<Tr, D, KIND>), dim3((unsigned)grid),
-                       dim3(kDecodeWgWaves * 64), 0, stream, (const uint16_t*)q, kc, vc, k_scale,
-                       v_scale, per_block, bt, lens, (uint16_t*)out, ws_o, ws_lse, Hq, Hkv,
-                       max_blocks, num_blocks, S_contig, max_splits, n_hc, total_waves,
-                       scale * kLog2e);
-  }
+  if (total_waves > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((decode_dma_kernel<Tr, D, KIND>), dim3((unsigned)total_waves), dim3(64), 0,
+                     stream, (const uint16_t*)q, kc, vc, k_scale, v_scale, per_block, bt, lens,
+                     (uint16_t*)out, ws_o, ws_lse, Hq, Hkv, max_blocks, num_blocks, max_splits,
+                     n_hc, scale * kLog2e);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_splits <= 1) return e;
   hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
-                     KIND == kKindContig16 ? nullptr : lens, max_tokens, ws_o, ws_lse, out, Hq,
-                     max_splits, pps);
+                     lens, max_tokens, ws_o, ws_lse, out, Hq, max_splits, DmaCfg<KIND>::kPages);
+  return hipGetLastError();
+}
+
+template <typename Tr, int D>
+static hipError_t launch_contig_decode_t(const void* q, const void* k, const void* v, void* out,
+                                         int N, int Hq, int Hkv, int S, float scale, void* ws,
+                                         size_t ws_bytes, hipStream_t stream) {
+  const int pages = (S + kDecodePage - 1) / kDecodePage;
+  const int max_splits = max(1, (pages + kPagesPerWave - 1) / kPagesPerWave);
+  const int Gq = Hq / Hkv;
+  const int n_hc = (Gq + 15) / 16;
+  const size_t need = decode_workspace_bytes(N, Hq, D, S);
+  if (ws_bytes < need) return hipErrorInvalidValue;
+  float* ws_o = (float*)ws;
+  float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
+  const long long total_waves = (long long)N * Hkv * n_hc * max_splits;
+  if (total_waves == 0) return hipSuccess;
+  const long long grid = (total_waves + kDecodeWgWaves - 1) / kDecodeWgWaves;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((decode_split_kernel<Tr, D>), dim3((unsigned)grid), dim3(kDecodeWgWaves * 64),
+                     0, stream, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                     (uint16_t*)out, ws_o, ws_lse, Hq, Hkv, S, max_splits, n_hc, total_waves,
+                     scale * kLog2e);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || max_splits <= 1) return e;
+  hipLaunchKernelGGL((decode_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
+                     nullptr, S, ws_o, ws_lse, out, Hq, max_splits, kPagesPerWave);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// float32 decode, contiguous or paged cache (VALU).
+// float32-query decode: contiguous or paged float32 cache, or paged FP8 e4m3
+// cache (VALU).
 //
 // The reference instantiates its decode and paged kernels for float
-// (async_flash_decode_instantiations.cu:4, paged_attention_instantiations.cu);
-// fp32 has no 16-bit MFMA operand form and decode is HBM-bound, so here the
-// dot products are fp32 FMAs. Per step of 64 tokens each lane owns one token
-// for S = q.k (the wave's G query heads are broadcast from LDS, pre-scaled to
-// log2 units), the step's max is a wave reduction, and for O += P V each lane
-// owns D/64 head-dim elements with P broadcast from LDS. Same split-K
-// partition (kPagesPerWave pages per wave, split index outermost), workspace
-// layout and merge as the 16-bit kernels. A paged sequence's tokens past its
-// length are never read into O (their bytes may be anything).
+// (async_flash_decode_instantiations.cu:4, paged_attention_instantiations.cu)
+// and its FP8 paged kernel for float queries and output
+// (fp8_paged_attention_instantiations.cu:4, dispatched for at::kFloat at
+// fused_softmax_binding.cpp:683-691). fp32 has no 16-bit MFMA operand form
+// and decode is HBM-bound, so here the dot products are fp32 FMAs. Per step
+// of 64 tokens each lane owns one token for S = q.k (the wave's G query heads
+// are broadcast from LDS, pre-scaled to log2 units), the step's max is a
+// wave reduction, and for O += P V each lane owns D/64 head-dim elements with
+// P broadcast from LDS. FP8 caches decode e4m3 codes exactly to fp32 and fold
+// the scales as the reference does (fp8_paged_attention_kernel.cuh:94,104,
+// 137): logit = (sum q * code_k) * k_scale, o += p * v_scale * code_v, with
+// the scale of the token's physical page (per_block) or of the kv head. Same
+// split-K partition (kPagesPerWave pages per wave, split index outermost),
+// workspace layout and merge as the 16-bit kernels. A paged sequence's tokens
+// past its length are never read into O (their bytes may be anything); block
+// ids outside [0, num_blocks) are clamped, as in the 16-bit kernels.
 // ---------------------------------------------------------------------------
+enum : int { kSrcF32Contig = 0, kSrcF32Paged = 1, kSrcFp8Paged = 2 };
+
 __device__ __forceinline__ float wave_max_f(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = __builtin_fmaxf(x, __shfl_xor(x, off, 64));
@@ -951,13 +791,23 @@ __device__ __forceinline__ float wave_sum_f(float x) {
   for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
   return x;
 }
+// one e4m3 code (byte `b` of w) -> float, exact
+__device__ __forceinline__ float e4m3_to_f32(uint32_t w, int b) {
+  const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
+  const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
+  return b == 0 ? lo[0] : b == 1 ? lo[1] : b == 2 ? hi[0] : hi[1];
+}
 
-template <int D, bool PAGED, int G>
+template <int D, int SRC, int G>
 __global__ __launch_bounds__(64) void decode_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ Kc, const float* __restrict__ Vc,
+    const float* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
     float* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
-    int Hkv, int S_contig, int max_blocks, int max_splits, int n_hc, float scale_log2) {
+    int Hkv, int S_contig, int max_blocks, int num_blocks, int max_splits, int n_hc,
+    float scale_log2) {
+  constexpr bool PAGED = SRC != kSrcF32Contig;
+  constexpr bool FP8 = SRC == kSrcFp8Paged;
   constexpr int PER = D / 64;
   constexpr int kSplitTokens = kPagesPerWave * kDecodePage;
   __shared__ float qs[G][D];
@@ -995,9 +845,20 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(
 #pragma unroll
     for (int i = 0; i < PER; ++i) o[g][i] = 0.f;
   }
-  const float* Kh = PAGED ? Kc : Kc + ((size_t)n * Hkv + hk) * S_contig * D;
-  const float* Vh = PAGED ? Vc : Vc + ((size_t)n * Hkv + hk) * S_contig * D;
+  const float* Kf = (const float*)Kc;
+  const float* Vf = (const float*)Vc;
+  const uint8_t* K8 = (const uint8_t*)Kc;
+  const uint8_t* V8 = (const uint8_t*)Vc;
+  const float* Kh = PAGED ? Kf : Kf + ((size_t)n * Hkv + hk) * S_contig * D;
+  const float* Vh = PAGED ? Vf : Vf + ((size_t)n * Hkv + hk) * S_contig * D;
   const int32_t* bt = PAGED ? block_tables + (size_t)n * max_blocks : nullptr;
+  auto block_of = [&](int page) CA_INLINE { return min(max(bt[page], 0), num_blocks - 1); };
+  auto kscale_of = [&](int blk) CA_INLINE {
+    return per_block ? k_scale[(size_t)blk * Hkv + hk] : k_scale[hk];
+  };
+  auto vscale_of = [&](int blk) CA_INLINE {
+    return per_block ? v_scale[(size_t)blk * Hkv + hk] : v_scale[hk];
+  };
 
   for (int t0 = t_begin; t0 < t_end; t0 += 64) {  // t0 is a multiple of 64: 4 whole pages
     const int t = t0 + lane;
@@ -1006,9 +867,21 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(
     float s[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) s[g] = 0.f;
-    if (PAGED) {
-      const int blk = bt[tc / kDecodePage];
-      const float* kp = Kc + ((size_t)blk * Hkv + hk) * D * kDecodePage + (tc % kDecodePage);
+    if (FP8) {
+      const int blk = block_of(tc / kDecodePage);
+      const uint8_t* kp = K8 + ((size_t)blk * Hkv + hk) * D * kDecodePage + (tc % kDecodePage);
+#pragma unroll 8
+      for (int d = 0; d < D; ++d) {
+        const float kv = e4m3_to_f32(kp[d * kDecodePage], 0);
+#pragma unroll
+        for (int g = 0; g < G; ++g) s[g] = __builtin_fmaf(qs[g][d], kv, s[g]);
+      }
+      const float ks = kscale_of(blk);
+#pragma unroll
+      for (int g = 0; g < G; ++g) s[g] *= ks;
+    } else if (PAGED) {
+      const int blk = block_of(tc / kDecodePage);
+      const float* kp = Kf + ((size_t)blk * Hkv + hk) * D * kDecodePage + (tc % kDecodePage);
 #pragma unroll 8
       for (int d = 0; d < D; ++d) {
         const float kv = kp[d * kDecodePage];
@@ -1045,17 +918,30 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(
     const int nv = min(64, t_end - t0);
     if (PAGED) {
       for (int pg = 0; pg < 4 && 16 * pg < nv; ++pg) {
-        const int blk = bt[t0 / kDecodePage + pg];
-        const float* vp = Vc + ((size_t)blk * Hkv + hk) * D * kDecodePage;
+        const int blk = block_of(t0 / kDecodePage + pg);
         const int cnt = min(16, nv - 16 * pg);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-          const float* vrow = vp + (size_t)(lane + 64 * i) * kDecodePage;
           float vv[16];
+          if (FP8) {
+            const uint8_t* vrow = V8 + (((size_t)blk * Hkv + hk) * D + lane + 64 * i) * kDecodePage;
+            const uint4 x = *(const uint4*)vrow;
+            const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+            const float vs = vscale_of(blk);
 #pragma unroll
-          for (int j = 0; j < 16; j += 4) {
-            const float4 x = *(const float4*)(vrow + j);
-            vv[j] = x.x; vv[j + 1] = x.y; vv[j + 2] = x.z; vv[j + 3] = x.w;
+            for (int j = 0; j < 16; j += 2) {
+              const f32x2 f = (j & 2) ? __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(wd[j / 4], 1.0f, true)
+                                      : __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(wd[j / 4], 1.0f, false);
+              vv[j] = f[0] * vs;
+              vv[j + 1] = f[1] * vs;
+            }
+          } else {
+            const float* vrow = Vf + (((size_t)blk * Hkv + hk) * D + lane + 64 * i) * kDecodePage;
+#pragma unroll
+            for (int j = 0; j < 16; j += 4) {
+              const float4 x = *(const float4*)(vrow + j);
+              vv[j] = x.x; vv[j + 1] = x.y; vv[j + 2] = x.z; vv[j + 3] = x.w;
+            }
           }
           for (int j = 0; j < cnt; ++j) {
 #pragma unroll
@@ -1096,51 +982,66 @@ __global__ __launch_bounds__(64) void decode_f32_kernel(
   }
 }
 
-template <int D, bool PAGED, int G>
-static hipError_t launch_decode_f32_t(const void* q, const void* kc, const void* vc,
-                                      const int32_t* bt, const int32_t* lens, void* out, int N,
-                                      int Hq, int Hkv, int max_blocks, int S_contig, float scale,
-                                      void* ws, size_t ws_bytes, hipStream_t stream) {
-  const int max_tokens = PAGED ? max_blocks * kDecodePage : S_contig;
+// Arguments of a float32-query decode launch.
+struct F32DecodeArgs {
+  const void* q;
+  const void* kc;
+  const void* vc;
+  const float* k_scale;
+  const float* v_scale;
+  int per_block;
+  const int32_t* bt;
+  const int32_t* lens;
+  void* out;
+  int N, Hq, Hkv, max_blocks, num_blocks, S_contig;
+  float scale;
+  void* ws;
+  size_t ws_bytes;
+};
+
+template <int D, int SRC, int G>
+static hipError_t launch_decode_f32_t(const F32DecodeArgs& a, hipStream_t stream) {
+  constexpr bool PAGED = SRC != kSrcF32Contig;
+  const int max_tokens = PAGED ? a.max_blocks * kDecodePage : a.S_contig;
   const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
   const int max_splits = max(1, (pages + kPagesPerWave - 1) / kPagesPerWave);
-  const int Gq = Hq / Hkv;
+  const int Gq = a.Hq / a.Hkv;
   const int n_hc = (Gq + G - 1) / G;
-  const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
-  if (ws_bytes < need) return hipErrorInvalidValue;
-  float* ws_o = (float*)ws;
-  float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
-  const long long grid = (long long)N * Hkv * n_hc * max_splits;
+  const size_t need = decode_workspace_bytes(a.N, a.Hq, D, max_tokens);
+  if (a.ws_bytes < need) return hipErrorInvalidValue;
+  float* ws_o = (float*)a.ws;
+  float* ws_lse = need ? ws_o + (size_t)a.N * a.Hq * max_splits * D : nullptr;
+  const long long grid = (long long)a.N * a.Hkv * n_hc * max_splits;
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((decode_f32_kernel<D, PAGED, G>), dim3((unsigned)grid), dim3(64), 0, stream,
-                     (const float*)q, (const float*)kc, (const float*)vc, bt, lens, (float*)out,
-                     ws_o, ws_lse, Hq, Hkv, S_contig, max_blocks, max_splits, n_hc,
-                     scale * kLog2e);
+  hipLaunchKernelGGL((decode_f32_kernel<D, SRC, G>), dim3((unsigned)grid), dim3(64), 0, stream,
+                     (const float*)a.q, a.kc, a.vc, a.k_scale, a.v_scale, a.per_block, a.bt, a.lens,
+                     (float*)a.out, ws_o, ws_lse, a.Hq, a.Hkv, a.S_contig, a.max_blocks,
+                     a.num_blocks, max_splits, n_hc, a.scale * kLog2e);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_splits <= 1) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<F32, D>), dim3((unsigned)(N * Hq)), dim3(64), 0, stream,
-                     PAGED ? lens : nullptr, max_tokens, ws_o, ws_lse, out, Hq, max_splits,
-                     kPagesPerWave);
+  hipLaunchKernelGGL((decode_merge_kernel<F32, D>), dim3((unsigned)(a.N * a.Hq)), dim3(64), 0,
+                     stream, PAGED ? a.lens : nullptr, max_tokens, ws_o, ws_lse, a.out, a.Hq,
+                     max_splits, kPagesPerWave);
   return hipGetLastError();
 }
 
 // Query heads per wave for the fp32 kernel: the group size rounded up to a
 // power of two, at most 8 (larger groups take several waves).
-template <int D, bool PAGED>
-static hipError_t launch_decode_f32(const void* q, const void* kc, const void* vc,
-                                    const int32_t* bt, const int32_t* lens, void* out, int N,
-                                    int Hq, int Hkv, int max_blocks, int S_contig, float scale,
-                                    void* ws, size_t ws_bytes, hipStream_t stream) {
-  const int Gq = Hq / Hkv;
-#define CA_F32D(GG)                                                                          \
-  return launch_decode_f32_t<D, PAGED, GG>(q, kc, vc, bt, lens, out, N, Hq, Hkv, max_blocks, \
-                                           S_contig, scale, ws, ws_bytes, stream);
-  if (Gq <= 1) { CA_F32D(1) }
-  if (Gq <= 2) { CA_F32D(2) }
-  if (Gq <= 4) { CA_F32D(4) }
-  CA_F32D(8)
+template <int SRC>
+static hipError_t launch_decode_f32(int D, const F32DecodeArgs& a, hipStream_t stream) {
+  const int Gq = a.Hq / a.Hkv;
+#define CA_F32D(DD, GG) return launch_decode_f32_t<DD, SRC, GG>(a, stream);
+#define CA_F32G(DD)                  \
+  if (Gq <= 1) { CA_F32D(DD, 1) }    \
+  if (Gq <= 2) { CA_F32D(DD, 2) }    \
+  if (Gq <= 4) { CA_F32D(DD, 4) }    \
+  CA_F32D(DD, 8)
+  if (D == 64) { CA_F32G(64) }
+  if (D == 128) { CA_F32G(128) }
+#undef CA_F32G
 #undef CA_F32D
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const void* kc,
@@ -1149,21 +1050,19 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
                                const int32_t* context_lens, void* out, int N, int Hq, int Hkv,
                                int D, int max_blocks_per_seq, int num_blocks, float scale,
                                void* ws, size_t ws_bytes, hipStream_t stream) {
-#define CA_DEC(TR, DD, KIND)                                                                \
-  if (D == DD)                                                                              \
-    return launch_decode_t<TR, DD, KIND>(q, kc, vc, k_scale, v_scale, per_block_scales,     \
-                                         block_tables, context_lens, out, N, Hq, Hkv,       \
-                                         max_blocks_per_seq, num_blocks, 0, scale, ws,      \
-                                         ws_bytes, stream);
+#define CA_DEC(TR, DD, KIND)                                                                 \
+  if (D == DD)                                                                               \
+    return launch_paged_decode_t<TR, DD, KIND>(q, kc, vc, k_scale, v_scale, per_block_scales, \
+                                               block_tables, context_lens, out, N, Hq, Hkv,   \
+                                               max_blocks_per_seq, num_blocks, scale, ws,      \
+                                               ws_bytes, stream);
+  if (dtype == kDtypeF32) {
+    const F32DecodeArgs a{q,   kc, vc, k_scale, v_scale, per_block_scales, block_tables, context_lens,
+                          out, N,  Hq, Hkv,     max_blocks_per_seq, num_blocks, 0, scale, ws, ws_bytes};
+    return cache_kind == 0 ? launch_decode_f32<kSrcF32Paged>(D, a, stream)
+                           : launch_decode_f32<kSrcFp8Paged>(D, a, stream);
+  }
   if (cache_kind == 0) {
-    if (dtype == kDtypeF32) {
-      if (D == 64)
-        return launch_decode_f32<64, true>(q, kc, vc, block_tables, context_lens, out, N, Hq, Hkv,
-                                           max_blocks_per_seq, 0, scale, ws, ws_bytes, stream);
-      if (D == 128)
-        return launch_decode_f32<128, true>(q, kc, vc, block_tables, context_lens, out, N, Hq, Hkv,
-                                            max_blocks_per_seq, 0, scale, ws, ws_bytes, stream);
-    }
     if (dtype == kDtypeBF16) { CA_DEC(BF16, 64, kKindPaged16) CA_DEC(BF16, 128, kKindPaged16) }
     if (dtype == kDtypeF16) { CA_DEC(F16, 64, kKindPaged16) CA_DEC(F16, 128, kKindPaged16) }
   } else {
@@ -1177,21 +1076,15 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,
                                int B, int Hq, int Hkv, int S, int D, float scale, void* ws,
                                size_t ws_bytes, hipStream_t stream) {
-#define CA_FD(TR, DD)                                                                        \
-  if (D == DD)                                                                               \
-    return launch_decode_t<TR, DD, kKindContig16>(q, k, v, nullptr, nullptr, 0, nullptr,     \
-                                                  nullptr, o, B, Hq, Hkv, 0, 0, S, scale, ws, \
-                                                  ws_bytes, stream);
+#define CA_FD(TR, DD) \
+  if (D == DD) return launch_contig_decode_t<TR, DD>(q, k, v, o, B, Hq, Hkv, S, scale, ws, ws_bytes, stream);
   if (dtype == kDtypeBF16) { CA_FD(BF16, 64) CA_FD(BF16, 128) }
   if (dtype == kDtypeF16) { CA_FD(F16, 64) CA_FD(F16, 128) }
 #undef CA_FD
   if (dtype == kDtypeF32) {
-    if (D == 64)
-      return launch_decode_f32<64, false>(q, k, v, nullptr, nullptr, o, B, Hq, Hkv, 0, S, scale,
-                                          ws, ws_bytes, stream);
-    if (D == 128)
-      return launch_decode_f32<128, false>(q, k, v, nullptr, nullptr, o, B, Hq, Hkv, 0, S, scale,
-                                           ws, ws_bytes, stream);
+    const F32DecodeArgs a{q, k, v, nullptr, nullptr, 0, nullptr, nullptr, o, B, Hq, Hkv, 0, 1, S,
+                          scale, ws, ws_bytes};
+    return launch_decode_f32<kSrcF32Contig>(D, a, stream);
   }
   return hipErrorInvalidValue;
 }

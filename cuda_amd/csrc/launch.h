@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace ca {
 
 // dtype codes; the same values as ca_dtype in include/cuda_llm_abi.h
@@ -46,16 +48,18 @@ hipError_t launch_flash_bwd_f32(const float* q, const float* k, const float* v, 
                                 bool causal, void* ws, hipStream_t stream);
 
 // Compute units of the current device (cached per device; 0 if unknown).
+// Safe for concurrent first calls: each slot is an atomic, and every thread
+// that finds it empty stores the same attribute value.
 inline int device_cus() {
-  static int cached[64];
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 // Workgroups of a prefill launch of n_qt query tiles per (b, h). A causal
@@ -71,22 +75,14 @@ inline long long prefill_grid(int B, int Hq, int n_qt, bool causal, int wg_per_c
   return *paired ? pairs : single;
 }
 
-// Split-K geometry of the decode kernels: pages of 16 tokens; one wave walks
-// one split of kPagesPerWave pages.
+// Split-K geometry of the decode kernels: pages of 16 tokens. The
+// workspace and the contiguous-cache kernel split at kPagesPerWave pages
+// (one page id per lane of a wave); the paged kernels split at a multiple of
+// it (decode.hip, DmaCfg), so the workspace sized for kPagesPerWave-page
+// splits covers them.
 constexpr int kDecodePage = 16;
-#ifndef CA_PAGES_PER_WAVE
-#define CA_PAGES_PER_WAVE 64
-#endif
-#ifndef CA_DECODE_WG_WAVES
-#define CA_DECODE_WG_WAVES 4
-#endif
-#ifndef CA_DECODE_DMA
-#define CA_DECODE_DMA 1
-#endif
-constexpr int kPagesPerWave = CA_PAGES_PER_WAVE;  // <= 64: one page id per lane
-constexpr bool kDecodeDma = CA_DECODE_DMA != 0;   // paged decode via HBM -> LDS loads
-constexpr int kDecodeWgWaves = CA_DECODE_WG_WAVES;  // independent waves per workgroup
-static_assert(kPagesPerWave % 2 == 0 && kPagesPerWave <= 64, "pages per wave");
+constexpr int kPagesPerWave = 64;
+constexpr int kDecodeWgWaves = 4;  // independent waves per workgroup (contiguous kernel)
 
 // Workspace for split-K partial results: [N][Hq][max_splits] x (D + 1) floats.
 size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens);

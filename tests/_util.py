@@ -85,9 +85,9 @@ def build_paged(lens, hq, hkv, d, dtype, device, fp8=False, per_block=True, pool
     return case
 
 
-def paged_oracle(case, seqs=None):
+def paged_oracle(case, seqs=None, dtype=np.float32):
     """Oracle output [len(seqs), Hq, D] for the selected sequences, copying
-    only their pages to the host."""
+    only their pages to the host (arithmetic in `dtype`)."""
     n = case["query"].shape[0]
     seqs = list(range(n)) if seqs is None else list(seqs)
     lens = case["context_lens"].cpu().numpy()
@@ -114,7 +114,7 @@ def paged_oracle(case, seqs=None):
         kc_np, vc_np, ks, vs = to_np(kc), to_np(vc), None, None
     q = to_np(case["query"])[seqs]
     return oracle.paged_decode(q, kc_np, vc_np, sub_tables, lens[seqs],
-                               k_scale=ks, v_scale=vs)
+                               k_scale=ks, v_scale=vs, dtype=dtype)
 
 
 def mx_inputs(b, h, s, d, device, seed=0):

@@ -173,11 +173,17 @@ def test_paged_rejects_bad_arguments():
     assert b"workspace" in L.load().ca_last_error()
     fp8 = [L.CA_BF16, P, P, P, None, None, 1, P, P, P, 2, 8, 2, 128, 4, 16, 10, 0.1, None, 0, None]
     assert _status("ca_fp8_paged_attention", *fp8) == L.CA_INVALID_ARGUMENT
-    # the FP8 cache entry point has no float32-query form (the reference's
-    # instantiations are half / bf16 only)
+    # float32 queries are accepted (the reference instantiates
+    # dispatch_fp8_paged_attention<float, float>, fp8_paged_attention_
+    # instantiations.cu:4): they reach the same argument checks
     fp8_f32 = list(fp8)
     fp8_f32[0] = L.CA_F32
-    assert _status("ca_fp8_paged_attention", *fp8_f32) == L.CA_UNSUPPORTED
+    assert _status("ca_fp8_paged_attention", *fp8_f32) == L.CA_INVALID_ARGUMENT
+    assert b"scale" in L.load().ca_last_error()
+    fp8_bad_dtype = list(fp8)
+    fp8_bad_dtype[0] = 7
+    assert _status("ca_fp8_paged_attention", *fp8_bad_dtype) == L.CA_INVALID_ARGUMENT
+    assert b"dtype" in L.load().ca_last_error()
 
 
 def test_mxfp8_rejects_bad_arguments():
@@ -209,3 +215,23 @@ def test_mx_scale_conversion():
     assert torch.equal(cuda_llm.mx_scales_to_e8m0(b.view(torch.float8_e8m0fnu)), b)
     with pytest.raises(RuntimeError, match="powers of two"):
         cuda_llm.mx_scales_to_e8m0(torch.full((2,), 3.0))
+
+
+def test_reference_module_name_imports():
+    """The reference's callers `import fused_online_softmax_cuda` (tests/
+    conftest.py:25, setup.py:128 there): the module exists and binds the
+    attention entry points of fused_softmax_binding.cpp:721-809 to this
+    build's functions; names outside the attention forward path raise
+    AttributeError (as in a reference build compiled without them)."""
+    import importlib
+    m = importlib.import_module("fused_online_softmax_cuda")
+    for name in ("flash_attention_forward", "flash_attention_v3_hopper", "fused_gqa_forward",
+                 "async_flash_decode", "paged_attention_forward", "fp8_paged_attention_forward",
+                 "fused_rope_flash_attention", "flash_attention_backward"):
+        assert getattr(m, name) is getattr(cuda_llm, name), name
+    for name in ("forward", "fused_mla_forward", "fused_llama_megablock", "no_such_thing"):
+        with pytest.raises(AttributeError):
+            getattr(m, name)
+    q = torch.randn(1, 2, 8, 64)
+    with pytest.raises(RuntimeError, match="Inputs must be on CUDA"):
+        m.flash_attention_forward(q, q, q)

@@ -1,12 +1,18 @@
-"""GPU tier: float32 inputs (prefill, flash_decode, paged decode) vs the oracle.
+"""GPU tier: float32 inputs (prefill, flash_decode, paged and FP8 paged
+decode) vs the oracle.
 
 The reference binding dispatches float32 for flash_attention / _v3_hopper /
-fused_gqa (fused_softmax_binding.cpp:77-81, 275-277), async_flash_decode and
-paged_attention (:142-146); its tests use fp16/bf16 only (tests/
-test_attention.py:13 there), so the grids below are its fp16/bf16 grids run in
-float32, plus split-K lengths, ragged S, the golden vectors and NaN bytes past
-a paged context's end. Tolerance: the reference's float32 tolerance
-(tests/_utils.py:23-27 there, 1e-4), here as max-abs 1e-4 and mean-abs 1e-5.
+fused_gqa (fused_softmax_binding.cpp:77-81, 275-277), async_flash_decode,
+paged_attention (:142-146) and fp8_paged_attention with float queries
+(:683-691, instantiated at fp8_paged_attention_instantiations.cu:4); its tests
+use fp16/bf16 only (tests/test_attention.py:13 there), so the grids below are
+its fp16/bf16 grids run in float32, plus split-K lengths, ragged S, the golden
+vectors, NaN bytes past a paged context's end and BASELINE config C1 (fp32
+causal B=2 H=8 S=1024 D=64, the workload of tests/_utils.py:48-53 there).
+Tolerance: the reference's float32 tolerance (tests/_utils.py:23-27 there,
+1e-4), here as max-abs 1e-4 and mean-abs 1e-5 against the float64 oracle (for
+FP8 caches: on the dequantised codes, so only fp32 arithmetic separates the
+two).
 """
 import os
 
@@ -131,3 +137,55 @@ def test_causal_paired_query_tiles_f32(dev, head_dim):
         ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
                                to_np(v[bi:bi + 1, kh:kh + 1]), is_causal=True, dtype=np.float64)
         assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_F32, name=f"head {bi},{hi}")
+
+
+def test_baseline_c1(dev):
+    """BASELINE configs[0] (C1): fp32 q, k, v ~ N(0,1) [2, 8, 1024, 64], causal,
+    scale 1/8, seeded, through cuda_llm.flash_attention."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    q, k, v = (torch.randn(2, 8, 1024, 64, device=dev, generator=g) for _ in range(3))
+    out = cuda_llm.flash_attention(q, k, v, is_causal=True)
+    torch.cuda.synchronize()
+    assert out.dtype == F32 and out.shape == q.shape
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=True, dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name="C1")
+    # causal row 0 attends to key 0 only: out = v[..., 0, :]
+    assert torch.allclose(out[:, :, 0], v[:, :, 0], atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("per_block", [False, True])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (32, 8), (40, 2)])
+def test_fp8_paged_f32_queries(dev, head_dim, per_block, hq, hkv):
+    """Float32 queries over e4m3 caches, per-head or per-(page, head) scales,
+    GQA, split-K lengths; float32 output."""
+    lens = [0, 1, 17, 300, 1024, 1025, 3000]
+    case = build_paged(lens, hq, hkv, head_dim, F32, dev, fp8=True, per_block=per_block, pool=700)
+    out = cuda_llm.fp8_paged_attention_forward(case["query"], case["key_cache"],
+                                               case["value_cache"], case["k_scale"],
+                                               case["v_scale"], case["block_tables"],
+                                               case["context_lens"])
+    torch.cuda.synchronize()
+    assert out.dtype == F32
+    assert_close(to_np(out), paged_oracle(case, dtype=np.float64), **TOL_F32,
+                 name=f"fp8 paged f32 {hq}/{hkv} per_block={per_block}")
+    assert torch.all(out[0] == 0)
+
+
+def test_fp8_paged_f32_nan_tail_does_not_leak(dev):
+    """e4m3 NaN codes (0x7f) past a sequence's length in its last page never
+    reach the output."""
+    lens = [37, 5, 2100]
+    case = build_paged(lens, 8, 2, 128, F32, dev, fp8=True, per_block=True)
+    ref = paged_oracle(case, dtype=np.float64)
+    for i, L in enumerate(lens):
+        blk = int(case["block_tables"][i, (L - 1) // 16])
+        case["key_cache"][blk, :, :, L % 16:] = 0x7F
+        case["value_cache"][blk, :, :, L % 16:] = 0x7F
+    out = cuda_llm.fp8_paged_attention_forward(case["query"], case["key_cache"],
+                                               case["value_cache"], case["k_scale"],
+                                               case["v_scale"], case["block_tables"],
+                                               case["context_lens"])
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref, **TOL_F32, name="fp8 paged f32 nan tail")

@@ -106,6 +106,22 @@ def test_attention_vs_torch_sdpa(causal, hq, hkv, s, d):
     np.testing.assert_allclose(out, ref.numpy(), atol=2e-5, rtol=0)
 
 
+def test_attention_c1_config():
+    """BASELINE configs[0] (C1): fp32 q, k, v ~ N(0,1) [2, 8, 1024, 64], causal,
+    scale 1/8 (tests/_utils.py:48-53 there). The fp32 oracle agrees with
+    torch's CPU SDPA and with itself in float64 at that size, and its causal
+    row 0 is v's row 0."""
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(2, 8, 1024, 64, generator=g) for _ in range(3))
+    out = oracle.attention(q.numpy(), k.numpy(), v.numpy(), is_causal=True)
+    assert out.dtype == np.float32 and out.shape == (2, 8, 1024, 64)
+    ref = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    np.testing.assert_allclose(out, ref.numpy(), atol=2e-5, rtol=0)
+    out64 = oracle.attention(q.numpy(), k.numpy(), v.numpy(), is_causal=True, dtype=np.float64)
+    np.testing.assert_allclose(out, out64, atol=1e-5, rtol=0)
+    np.testing.assert_array_equal(out[:, :, 0], v.numpy()[:, :, 0])
+
+
 def test_lse_vs_torch():
     g = torch.Generator().manual_seed(2)
     q = torch.randn(1, 2, 50, 64, generator=g)
