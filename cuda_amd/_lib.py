@@ -35,6 +35,7 @@ SIGNATURES = {
     "ca_flash_decode": (_I, [_I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),
     "ca_paged_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),
     "ca_fp8_paged_attention": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),
+    "ca_fp8_paged_attention_noalloc": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
     "ca_fused_microscaled_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P]),
     "ca_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "ca_last_error": (ctypes.c_char_p, []),

@@ -183,7 +183,8 @@ static ca_status paged_common_checks(const char* what, const void* query, const 
                                      const void* vc, const int32_t* bt, const int32_t* lens,
                                      void* out, int num_seqs, int hq, int hkv, int head_dim,
                                      int max_blocks, int page_size, int num_blocks,
-                                     void* workspace, size_t workspace_bytes) {
+                                     void* workspace, size_t workspace_bytes,
+                                     bool check_workspace = true) {
   ca_status st;
   if ((st = check_heads(hq, hkv, what)) != CA_OK) return st;
   if ((st = check_head_dim(head_dim, what)) != CA_OK) return st;
@@ -198,7 +199,7 @@ static ca_status paged_common_checks(const char* what, const void* query, const 
   if (!aligned16(query) || !aligned16(kc) || !aligned16(vc) || !aligned16(out))
     return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
   const size_t need = ca::decode_workspace_bytes(num_seqs, hq, head_dim, max_blocks * page_size);
-  if (workspace_bytes < need || (need && !workspace))
+  if (check_workspace && (workspace_bytes < need || (need && !workspace)))
     return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
                 workspace_bytes);
   return CA_OK;
@@ -253,6 +254,47 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
                                           num_kv_heads, head_dim, max_blocks_per_seq,
                                           num_blocks > 0 ? num_blocks : 1, softmax_scale,
                                           workspace, workspace_bytes, (hipStream_t)stream),
+                  what);
+}
+
+ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
+                                         const uint8_t* key_cache, const uint8_t* value_cache,
+                                         const float* k_scale, const float* v_scale,
+                                         int per_block_scales, const int32_t* block_tables,
+                                         const int32_t* context_lens, void* out, int num_seqs,
+                                         int num_q_heads, int num_kv_heads, int head_dim,
+                                         int max_blocks_per_seq, int page_size, int num_blocks,
+                                         float softmax_scale, void* stream) {
+  const char* what = "fp8_paged_attention_noalloc";
+  ca_status st;
+  if ((st = check_float_dtype(dtype, what)) != CA_OK) return st;
+  // the same checks as the workspace form, with no workspace required
+  if ((st = paged_common_checks(what, query, key_cache, value_cache, block_tables, context_lens,
+                                out, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                max_blocks_per_seq, page_size, num_blocks, nullptr, 0,
+                                false)) != CA_OK)
+    return st;
+  if (num_seqs == 0) return CA_OK;
+  if (!k_scale || !v_scale) return fail(CA_INVALID_ARGUMENT, "%s: null scale pointer", what);
+  const size_t need = ca::paged_decode_partials_bytes((int)dtype, 1, num_seqs, num_q_heads,
+                                                      head_dim, max_blocks_per_seq);
+  if (need > ca::kNoAllocScratchBytes)
+    return fail(CA_INVALID_ARGUMENT,
+                "%s: these sizes need %zu bytes of split partials, more than the %zu bytes of "
+                "the library's scratch (use ca_fp8_paged_attention with a workspace)",
+                what, need, ca::kNoAllocScratchBytes);
+  void* scratch = nullptr;
+  if (need > 0) {
+    const hipError_t e = ca::noalloc_scratch(&scratch);
+    if (e != hipSuccess)
+      return fail(CA_LAUNCH_FAILED, "%s: scratch lookup failed: %s", what, hipGetErrorString(e));
+  }
+  return from_hip(ca::launch_paged_decode((int)dtype, 1, query, key_cache, value_cache, k_scale,
+                                          v_scale, per_block_scales != 0, block_tables,
+                                          context_lens, out, num_seqs, num_q_heads,
+                                          num_kv_heads, head_dim, max_blocks_per_seq,
+                                          num_blocks > 0 ? num_blocks : 1, softmax_scale,
+                                          scratch, need, (hipStream_t)stream),
                   what);
 }
 

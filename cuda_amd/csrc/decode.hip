@@ -30,6 +30,8 @@
 // A sequence that fits one split writes its output directly; otherwise each
 // wave writes (o / l, log2-sum-exp) to the workspace and decode_merge_kernel
 // combines the splits.
+#include <mutex>
+
 #include "common.h"
 #include "launch.h"
 #include "lds_dma.h"
@@ -692,11 +694,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   for (int i = 0; i < PER; ++i) Tr::store(O, ((size_t)n * Hq + hq) * D + lane * PER + i, acc[i] * inv);
 }
 
-size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
-  const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  const int max_splits = (pages + kPagesPerWave - 1) / kPagesPerWave;
+// Bytes of split partials for max_splits splits per (sequence, query head):
+// [N][Hq][max_splits] x D floats of o / l, then [N][Hq][max_splits] floats
+// of log2-sum-exp; none when every context fits one split.
+static size_t split_partials_bytes(int N, int Hq, int D, int max_splits) {
   if (max_splits <= 1) return 0;
   return (size_t)N * Hq * max_splits * (size_t)(D + 1) * sizeof(float);
+}
+
+size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
+  const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
+  return split_partials_bytes(N, Hq, D, (pages + kPagesPerWave - 1) / kPagesPerWave);
 }
 
 template <typename Tr, int D, int KIND>
@@ -707,12 +715,12 @@ static hipError_t launch_paged_decode_t(const void* q, const void* kc, const voi
                                         float scale, void* ws, size_t ws_bytes,
                                         hipStream_t stream) {
   const int max_tokens = max_blocks * kDecodePage;
-  // splits of DmaCfg<KIND>::kPages pages; the workspace (sized for
-  // kPagesPerWave-page splits) covers them
+  // splits of DmaCfg<KIND>::kPages pages (the workspace the entry points
+  // require, sized for kPagesPerWave-page splits, covers them)
   const int max_splits = max(1, (max_blocks + DmaCfg<KIND>::kPages - 1) / DmaCfg<KIND>::kPages);
   const int Gq = Hq / Hkv;
   const int n_hc = (Gq + 15) / 16;
-  const size_t need = decode_workspace_bytes(N, Hq, D, max_tokens);
+  const size_t need = split_partials_bytes(N, Hq, D, max_splits);
   if (ws_bytes < need) return hipErrorInvalidValue;
   float* ws_o = (float*)ws;
   float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
@@ -1071,6 +1079,48 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
   }
 #undef CA_DEC
   return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch for the allocation-free FP8 paged decode entry point: the split-K
+// partials live in this file-scope device array instead of a caller
+// workspace. Each device holds its own copy (at its own address) from the
+// library's load until the process ends; every call on a device shares it,
+// so calls that overlap on one device race. Its contents need no clearing:
+// the merge reads only the partials its own launch wrote.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_dev[64];  // device -> device address of `scratch` there
+}  // namespace
+
+hipError_t noalloc_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    // host code names `scratch` only here: its device address comes from the
+    // runtime, once per device, with that device current
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    g_scratch_dev[dev] = p;
+  }
+  *ptr = g_scratch_dev[dev];
+  return hipSuccess;
+}
+
+size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int D,
+                                   int max_blocks_per_seq) {
+  const int pages_per_split = (dtype == kDtypeF32) ? kPagesPerWave
+                              : cache_kind == 0    ? DmaCfg<kKindPaged16>::kPages
+                                                   : DmaCfg<kKindPagedFp8>::kPages;
+  return split_partials_bytes(N, Hq, D, (max_blocks_per_seq + pages_per_split - 1) / pages_per_split);
 }
 
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,

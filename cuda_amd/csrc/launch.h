@@ -96,6 +96,18 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
                                int D, int max_blocks_per_seq, int num_blocks, float scale,
                                void* ws, size_t ws_bytes, hipStream_t stream);
 
+// Bytes of split partials a paged decode launch writes (the exact minimum
+// of its workspace; the entry points require decode_workspace_bytes, which
+// is at least this).
+size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int D,
+                                   int max_blocks_per_seq);
+
+// The allocation-free paged decode's scratch (decode.hip): a file-scope
+// device array of kNoAllocScratchBytes per device; *ptr receives its address
+// on the current device (looked up once per device).
+constexpr size_t kNoAllocScratchBytes = 16u << 20;
+hipError_t noalloc_scratch(void** ptr);
+
 // Contiguous-cache decode (q_len = 1 over k/v [B, Hkv, S, D]).
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,
                                int B, int Hq, int Hkv, int S, int D, float scale, void* ws,

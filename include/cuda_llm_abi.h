@@ -10,12 +10,17 @@
  *  - All tensor arguments are raw device pointers to contiguous row-major
  *    buffers in the layouts stated per function; 16-byte aligned.
  *  - The library never allocates, frees or retains caller memory. Split-K
- *    decode needs a caller-provided workspace of ca_decode_workspace_bytes().
+ *    decode needs a caller-provided workspace of ca_decode_workspace_bytes()
+ *    (ca_fp8_paged_attention_noalloc instead uses a fixed scratch array the
+ *    library holds per device).
  *  - `stream` is a hipStream_t (NULL = the default stream). Calls enqueue
  *    work asynchronously and never synchronise the host.
  *  - Non-OK status: ca_last_error() returns a thread-local message.
- *  - Element types: CA_BF16 and CA_F16 for 16-bit q/k/v/out. (CA_F32 is
- *    reserved and currently returns CA_UNSUPPORTED.)
+ *  - Element types: CA_BF16 and CA_F16 for 16-bit q/k/v/out everywhere;
+ *    CA_F32 for prefill (with and without LSE), backward, RoPE prefill,
+ *    flash_decode, paged and FP8 paged decode (the entry points the reference
+ *    instantiates for float). paged_kv_append takes CA_BF16 / CA_F16 only, and
+ *    MXFP8 writes CA_BF16 / CA_F16 outputs.
  *  - head_dim must be 64 or 128 (fused_softmax_binding.cpp:65-67); the MXFP8
  *    entry point requires 128.
  *  - GQA: num_q_heads % num_kv_heads == 0, kv head = q head / (Hq / Hkv)
@@ -173,6 +178,28 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
                                  int head_dim, int max_blocks_per_seq, int page_size,
                                  int num_blocks, float softmax_scale, void* workspace,
                                  size_t workspace_bytes, void* stream);
+
+/* FP8 paged decode that allocates nothing and takes no workspace: the
+ * arguments, checks and results of ca_fp8_paged_attention (the same kernels),
+ * with the split-K partials held in a scratch array of the library
+ * (CA_NOALLOC_SCRATCH_BYTES per device, kept from the library's load until
+ * the process ends). No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Sizes whose partials exceed the
+ * scratch, num_seqs * num_q_heads * splits * (head_dim + 1) * 4 bytes with
+ * splits = ceil(max_blocks_per_seq / 128) for fp16/bf16 queries and
+ * ceil(max_blocks_per_seq / 64) for float32 (none when that is 1), return
+ * CA_INVALID_ARGUMENT. Every call on a device shares that device's scratch:
+ * calls that overlap on one device (concurrent streams or threads) race. */
+#define CA_NOALLOC_SCRATCH_BYTES (16u << 20)
+ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
+                                         const uint8_t* key_cache, const uint8_t* value_cache,
+                                         const float* k_scale, const float* v_scale,
+                                         int per_block_scales, const int32_t* block_tables,
+                                         const int32_t* context_lens, void* out, int num_seqs,
+                                         int num_q_heads, int num_kv_heads, int head_dim,
+                                         int max_blocks_per_seq, int page_size, int num_blocks,
+                                         float softmax_scale, void* stream);
 
 /* MXFP8 attention: q, k, v are OCP e4m3 codes [batch, num_heads, seq_len,
  * head_dim] with one e8m0 scale byte per 32 elements along head_dim

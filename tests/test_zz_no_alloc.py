@@ -1,0 +1,70 @@
+"""GPU tier: ca_fp8_paged_attention_noalloc, the FP8 paged decode entry point
+that allocates nothing (split-K partials in the library's per-device scratch).
+
+Called through the C ABI and compared with ca_fp8_paged_attention (the
+workspace form, same kernels) bit for bit, on two calls in a row whose second
+is smaller (the scratch keeps the first call's partials), and with the oracle
+at the FP8 tolerance. No counterpart in the reference.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import cuda_amd._lib as L
+import cuda_llm
+from _util import TOL_FP8, assert_close, build_paged, paged_oracle, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _noalloc(case, scale=None):
+    q = case["query"]
+    n, hq, d = q.shape
+    kc = case["key_cache"]
+    per_block = case["k_scale"].dim() == 2
+    out = torch.empty_like(q)
+    dt = {torch.bfloat16: L.CA_BF16, torch.float16: L.CA_F16, torch.float32: L.CA_F32}[q.dtype]
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    L.call("ca_fp8_paged_attention_noalloc", dt, p(q), p(kc), p(case["value_cache"]),
+           p(case["k_scale"]), p(case["v_scale"]), int(per_block), p(case["block_tables"]),
+           p(case["context_lens"]), p(out), n, hq, kc.shape[1], d, case["block_tables"].shape[1],
+           16, kc.shape[0], 1.0 / d ** 0.5 if scale is None else scale,
+           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    return out
+
+
+def _with_workspace(case):
+    return cuda_llm.fp8_paged_attention_forward(case["query"], case["key_cache"],
+                                                case["value_cache"], case["k_scale"],
+                                                case["v_scale"], case["block_tables"],
+                                                case["context_lens"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_noalloc_matches_workspace_form_twice(dev, dtype):
+    # first call: 4 sequences, up to 5000 tokens (3 splits of 128 pages), GQA 32/8
+    big = build_paged([5000, 3000, 200, 0], 32, 8, 128, dtype, dev, fp8=True, per_block=True,
+                      pool=700, seed=1)
+    # second call: smaller (2 sequences, 2 splits, per-head scales), other data
+    small = build_paged([2100, 17], 8, 2, 128, dtype, dev, fp8=True, per_block=False, seed=2)
+    for case, name in ((big, "first"), (small, "second, smaller")):
+        out = _noalloc(case)
+        ref = _with_workspace(case)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"{name}: differs from ca_fp8_paged_attention"
+        tol = TOL_FP8 if dtype != torch.float32 else dict(max_abs=1e-4, mean_abs=1e-5)
+        assert_close(to_np(out), paged_oracle(case, dtype=np.float64), **tol, name=name)
+    assert torch.all(_noalloc(big)[3] == 0)  # empty context -> zero row
+
+
+def test_noalloc_rejects_sizes_beyond_scratch(dev):
+    case = build_paged([16], 32, 8, 128, torch.bfloat16, dev, fp8=True, per_block=True)
+    # a table 2048 blocks wide for 512 sequences needs 512*32*16*129*4 bytes of partials
+    q = torch.zeros(512, 32, 128, dtype=torch.bfloat16, device=dev)
+    tables = torch.zeros(512, 2048, dtype=torch.int32, device=dev)
+    lens = torch.zeros(512, dtype=torch.int32, device=dev)
+    big = dict(case, query=q, block_tables=tables, context_lens=lens)
+    with pytest.raises(RuntimeError, match="scratch"):
+        _noalloc(big)
