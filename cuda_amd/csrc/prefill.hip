@@ -10,7 +10,7 @@
 //   one workgroup = 8 waves = 256 query rows of one (b, h);
 //   each wave owns 32 query rows for the whole KV walk;
 //   KV tiles of 64 keys travel HBM -> LDS by buffer loads into a ring of 4
-//   tiles (one barrier per tile) shared by the 8 waves.
+//   tiles (one barrier per two tiles) shared by the 8 waves.
 // Per wave and KV tile (32x32x16 MFMAs):
 //   S^T[64 keys x 32 q] = K Q^T   (A = K rows from LDS, B = Q from registers)
 //   softmax over keys: keys live in the registers of a lane (16 per 32-key
@@ -75,7 +75,7 @@ __device__ __forceinline__ void rope_q(typename Tr::vec8 (&qv)[D / 16], RopeQ rq
 // One workgroup = 256 query rows of one (b, h) = 8 waves of 32 rows, two per
 // SIMD (waves w and w+4 share one). K/V tiles of 64 keys travel HBM -> LDS
 // with buffer loads into a ring of kStages tiles (every wave loads 1/8 of
-// every K and V tile; one barrier per tile). Tile layout: 64 rows x 2D bytes,
+// every K and V tile; one barrier per two tiles). Tile layout: 64 rows x 2D bytes,
 // unpadded; the 16-byte chunk c of row r is stored at position c ^ swz(r),
 // which makes both read patterns bank-conflict free:
 //   K, ds_read_b128: a 16-lane group reads one chunk of 16 consecutive rows
@@ -109,6 +109,10 @@ constexpr int kPfWaves = 8;    // waves per workgroup (32 query rows each)
 constexpr int kPfStages = 4;   // K/V tiles in the LDS ring (32 KB each at D = 128)
 constexpr int kPfKDepth = 1;   // K fragments read ahead of the QK MFMAs (k-steps)
 constexpr int kPfVDepth = 2;   // V^T fragments read ahead of the PV MFMAs (steps)
+// Key tiles per workgroup barrier: one barrier every two tiles lets a
+// SIMD's two waves drift apart within the pair instead of meeting after
+// every PV (C2 +1.5 % over one barrier per tile, same box).
+constexpr int kPfGroup = 2;
 // 24 wait states: longer than any MFMA-result -> VALU and VALU -> MFMA-operand
 // hazard of gfx950, so MFMAs issued before it have written their results.
 __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
@@ -193,6 +197,18 @@ __device__ CA_INLINE void prefill_dma_qtile(
       dma16_buf(k_rsrc, (CA_LDS void*)(kdst + 1024 * i), dma_off[i]);
       dma16_buf(v_rsrc, (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i]);
     }
+  };
+  // load j of tile tt alone (j < kDmaPerWave: K, else V), in the same order
+  // as issue()
+  constexpr int kLoads = 2 * kDmaPerWave;
+  auto issue_one = [&](int tt, int j) CA_INLINE {
+    unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
+    const uint32_t toff = (uint32_t)tt * kTileB;
+    const int i = j >> 1;
+    if ((j & 1) == 0)
+      dma16_buf(make_rsrc_at(Kp, toff, kv_bytes), (CA_LDS void*)(kdst + 1024 * i), dma_off[i]);
+    else
+      dma16_buf(make_rsrc_at(Vp, toff, kv_bytes), (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i]);
   };
 
   // LDS read addresses (bytes from the stage base).
@@ -316,6 +332,11 @@ __device__ CA_INLINE void prefill_dma_qtile(
   };
 
   // S^T(tn) = K(tn) Q^T, K fragments kPfKDepth k-steps ahead of the MFMAs
+  // The wave's loads of tile tn + kStages - kPfGroup (if past the first
+  // kStages tiles, which are issued up front) go out between its k-steps,
+  // one after every kNKS / kLoads of them: issued all at once after the
+  // barrier, the 8 waves' loads queue behind each other (C2 +1.8 %).
+  constexpr int kAhead = kStages - kPfGroup;
   auto qk = [&](int tn) CA_INLINE {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -345,6 +366,8 @@ __device__ CA_INLINE void prefill_dma_qtile(
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
       }
+      if (ks % (kNKS / kLoads) == kNKS / kLoads - 1 && tn + kAhead >= kStages)
+        issue_one(tn + kAhead, ks / (kNKS / kLoads));
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -388,45 +411,53 @@ __device__ CA_INLINE void prefill_dma_qtile(
 
   // ---- the tile walk ----------------------------------------------------------
   // Every wave walks all n_tiles tiles (it loads its share of each and meets
-  // the others at the per-tile barrier). Only a wave's last tile can need a
+  // the others at the barrier of every tile pair). Only a wave's last tile can need a
   // mask (bounds or causal diagonal); it is masked when taken out of the
   // accumulators. The wave's first tile takes the full row max, later tiles
   // the stale-max step.
   using T_ = std::true_type;
   using F_ = std::false_type;
-  constexpr int DIST = kStages - 1;  // tiles in flight ahead of the one waited for
 #pragma unroll
-  for (int tt = 0; tt < DIST; ++tt) issue(tt);
-  // Barrier t: every wave has its loads of tile t resident and is past its
-  // last read of tile t - 1, whose slot then takes tile t + DIST.
-  auto sync = [&](int t) CA_INLINE {
-    wait_vmcnt<2 * kDmaPerWave * (DIST - 1)>();  // this wave's loads of tile t landed
-    __builtin_amdgcn_s_barrier();                // ... and every wave's
-    issue(t + DIST);
+  for (int tt = 0; tt < kStages; ++tt) issue(tt);
+  // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
+  // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
+  // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead .. A
+  // wave that computes on tile t issues tile t + kAhead's loads inside qk(t);
+  // one that does not, in sync(t, true). Loads issued after the group's:
+  // kStages - kPfGroup tiles at t = 0 (the up-front ones), kStages -
+  // 2 kPfGroup after that.
+  auto sync = [&](int t, bool load_here) CA_INLINE {
+    if (t % kPfGroup == 0) {
+      // this wave's loads of the group landed ...
+      if (t == 0) wait_vmcnt<2 * kDmaPerWave * (kStages - kPfGroup)>();
+      else wait_vmcnt<2 * kDmaPerWave * (kStages - 2 * kPfGroup)>();
+      __builtin_amdgcn_s_barrier();  // ... and every wave's
+    }
+    if (load_here && t + kAhead >= kStages) issue(t + kAhead);
   };
   int t = 0;
   if (w_tiles > 1) {
-    sync(0);
+    sync(0, false);
     qk(0);
     first_softmax(0, F_{});
     pv(0);
     t = 1;
   }
   for (; t + 1 < w_tiles; ++t) {
-    sync(t);
+    sync(t, false);
     qk(t);
     stale_softmax(t, F_{});
     pv(t);
   }
   if (t + 1 == w_tiles) {  // the wave's last tile, masked
-    sync(t);
+    sync(t, false);
     qk(t);
     if (t == 0) first_softmax(t, T_{});
     else stale_softmax(t, T_{});
     pv(t);
     ++t;
   }
-  for (; t < n_tiles; ++t) sync(t);
+  for (; t < n_tiles; ++t) sync(t, true);
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
   acc_gap();
 
