@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(_HERE, "libcuda_llm_amd.so")
 
 CA_OK, CA_INVALID_ARGUMENT, CA_UNSUPPORTED, CA_LAUNCH_FAILED = 0, 1, 2, 3
 CA_F32, CA_F16, CA_BF16 = 0, 1, 2
+CA_SCALE_E8M0, CA_SCALE_F32 = 0, 1
 
 #: exported symbol -> (restype, argtypes); the single source of truth for the
 #: ABI surface, checked against include/cuda_llm_abi.h by the CPU tests.
@@ -36,7 +37,9 @@ SIGNATURES = {
     "ca_paged_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),
     "ca_fp8_paged_attention": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _Z, _P]),
     "ca_fp8_paged_attention_noalloc": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P]),
-    "ca_fused_microscaled_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P]),
+    "ca_fused_microscaled_attention": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _F,
+                                            _I, _P, _Z, _P]),
+    "ca_mx_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "ca_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "ca_last_error": (ctypes.c_char_p, []),
     "ca_version": (ctypes.c_char_p, []),

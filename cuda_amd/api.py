@@ -430,8 +430,11 @@ def fused_microscaled_attention(q_fp8, q_scale, k_fp8, k_scale, v_fp8, v_scale,
     """Attention over MXFP8 q/k/v (README.md:29-31,80-81; kernels_api.h:103-108).
 
     q/k/v: e4m3 codes (uint8 / int8 / float8_e4m3fn) [B, H, S, 128];
-    scales: one e8m0 per 32 elements along D, [B, H, S, 4] (uint8,
-    float8_e8m0fnu, or float powers of two). Output [B, H, S, 128] bf16/fp16.
+    scales: one per 32 elements along D, [B, H, S, 4]: e8m0 bytes (uint8 /
+    float8_e8m0fnu) or floating tensors holding powers of two (the
+    reference's float form; passed to the C ABI as float32, which rejects
+    anything else). Mixed forms are brought to e8m0 bytes here. Output
+    [B, H, S, 128] bf16/fp16.
     """
     for t in (q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale):
         _check(t.is_cuda, "Inputs must be on CUDA")
@@ -444,11 +447,18 @@ def fused_microscaled_attention(q_fp8, q_scale, k_fp8, k_scale, v_fp8, v_scale,
     for sc in (q_scale, k_scale, v_scale):
         _check(tuple(sc.shape) == (b, h, s, d // 32), "MX scales must be [B, H, S, head_dim/32]")
     _check(out_dtype in (torch.bfloat16, torch.float16), "out_dtype must be bfloat16 or float16")
-    qs, ks, vs = (mx_scales_to_e8m0(t).contiguous() for t in (q_scale, k_scale, v_scale))
+    scales = (q_scale, k_scale, v_scale)
+    if all(t.is_floating_point() and t.dtype != torch.float8_e8m0fnu for t in scales):
+        kind = _lib.CA_SCALE_F32
+        qs, ks, vs = (_aligned(t.to(torch.float32).contiguous()) for t in scales)
+    else:
+        kind = _lib.CA_SCALE_E8M0
+        qs, ks, vs = (mx_scales_to_e8m0(t).contiguous() for t in scales)
+        ks = _aligned(ks)
     q8, k8, v8 = (_aligned(t.contiguous()) for t in (q_fp8, k_fp8, v_fp8))
-    ks = _aligned(ks)
     out = torch.empty((b, h, s, d), dtype=out_dtype, device=q_fp8.device)
+    ws, nbytes = _workspace(int(_lib.load().ca_mx_workspace_bytes(kind, b, h, s, d)), q_fp8.device)
     _lib.call("ca_fused_microscaled_attention", _DT[out_dtype], _ptr(q8), _ptr(qs), _ptr(k8),
-              _ptr(ks), _ptr(v8), _ptr(vs), _ptr(out), b, h, s, d, _scale(softmax_scale, d),
-              int(bool(is_causal)), _stream())
+              _ptr(ks), _ptr(v8), _ptr(vs), kind, _ptr(out), b, h, s, d, _scale(softmax_scale, d),
+              int(bool(is_causal)), _ptr(ws), nbytes, _stream())
     return out

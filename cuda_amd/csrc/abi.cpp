@@ -298,16 +298,25 @@ ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
                   what);
 }
 
-ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
-                                         const uint8_t* q_scale, const uint8_t* k,
-                                         const uint8_t* k_scale, const uint8_t* v,
-                                         const uint8_t* v_scale, void* out, int batch,
-                                         int num_heads, int seq_len, int head_dim,
-                                         float softmax_scale, int is_causal, void* stream) {
+size_t ca_mx_workspace_bytes(ca_scale_kind scale_kind, int batch, int num_heads, int seq_len,
+                             int head_dim) {
+  if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim != 128) return 0;
+  if (scale_kind != CA_SCALE_E8M0 && scale_kind != CA_SCALE_F32) return 0;
+  return ca::mx_workspace_bytes((int)scale_kind, batch, num_heads, seq_len, head_dim);
+}
+
+ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, const void* q_scale,
+                                         const uint8_t* k, const void* k_scale, const uint8_t* v,
+                                         const void* v_scale, ca_scale_kind scale_kind, void* out,
+                                         int batch, int num_heads, int seq_len, int head_dim,
+                                         float softmax_scale, int is_causal, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
   const char* what = "fused_microscaled_attention";
   if (out_dtype != CA_BF16 && out_dtype != CA_F16)
     return fail(out_dtype == CA_F32 ? CA_UNSUPPORTED : CA_INVALID_ARGUMENT,
                 "%s: output dtype must be bf16 or fp16", what);
+  if (scale_kind != CA_SCALE_E8M0 && scale_kind != CA_SCALE_F32)
+    return fail(CA_INVALID_ARGUMENT, "%s: unknown scale kind %d", what, (int)scale_kind);
   if (head_dim != 128)
     return fail(CA_INVALID_ARGUMENT, "%s: head_dim must be 128 (got %d)", what, head_dim);
   if (batch < 0 || num_heads < 0 || seq_len < 0)
@@ -315,14 +324,32 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
   if (batch == 0 || num_heads == 0 || seq_len == 0) return CA_OK;
   if (!q || !k || !v || !q_scale || !k_scale || !v_scale || !out)
     return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-    return fail(CA_INVALID_ARGUMENT, "%s: code/output pointers must be 16-byte aligned", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || !aligned16(workspace))
+    return fail(CA_INVALID_ARGUMENT, "%s: code/output/workspace pointers must be 16-byte aligned",
+                what);
+  const uintptr_t scale_align = scale_kind == CA_SCALE_F32 ? 4u : 1u;
+  if ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(v_scale)) & (scale_align - 1))
+    return fail(CA_INVALID_ARGUMENT, "%s: float scales must be 4-byte aligned", what);
   if ((reinterpret_cast<uintptr_t>(k_scale) & 3u) != 0)
     return fail(CA_INVALID_ARGUMENT, "%s: k_scale must be 4-byte aligned", what);
-  return from_hip(ca::launch_mxfp8((int)out_dtype, q, q_scale, k, k_scale, v, v_scale, out, batch,
-                                   num_heads, seq_len, head_dim, softmax_scale, is_causal != 0,
-                                   (hipStream_t)stream),
-                  what);
+  if ((long long)batch * num_heads * seq_len * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  const size_t need = ca::mx_workspace_bytes((int)scale_kind, batch, num_heads, seq_len, head_dim);
+  if (workspace_bytes < need || !workspace)
+    return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
+                workspace_bytes);
+  bool bad_scales = false;
+  const ca_status st = from_hip(
+      ca::launch_mxfp8((int)out_dtype, (int)scale_kind, q, q_scale, k, k_scale, v, v_scale, out,
+                       batch, num_heads, seq_len, head_dim, softmax_scale, is_causal != 0, workspace,
+                       workspace_bytes, &bad_scales, (hipStream_t)stream),
+      what);
+  if (st != CA_OK) return st;
+  if (bad_scales)
+    return fail(CA_INVALID_ARGUMENT,
+                "%s: float MX scales must be powers of two in [2^-127, 2^127] (the e8m0 values)",
+                what);
+  return CA_OK;
 }
 
 size_t ca_rope_workspace_bytes(ca_dtype dtype, int batch, int num_q_heads, int num_kv_heads,

@@ -131,9 +131,21 @@ hipError_t launch_rope_prefill(int dtype, const void* q, const void* k, const vo
 // Streaming read of `bytes` (multiple of 16) for the bandwidth ceiling (stream_read.hip).
 hipError_t launch_stream_read(const void* p, size_t bytes, void* sink, hipStream_t stream);
 
-// MXFP8 attention: e4m3 q/k/v [B, H, S, D] with e8m0 scale bytes [B, H, S, D/32].
-hipError_t launch_mxfp8(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
-                        const uint8_t* ks, const uint8_t* v, const uint8_t* vs, void* o, int B,
-                        int H, int S, int D, float scale, bool causal, hipStream_t stream);
+// MXFP8 attention (mxfp8.hip): e4m3 q/k/v [B, H, S, D] with scales [B, H, S,
+// D/32], e8m0 bytes (scale_kind 0) or float32 powers of two (scale_kind 1);
+// ws holds mx_workspace_bytes (V dequantised to bf16; with float scales the
+// converted q/k scale bytes and a flag). A float scale that is not a power of
+// two in [2^-127, 2^127] sets *bad_scales (the launch then waits for that
+// check) and no attention kernel runs.
+size_t mx_workspace_bytes(int scale_kind, int B, int H, int S, int D);
+hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const void* qs,
+                        const uint8_t* k, const void* ks, const uint8_t* v, const void* vs, void* o,
+                        int B, int H, int S, int D, float scale, bool causal, void* ws,
+                        size_t ws_bytes, bool* bad_scales, hipStream_t stream);
+// The MX prefill kernel (prefill.hip): e4m3 q, k with e8m0 scale bytes
+// qs, ks ([B, H, S, 4]) and the bf16 dequantised v; D = 128.
+hipError_t launch_prefill_mx(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
+                             const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
+                             float scale, bool causal, hipStream_t stream);
 
 }  // namespace ca

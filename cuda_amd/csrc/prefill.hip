@@ -124,49 +124,101 @@ __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\
 // (s_setprio), so a wave's MFMAs win issue over its partner wave's softmax
 // VALU. On return every wave has waited for its own HBM -> LDS loads, but
 // other waves may still read the ring.
-template <typename Tr, int D, bool CAUSAL, bool POS>
+//
+// MX (MXFP8 attention, D = 128): Q and K are OCP e4m3 codes with one e8m0
+// scale byte per 32 elements along D (QS, KS: [rows][4]); V is its exact
+// bf16 dequantisation (written by mx_prepare_kernel), so PV and the softmax
+// are those of the bf16 kernel. QK contracts over D, the axis the MX blocks
+// run along, so it runs on v_mfma_scale_f32_32x32x64_f8f6f4: each MFMA covers
+// 64 d (two MX blocks) and takes one e8m0 byte per lane. Hardware k-block 0
+// of that instruction is bytes 0-15 of both lane halves and k-block 1 bytes
+// 16-31, with the scale of k-block b read from lane half b; so lane half h
+// supplies d = 64s + 16h + [0,16) in bytes 0-15 and d = 64s + 32 + 16h +
+// [0,16) in bytes 16-31 of k-step s, and the scale of MX block 2s + h. Both
+// operands (K rows from LDS, Q rows from registers) use that assignment, so
+// every fp8 product meets its own two scales. The K tile is 64 rows of 128
+// code bytes (the swizzle of 128-byte rows), followed in the ring stage by
+// the V tile and the tile's 64 scale words (4 bytes per key).
+template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
 __device__ CA_INLINE void prefill_dma_qtile(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int bh, int qt, int q_shift, RopeQ rq) {
-  using Gm = PfGeom<D>;
+    const void* __restrict__ Qv, const void* __restrict__ Kv, const uint8_t* __restrict__ QS,
+    const uint8_t* __restrict__ KS, const uint16_t* __restrict__ V, void* __restrict__ Ov,
+    float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh, int qt, int q_shift,
+    RopeQ rq) {
+  static_assert(!MX || (D == 128 && std::is_same<Tr, BF16>::value), "MX: D = 128, bf16 PV");
+  using Gv = PfGeom<D>;                   // V tile geometry (and K's for 16-bit K)
+  using Gk = PfGeom<MX ? 64 : D>;         // K tile geometry: 128-byte rows for MX codes
   using vec8 = typename Tr::vec8;
-  using vec4 = typename Tr::vec4;
-  using vec2 = typename Tr::vec2;
-  constexpr int kBN = Gm::kBN, kRowB = Gm::kRowB, kTileB = Gm::kTileB, kStageB = Gm::kStageB;
-  constexpr int kNKS = Gm::kNKS, kNOB = Gm::kNOB;
+  using ovec4 = typename OutTr::vec4;
+  using ovec2 = typename OutTr::vec2;
+  constexpr int kBN = Gv::kBN;
+  constexpr int kKRowB = Gk::kRowB, kVRowB = Gv::kRowB;       // bytes per K / V row in LDS
+  constexpr int kKTileB = kBN * kKRowB, kVTileB = kBN * kVRowB;
+  constexpr int kScaleB = MX ? kBN * 4 : 0;                   // K scale words of a tile
+  constexpr int kStageB = kKTileB + kVTileB + kScaleB;
+  constexpr int kNOB = Gv::kNOB;
   constexpr int kBM = kPfRows, kStages = kPfStages, kNW = kPfWaves;
-  constexpr int kDmaPerWave = kTileB / 1024 / kNW;  // 1 KB loads per wave per tile (K, and V)
-  static_assert(kDmaPerWave >= 1 && kTileB % (1024 * kNW) == 0, "tile loads");
+  constexpr int kKL = kKTileB / 1024 / kNW;  // 1 KB K loads per wave per tile
+  constexpr int kVL = kVTileB / 1024 / kNW;  // 1 KB V loads per wave per tile
+  constexpr int kSL = MX ? 1 : 0;            // scale loads (every wave loads the same 256 B)
+  constexpr int kLoads = kKL + kVL + kSL;
+  static_assert(kKL >= 1 && kVL >= 1 && kKTileB % (1024 * kNW) == 0 && kVTileB % (1024 * kNW) == 0,
+                "tile loads");
+  static_assert(kStageB % 256 == 0, "stage alignment (bank rows)");
+  // QK steps (MFMAs issued after one K fragment wait): bf16 k-steps of 16 d;
+  // MX (key block, k-step of 64 d) pairs
+  constexpr int kQkSteps = MX ? 4 : Gv::kNKS;
+  static_assert(kQkSteps % kLoads == 0, "loads spread over the QK steps");
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
 
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
   const int q0 = qt * kBM - q_shift;  // tile 0 may start before row 0 (rows < 0 are padding)
-  const uint16_t* Qp = Q + (size_t)(b * Hq + h) * S * D;
-  uint16_t* Op = O + (size_t)(b * Hq + h) * S * D;
-  const uint16_t* Kp = K + (size_t)(b * Hkv + hk) * S * D;
-  const uint16_t* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+  const size_t qhead = (size_t)(b * Hq + h) * S, khead = (size_t)(b * Hkv + hk) * S;
+  const unsigned char* Kp = (const unsigned char*)Kv + khead * kKRowB;
+  const uint16_t* Vp = V + khead * D;
+  const uint8_t* KSp = MX ? KS + khead * 4 : nullptr;
 
   const int lane = __builtin_amdgcn_workitem_id_x() & 63;
   const int wave = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_workitem_id_x() >> 6);
   const int l32 = lane & 31, hl = lane >> 5;
   const int qw0 = q0 + wave * 32;
   const int myq = qw0 + l32;
+  const bool q_in = myq >= 0 && myq < S;
 
   // Q as the B operand of S^T = K Q^T
-  vec8 qv[kNKS];
+  vec8 qv[MX ? 1 : Gv::kNKS];  // 16-bit Q, k-step ks: d = 16 ks + 8 hl + [0, 8)
+  i32x8 qx[2];                  // MX codes, k-step s (layout above)
+  int qsc[2];                   // MX scale bytes of blocks 2s + hl
+  if constexpr (MX) {
+    const uint8_t* Qr = (const uint8_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
 #pragma unroll
-  for (int ks = 0; ks < kNKS; ++ks) {
-    if (myq >= 0 && myq < S) {
-      qv[ks] = *(const vec8*)(Qp + (size_t)myq * D + 16 * ks + 8 * hl);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
+    for (int st = 0; st < 2; ++st) {
+      if (q_in) {
+        const u32x4 lo = *(const u32x4*)(Qr + 64 * st + 16 * hl);
+        const u32x4 hi = *(const u32x4*)(Qr + 64 * st + 32 + 16 * hl);
+        qx[st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                       (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        qsc[st] = QS[(qhead + myq) * 4 + 2 * st + hl];
+      } else {
+        qx[st] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+        qsc[st] = 127;
+      }
     }
+  } else {
+    const uint16_t* Qp = (const uint16_t*)Qv + qhead * D;
+#pragma unroll
+    for (int ks = 0; ks < Gv::kNKS; ++ks) {
+      if (q_in) {
+        qv[ks] = *(const vec8*)(Qp + (size_t)myq * D + 16 * ks + 8 * hl);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
+      }
+    }
+    if (rq.cos && q_in) rope_q<Tr, D>(qv, rq, myq, hl);
   }
-  if (rq.cos && myq >= 0 && myq < S) rope_q<Tr, D>(qv, rq, myq, hl);
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
   const int n_tiles = (kv_end + kBN - 1) / kBN;
@@ -176,57 +228,59 @@ __device__ CA_INLINE void prefill_dma_qtile(
 
   // HBM -> LDS with buffer loads over the keys this workgroup needs
   // ([0, kv_end) of the (b, kv head) slice; rows past it read as zero, so
-  // partial and trailing tiles need no clamp). Load i of this wave covers
-  // tile rows kRpk*(kDmaPerWave*wave + i) + lane/kLpr; the lane fetches the
-  // chunk that belongs at position lane % kLpr. Tile tt reads through
+  // partial and trailing tiles need no clamp). K load i of this wave covers
+  // tile rows kRpk*(kKL*wave + i) + lane/kLpr (likewise V); the lane fetches
+  // the chunk that belongs at position lane % kLpr. Tile tt reads through
   // resources that start at its first row.
-  const uint32_t kv_bytes = (uint32_t)kv_end * kRowB;
-  uint32_t dma_off[kDmaPerWave];
+  uint32_t k_off[kKL], v_off[kVL];
 #pragma unroll
-  for (int i = 0; i < kDmaPerWave; ++i) {
-    const int row = Gm::kRpk * (kDmaPerWave * wave + i) + lane / Gm::kLpr;
-    dma_off[i] = row * kRowB + 16 * ((lane % Gm::kLpr) ^ Gm::swz(row));
+  for (int i = 0; i < kKL; ++i) {
+    const int row = Gk::kRpk * (kKL * wave + i) + lane / Gk::kLpr;
+    k_off[i] = row * kKRowB + 16 * ((lane % Gk::kLpr) ^ Gk::swz(row));
   }
-  auto issue = [&](int tt) CA_INLINE {
-    unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
-    const uint32_t toff = (uint32_t)tt * kTileB;
-    const __amdgpu_buffer_rsrc_t k_rsrc = make_rsrc_at(Kp, toff, kv_bytes);
-    const __amdgpu_buffer_rsrc_t v_rsrc = make_rsrc_at(Vp, toff, kv_bytes);
 #pragma unroll
-    for (int i = 0; i < kDmaPerWave; ++i) {
-      dma16_buf(k_rsrc, (CA_LDS void*)(kdst + 1024 * i), dma_off[i]);
-      dma16_buf(v_rsrc, (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i]);
+  for (int i = 0; i < kVL; ++i) {
+    const int row = Gv::kRpk * (kVL * wave + i) + lane / Gv::kLpr;
+    v_off[i] = row * kVRowB + 16 * ((lane % Gv::kLpr) ^ Gv::swz(row));
+  }
+  // load j of tile tt: K loads, then V loads, then (MX) the scale words
+  auto issue_one = [&](int tt, int j) CA_INLINE {
+    unsigned char* st = lds + (tt % kStages) * kStageB;
+    if (j < kKL) {
+      dma16_buf(make_rsrc_at(Kp, (uint32_t)tt * kKTileB, (uint32_t)kv_end * kKRowB),
+                (CA_LDS void*)(st + 1024 * (kKL * wave + j)), k_off[j]);
+    } else if (j < kKL + kVL) {
+      const int i = j - kKL;
+      dma16_buf(make_rsrc_at(Vp, (uint32_t)tt * kVTileB, (uint32_t)kv_end * kVRowB),
+                (CA_LDS void*)(st + kKTileB + 1024 * (kVL * wave + i)), v_off[i]);
+    } else if constexpr (MX) {
+      dma4_buf(make_rsrc_at(KSp, (uint32_t)tt * kScaleB, (uint32_t)kv_end * 4),
+               (CA_LDS void*)(st + kKTileB + kVTileB), 4 * lane);
     }
   };
-  // load j of tile tt alone (j < kDmaPerWave: K, else V), in the same order
-  // as issue()
-  constexpr int kLoads = 2 * kDmaPerWave;
-  auto issue_one = [&](int tt, int j) CA_INLINE {
-    unsigned char* kdst = lds + (tt % kStages) * kStageB + wave * (kDmaPerWave * 1024);
-    const uint32_t toff = (uint32_t)tt * kTileB;
-    const int i = j >> 1;
-    if ((j & 1) == 0)
-      dma16_buf(make_rsrc_at(Kp, toff, kv_bytes), (CA_LDS void*)(kdst + 1024 * i), dma_off[i]);
-    else
-      dma16_buf(make_rsrc_at(Vp, toff, kv_bytes), (CA_LDS void*)(kdst + kTileB + 1024 * i), dma_off[i]);
+  auto issue = [&](int tt) CA_INLINE {
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) issue_one(tt, j);
   };
 
   // LDS read addresses (bytes from the stage base).
-  // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl.
+  // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl
+  // (MX: chunks 4s + hl and 4s + 2 + hl, i.e. "ks" = 2s and 2s + 1).
   const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
-  const int fk = Gm::swz(krow);
-  const uint32_t kofs = krow * kRowB + 32 * (fk >> 1) + 16 * (hl ^ (fk & 1));  // ^ 32*ks
+  const int fk = Gk::swz(krow);
+  const uint32_t kofs = krow * kKRowB + 32 * (fk >> 1) + 16 * (hl ^ (fk & 1));  // ^ 32*ks
   // V^T: tr16 source lane -> row tr_row (+4 for the second read), logical
   // chunk 4*ob + c0, byte 8*(s16 & 1) of it.
   const int g16 = lane >> 4, s16 = lane & 15;
   const int tr_row = 8 * (g16 >> 1) + (s16 >> 2);
   const int c0 = 2 * (g16 & 1) + ((s16 & 3) >> 1);
   // D = 128: swz(tr_row + 4) == swz(tr_row) + 1 (tr_row % 8 < 4)
-  const int fv = Gm::swz(tr_row);
-  const int fv2 = D == 128 ? fv + 1 : Gm::swz(tr_row + 4);
-  const uint32_t vofs1 = kTileB + tr_row * kRowB + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
+  const int fv = Gv::swz(tr_row);
+  const int fv2 = D == 128 ? fv + 1 : Gv::swz(tr_row + 4);
+  const uint32_t vofs1 = kKTileB + tr_row * kVRowB + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
   const uint32_t vofs2 =
-      kTileB + (tr_row + 4) * kRowB + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
+      kKTileB + (tr_row + 4) * kVRowB + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
+  const uint32_t sofs = kKTileB + kVTileB + 4 * krow;  // MX: the scale word of row krow
   const uint32_t lds0 = lds_off(lds);
   auto stage = [&](int tt) CA_INLINE { return lds0 + (uint32_t)((tt % kStages) * kStageB); };
 
@@ -242,17 +296,26 @@ __device__ CA_INLINE void prefill_dma_qtile(
   constexpr float kMaskVal = POS ? kNegInf : -kNegInf;  // raw logit whose scaled image is -inf
 
   // P for logit pair p (16 pairs: P^T k-step kk = p/4, logits 8kk + 2j, +1
-  // with j = p%4; sv[8kk + e] <-> P^T k-step kk); two partial row sums
+  // with j = p%4; sv[8kk + e] <-> P^T k-step kk); two partial row sums. MX
+  // sums the bf16-rounded weights that enter PV (one v_dot2 with ones per
+  // pair, exact in fp32), so the weights of a row sum to exactly 1: its
+  // wide-range data gives peaked rows, where normalising by the unrounded
+  // sum would leave the dominant key's rounding (2^-9 of |v|) in the output.
   float psum[2];
+  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
   auto exp_pair = [&](int p) CA_INLINE {
     const int kk = p >> 2, j = p & 3;
     const int i0 = 8 * kk + 2 * j;
     const float p0 = fast_exp2(__builtin_fmaf(sv[i0], scale_log2, -msub));
     const float p1 = fast_exp2(__builtin_fmaf(sv[i0 + 1], scale_log2, -msub));
-    const vec2 pk = Tr::pack2(p0, p1);
+    const typename Tr::vec2 pk = Tr::pack2(p0, p1);
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
-    psum[j & 1] += p0 + p1;
+    if constexpr (MX)
+      psum[j & 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), ones2,
+                                                    psum[j & 1], false);
+    else
+      psum[j & 1] += p0 + p1;
   };
   auto exp_all = [&]() CA_INLINE {
     psum[0] = psum[1] = 0.f;
@@ -331,10 +394,10 @@ __device__ CA_INLINE void prefill_dma_qtile(
     l_run += psum[0] + psum[1];
   };
 
-  // S^T(tn) = K(tn) Q^T, K fragments kPfKDepth k-steps ahead of the MFMAs
+  // S^T(tn) = K(tn) Q^T, K fragments kPfKDepth steps ahead of the MFMAs.
   // The wave's loads of tile tn + kStages - kPfGroup (if past the first
-  // kStages tiles, which are issued up front) go out between its k-steps,
-  // one after every kNKS / kLoads of them: issued all at once after the
+  // kStages tiles, which are issued up front) go out between its QK steps,
+  // one after every kQkSteps / kLoads of them: issued all at once after the
   // barrier, the 8 waves' loads queue behind each other (C2 +1.8 %).
   constexpr int kAhead = kStages - kPfGroup;
   auto qk = [&](int tn) CA_INLINE {
@@ -344,30 +407,58 @@ __device__ CA_INLINE void prefill_dma_qtile(
       for (int r = 0; r < 16; ++r) sacc[mb][r] = 0.f;
     __builtin_amdgcn_s_setprio(1);
     const uint32_t ka = stage(tn) + kofs;
+    uint32_t ksw[2] = {0u, 0u};  // MX: the scale words of the lane's two key rows
+    if constexpr (MX) {
+      ksw[0] = lds_read_b32<0>(stage(tn) + sofs);
+      ksw[1] = lds_read_b32<128>(stage(tn) + sofs);
+    }
     constexpr int KD = kPfKDepth;
     u32x4 kr[KD + 1][2];
-    auto kread = [&](int ks) CA_INLINE {
-      const uint32_t an = ka ^ (32 * ks);
-      kr[ks % (KD + 1)][0] = lds_read_b128<0>(an);
-      kr[ks % (KD + 1)][1] = lds_read_b128<32 * kRowB>(an);
+    // step st's K fragment: bf16, k-step st of both key blocks; MX, key
+    // block st % 2, k-step st / 2, both 16-byte pieces
+    auto kread = [&](int st) CA_INLINE {
+      if constexpr (MX) {
+        const int mb = st & 1, s2 = st >> 1;
+        const uint32_t an = ka + 32 * kKRowB * mb;
+        kr[st % (KD + 1)][0] = lds_read_b128<0>(an ^ (32 * (2 * s2)));
+        kr[st % (KD + 1)][1] = lds_read_b128<0>(an ^ (32 * (2 * s2 + 1)));
+      } else {
+        const uint32_t an = ka ^ (32 * st);
+        kr[st % (KD + 1)][0] = lds_read_b128<0>(an);
+        kr[st % (KD + 1)][1] = lds_read_b128<32 * kKRowB>(an);
+      }
     };
 #pragma unroll
-    for (int ks = 0; ks < KD; ++ks) kread(ks);
+    for (int st = 0; st < KD; ++st) kread(st);
 #pragma unroll
-    for (int ks = 0; ks < kNKS; ++ks) {
-      const int cb = ks % (KD + 1);
-      if (ks + KD < kNKS) kread(ks + KD);
-      wait_lgkm_n(2 * (KD < kNKS - 1 - ks ? KD : kNKS - 1 - ks));  // k-step ks landed
+    for (int st = 0; st < kQkSteps; ++st) {
+      const int cb = st % (KD + 1);
+      if (st + KD < kQkSteps) kread(st + KD);
+      wait_lgkm_n(2 * (KD < kQkSteps - 1 - st ? KD : kQkSteps - 1 - st));  // step st landed
       after_wait(kr[cb][0]);
       after_wait(kr[cb][1]);
+      if constexpr (MX) {
+        if (st == 0) {
+          after_wait(ksw[0]);
+          after_wait(ksw[1]);
+        }
+        const int mb = st & 1, s2 = st >> 1;
+        const i32x8 a = {(int)kr[cb][0][0], (int)kr[cb][0][1], (int)kr[cb][0][2], (int)kr[cb][0][3],
+                         (int)kr[cb][1][0], (int)kr[cb][1][1], (int)kr[cb][1][2], (int)kr[cb][1][3]};
+        const int ksc = (ksw[mb] >> (8 * (2 * s2 + hl))) & 0xff;
+        sacc[mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qx[s2], sacc[mb], 0, 0, 0,
+                                                                  ksc, 0, qsc[s2]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      } else {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb][mb]), qv[ks], sacc[mb]);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
+        for (int mb = 0; mb < 2; ++mb) {
+          sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb][mb]), qv[st], sacc[mb]);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
+        }
       }
-      if (ks % (kNKS / kLoads) == kNKS / kLoads - 1 && tn + kAhead >= kStages)
-        issue_one(tn + kAhead, ks / (kNKS / kLoads));
+      if (st % (kQkSteps / kLoads) == kQkSteps / kLoads - 1 && tn + kAhead >= kStages)
+        issue_one(tn + kAhead, st / (kQkSteps / kLoads));
       __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_setprio(0);
@@ -379,8 +470,8 @@ __device__ CA_INLINE void prefill_dma_qtile(
     const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
     constexpr int VD = kPfVDepth;
     u32x2 vr[VD + 1][2];
-    constexpr int NST = 4 * kNOB;    // steps: kNOB O^T blocks x 4 P^T k-steps
-    constexpr int kKK = 16 * kRowB;  // bytes per P^T k-step of V rows
+    constexpr int NST = 4 * kNOB;     // steps: kNOB O^T blocks x 4 P^T k-steps
+    constexpr int kKK = 16 * kVRowB;  // bytes per P^T k-step of V rows
     auto vread = [&](int st, int buf) CA_INLINE {
       const uint32_t x = 64 * (st >> 2);
       switch (st & 3) {
@@ -411,10 +502,10 @@ __device__ CA_INLINE void prefill_dma_qtile(
 
   // ---- the tile walk ----------------------------------------------------------
   // Every wave walks all n_tiles tiles (it loads its share of each and meets
-  // the others at the barrier of every tile pair). Only a wave's last tile can need a
-  // mask (bounds or causal diagonal); it is masked when taken out of the
-  // accumulators. The wave's first tile takes the full row max, later tiles
-  // the stale-max step.
+  // the others at the barrier of every tile pair). Only a wave's last tile
+  // can need a mask (bounds or causal diagonal); it is masked when taken out
+  // of the accumulators. The wave's first tile takes the full row max, later
+  // tiles the stale-max step.
   using T_ = std::true_type;
   using F_ = std::false_type;
 #pragma unroll
@@ -429,8 +520,8 @@ __device__ CA_INLINE void prefill_dma_qtile(
   auto sync = [&](int t, bool load_here) CA_INLINE {
     if (t % kPfGroup == 0) {
       // this wave's loads of the group landed ...
-      if (t == 0) wait_vmcnt<2 * kDmaPerWave * (kStages - kPfGroup)>();
-      else wait_vmcnt<2 * kDmaPerWave * (kStages - 2 * kPfGroup)>();
+      if (t == 0) wait_vmcnt<kLoads * (kStages - kPfGroup)>();
+      else wait_vmcnt<kLoads * (kStages - 2 * kPfGroup)>();
       __builtin_amdgcn_s_barrier();  // ... and every wave's
     }
     if (load_here && t + kAhead >= kStages) issue(t + kAhead);
@@ -463,29 +554,40 @@ __device__ CA_INLINE void prefill_dma_qtile(
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
-  if (Lse && hl == 0 && myq >= 0 && myq < S)
-    Lse[(size_t)(b * Hq + h) * S + myq] = row_lse(m_run, l_tot);
-  if (myq >= 0 && myq < S) {
+  if (Lse && hl == 0 && q_in) Lse[qhead + myq] = row_lse(m_run, l_tot);
+  if (q_in) {
+    uint16_t* Orow = (uint16_t*)Ov + (qhead + myq) * D;
 #pragma unroll
     for (int ob = 0; ob < kNOB; ++ob) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
         const int d = 32 * ob + 8 * a + 4 * hl;
-        const vec2 lo = Tr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
-        const vec2 hi = Tr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
-        vec4 w;
+        const ovec2 lo = OutTr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
+        const ovec2 hi = OutTr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
+        ovec4 w;
         w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
-        *(vec4*)(Op + (size_t)myq * D + d) = w;
+        *(ovec4*)(Orow + d) = w;
       }
     }
   }
 }
 
-template <typename Tr, int D, bool CAUSAL, bool POS>
+// Operands of a prefill launch: Q, K as 16-bit rows or (MX) e4m3 codes with
+// e8m0 scale bytes QS, KS; V 16-bit rows; O the output rows.
+struct PfArgs {
+  const void* q;
+  const void* k;
+  const uint8_t* qs;
+  const uint8_t* ks;
+  const uint16_t* v;
+  void* o;
+  float* lse;
+};
+
+template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
 __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
-    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ Lse, int S, int Hq,
-    int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired, int q_shift, RopeQ rq) {
+    PfArgs a, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired,
+    int q_shift, RopeQ rq) {
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
@@ -493,17 +595,17 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile refills the LDS ring: every wave must be done reading it
     if (pass) __builtin_amdgcn_s_barrier();
-    prefill_dma_qtile<Tr, D, CAUSAL, POS>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2,
-                                          pass ? wk.bh1 : wk.bh0, pass ? wk.qt1 : wk.qt0, q_shift, rq);
+    prefill_dma_qtile<Tr, OutTr, D, CAUSAL, POS, MX>(a.q, a.k, a.qs, a.ks, a.v, a.o, a.lse, S, Hq,
+                                                     Hkv, scale_log2, pass ? wk.bh1 : wk.bh0,
+                                                     pass ? wk.qt1 : wk.qt0, q_shift, rq);
   }
 }
 
-template <typename Tr, int D, bool CAUSAL>
-static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v, void* o, float* lse,
-                                     int B, int Hq, int Hkv, int S, float scale,
-                                     hipStream_t stream, RopeQ rq) {
+// Grid, ragged-S shift and launch of the prefill kernel (16-bit or MX).
+template <typename Tr, typename OutTr, int D, bool CAUSAL, bool MX>
+static hipError_t launch_prefill_kernel(const PfArgs& a, int B, int Hq, int Hkv, int S, float scale,
+                                        hipStream_t stream, RopeQ rq) {
   using Gm = PfGeom<D>;
-  static_assert(kPfStages * Gm::kStageB <= 160 * 1024, "LDS ring");
   const int n_qt = (S + kPfRows - 1) / kPfRows;
   // the padding rows of a ragged S go before row 0, in whole key tiles (so a
   // wave's causal diagonal still lies in one key tile): the partial tile is
@@ -516,17 +618,38 @@ static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v
   const float sl2 = scale * kLog2e;
   const dim3 block(64 * kPfWaves);
   if (sl2 >= 0.f) {
-    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, true>), dim3((unsigned)grid), block, 0,
-                       stream, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (uint16_t*)o, lse, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired, q_shift,
-                       rq);
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, true, MX>), dim3((unsigned)grid),
+                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired,
+                       q_shift, rq);
   } else {
-    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, false>), dim3((unsigned)grid), block, 0,
-                       stream, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                       (uint16_t*)o, lse, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired, q_shift,
-                       rq);
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, false, MX>), dim3((unsigned)grid),
+                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired,
+                       q_shift, rq);
   }
   return hipGetLastError();
+}
+
+template <typename Tr, int D, bool CAUSAL>
+static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v, void* o, float* lse,
+                                     int B, int Hq, int Hkv, int S, float scale,
+                                     hipStream_t stream, RopeQ rq) {
+  const PfArgs a{q, k, nullptr, nullptr, (const uint16_t*)v, o, lse};
+  return launch_prefill_kernel<Tr, Tr, D, CAUSAL, false>(a, B, Hq, Hkv, S, scale, stream, rq);
+}
+
+hipError_t launch_prefill_mx(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
+                             const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
+                             float scale, bool causal, hipStream_t stream) {
+  const PfArgs a{q, k, qs, ks, v_bf16, o, nullptr};
+#define CA_PF_MX(OUT)                                                                           \
+  return causal ? launch_prefill_kernel<BF16, OUT, 128, true, true>(a, B, H, H, S, scale, stream,  \
+                                                                    RopeQ{})                   \
+                : launch_prefill_kernel<BF16, OUT, 128, false, true>(a, B, H, H, S, scale, stream, \
+                                                                     RopeQ{});
+  if (out_dtype == kDtypeBF16) { CA_PF_MX(BF16) }
+  if (out_dtype == kDtypeF16) { CA_PF_MX(F16) }
+#undef CA_PF_MX
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,

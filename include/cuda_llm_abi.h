@@ -201,19 +201,35 @@ ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
                                          int max_blocks_per_seq, int page_size, int num_blocks,
                                          float softmax_scale, void* stream);
 
+/* Scale formats of the MXFP8 entry point: e8m0 bytes (the MX storage
+ * format, value 2^(byte - 127), 0xFF = NaN) or float32 powers of two (the
+ * reference's `const float*` form, kernels_api.h:103-108). */
+typedef enum { CA_SCALE_E8M0 = 0, CA_SCALE_F32 = 1 } ca_scale_kind;
+
 /* MXFP8 attention: q, k, v are OCP e4m3 codes [batch, num_heads, seq_len,
- * head_dim] with one e8m0 scale byte per 32 elements along head_dim
- * ([batch, num_heads, seq_len, head_dim / 32]); value = code * 2^(scale-127).
+ * head_dim] with one scale per 32 elements along head_dim ([batch, num_heads,
+ * seq_len, head_dim / 32], in scale_kind's format); value = code * scale.
  * Output [batch, num_heads, seq_len, head_dim] in out_dtype (CA_BF16 or
- * CA_F16). Replaces dispatch_fused_microscaled_attention<T_OUT>
- * (kernels_api.h:103-108), which takes the scales as float; e8m0 bytes are
- * the MX storage format (README.md:29-31). */
-ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q,
-                                         const uint8_t* q_scale, const uint8_t* k,
-                                         const uint8_t* k_scale, const uint8_t* v,
-                                         const uint8_t* v_scale, void* out, int batch,
-                                         int num_heads, int seq_len, int head_dim,
-                                         float softmax_scale, int is_causal, void* stream);
+ * CA_F16). head_dim must be 128. k_scale must be 4-byte aligned (with
+ * CA_SCALE_F32 so must q_scale and v_scale). Replaces
+ * dispatch_fused_microscaled_attention<T_OUT> (kernels_api.h:103-108).
+ * workspace: ca_mx_workspace_bytes(...) (v dequantised to bf16; with float
+ * scales also q's and k's converted scale bytes). With CA_SCALE_F32 a scale
+ * that is not a power of two in [2^-127, 2^127] returns CA_INVALID_ARGUMENT
+ * and no output is written; to report that, the float form waits for its
+ * scale check (the stream is synchronised once), while the e8m0 form is
+ * asynchronous like the other entry points. */
+ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, const void* q_scale,
+                                         const uint8_t* k, const void* k_scale, const uint8_t* v,
+                                         const void* v_scale, ca_scale_kind scale_kind, void* out,
+                                         int batch, int num_heads, int seq_len, int head_dim,
+                                         float softmax_scale, int is_causal, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+
+/* Bytes of the ca_fused_microscaled_attention workspace (0 for an invalid
+ * shape or scale kind). */
+size_t ca_mx_workspace_bytes(ca_scale_kind scale_kind, int batch, int num_heads, int seq_len,
+                             int head_dim);
 
 /* Bytes of workspace the decode entry points need (0 if none). max_tokens is
  * kv_len for ca_flash_decode and max_blocks_per_seq * page_size for the paged

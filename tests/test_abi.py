@@ -187,12 +187,28 @@ def test_paged_rejects_bad_arguments():
 
 
 def test_mxfp8_rejects_bad_arguments():
-    st = _status("ca_fused_microscaled_attention", L.CA_BF16, P, P, P, P, P, P, P, 1, 2, 64, 64,
-                 0.1, 1, None)
-    assert st == L.CA_INVALID_ARGUMENT
-    st = _status("ca_fused_microscaled_attention", L.CA_F32, P, P, P, P, P, P, P, 1, 2, 64, 128,
-                 0.1, 1, None)
-    assert st == L.CA_UNSUPPORTED
+    E8, F32 = L.CA_SCALE_E8M0, L.CA_SCALE_F32
+    ws = L.load().ca_mx_workspace_bytes(E8, 1, 2, 64, 128)
+    assert ws == 1 * 2 * 64 * 128 * 2  # the bf16 V
+    wsf = L.load().ca_mx_workspace_bytes(F32, 1, 2, 64, 128)
+    assert wsf == ws + 2 * 512 + 256   # + q/k scale bytes (256-aligned) + flag
+    assert L.load().ca_mx_workspace_bytes(E8, 1, 2, 64, 64) == 0
+    assert L.load().ca_mx_workspace_bytes(7, 1, 2, 64, 128) == 0
+
+    def mx(*over, **kw):
+        a = dict(dt=L.CA_BF16, kind=E8, d=128, ws=P, wsb=ws, ks=P)
+        a.update(kw)
+        return _status("ca_fused_microscaled_attention", a["dt"], P, P, P, a["ks"], P, P, a["kind"],
+                       P, 1, 2, 64, a["d"], 0.1, 1, a["ws"], a["wsb"], None)
+    assert mx(d=64) == L.CA_INVALID_ARGUMENT
+    assert mx(dt=L.CA_F32) == L.CA_UNSUPPORTED
+    assert mx(kind=5) == L.CA_INVALID_ARGUMENT
+    assert b"scale kind" in L.load().ca_last_error()
+    assert mx(wsb=ws - 1) == L.CA_INVALID_ARGUMENT
+    assert b"workspace" in L.load().ca_last_error()
+    assert mx(kind=F32) == L.CA_INVALID_ARGUMENT  # the float form needs the larger workspace
+    assert mx(ks=ctypes.c_void_p(18)) == L.CA_INVALID_ARGUMENT
+    assert b"aligned" in L.load().ca_last_error()
 
 
 def test_python_api_requires_device_tensors():

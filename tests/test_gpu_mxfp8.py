@@ -116,3 +116,51 @@ def test_baseline_c5_shape(dev):
         d = _ref(x, heads=(0, h))
         ref = oracle.attention(d["q"], d["k"], d["v"], is_causal=True)
         assert_close(to_np(out[:, h:h + 1]), ref, **TOL_FP8, name=f"C5 head {h}")
+
+
+def _abi_call(x, kind, scales, out, causal=True):
+    """ca_fused_microscaled_attention through ctypes with the given scale
+    tensors and scale kind; returns the status (no raise)."""
+    import ctypes
+    import cuda_amd._lib as L
+    b, h, s, d = x["q"].shape
+    ws = torch.empty(int(L.load().ca_mx_workspace_bytes(kind, b, h, s, d)), dtype=torch.uint8,
+                     device=x["q"].device)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    return L.load().ca_fused_microscaled_attention(
+        L.CA_BF16, p(x["q"]), p(scales[0]), p(x["k"]), p(scales[1]), p(x["v"]), p(scales[2]), kind,
+        p(out), b, h, s, d, 1.0 / d ** 0.5, int(causal), p(ws), ws.numel(),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
+def test_mx_float_scale_form_of_the_c_abi(dev):
+    """The reference's float-scale interface (kernels_api.h:103-108) at the C
+    ABI: float32 powers of two give the e8m0 form's output bit for bit; a
+    scale that is not such a power of two is rejected with
+    CA_INVALID_ARGUMENT before any attention kernel writes the output."""
+    import cuda_amd._lib as L
+    x = mx_inputs(2, 2, 300, 128, dev, seed=7)
+    e8 = [x[n + "_scale"].contiguous() for n in "qkv"]
+    f32 = [torch.ldexp(torch.ones_like(t, dtype=torch.float32), t.to(torch.int32) - 127) for t in e8]
+    a = torch.full_like(x["q"], 0, dtype=torch.bfloat16)
+    b = torch.full_like(a, 0)
+    assert _abi_call(x, L.CA_SCALE_E8M0, e8, a) == L.CA_OK
+    assert _abi_call(x, L.CA_SCALE_F32, f32, b) == L.CA_OK
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    d = _ref(x)
+    assert_close(to_np(b), oracle.attention(d["q"], d["k"], d["v"], is_causal=True), **TOL_FP8,
+                 name="float scales")
+    for bad, which in ((3.0, 0), (0.0, 1), (-0.5, 2), (float("nan"), 1), (0.75, 2)):
+        sc = [t.clone() for t in f32]
+        sc[which].view(-1)[123] = bad
+        out = torch.full_like(a, 7.0)
+        assert _abi_call(x, L.CA_SCALE_F32, sc, out) == L.CA_INVALID_ARGUMENT
+        assert b"powers of two" in L.load().ca_last_error()
+        torch.cuda.synchronize()
+        assert torch.all(out == 7.0), "no output is written for rejected scales"
+    # the smallest and largest e8m0 values are accepted in float form
+    sc = [t.clone() for t in f32]
+    sc[1].view(-1)[5] = 2.0 ** -127
+    sc[1].view(-1)[6] = 2.0 ** 127
+    assert _abi_call(x, L.CA_SCALE_F32, sc, torch.empty_like(a)) == L.CA_OK
