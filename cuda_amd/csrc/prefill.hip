@@ -591,6 +591,9 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
   const QTileWork wk =
       prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
   const int n_pass = wk.qt1 < 0 ? 1 : 2;
+  // A pair's long tile runs first: the pair workgroups of a head then start
+  // their walks together over the same keys and share their L2 lines
+  // (short tile first measured -1 % on C2, with 1.2x the HBM fetches).
 #pragma clang loop unroll(disable)
   for (int pass = 0; pass < n_pass; ++pass) {
     // the second tile refills the LDS ring: every wave must be done reading it
