@@ -41,6 +41,7 @@ SIGNATURES = {
                                             _I, _P, _Z, _P]),
     "ca_mx_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "ca_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
+    "ca_check_block_tables": (_I, [_P, _P, _I, _I, _I, _I, _P]),
     "ca_last_error": (ctypes.c_char_p, []),
     "ca_version": (ctypes.c_char_p, []),
 }

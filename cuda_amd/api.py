@@ -19,6 +19,7 @@ reference instantiates it).
 """
 import ctypes
 import math
+import os
 
 import torch
 
@@ -270,6 +271,16 @@ def _paged_checks(query, key_cache, value_cache, block_tables, context_lens):
     return n, hq, hkv, d
 
 
+def _debug_check_tables(block_tables, context_lens, num_blocks):
+    """With CUDA_LLM_CHECK_BLOCK_TABLES=1 in the environment, every paged call
+    first checks that the table entries its sequences use lie in the pool
+    (ca_check_block_tables, synchronous) and raises RuntimeError otherwise;
+    by default ids outside the pool are clamped by the kernels."""
+    if os.environ.get("CUDA_LLM_CHECK_BLOCK_TABLES", "0") not in ("", "0"):
+        _lib.call("ca_check_block_tables", _ptr(block_tables), _ptr(context_lens),
+                  block_tables.size(0), block_tables.size(1), num_blocks, 16, _stream())
+
+
 def paged_attention_forward(query, key_cache, value_cache, block_tables, context_lens,
                             softmax_scale=None):
     """vLLM-style paged decode (fused_softmax_binding.cpp:109-173).
@@ -283,6 +294,7 @@ def paged_attention_forward(query, key_cache, value_cache, block_tables, context
     dt = _dtype_code(query, "PagedAttention")
     query, key_cache, value_cache = (_aligned(t.contiguous()) for t in (query, key_cache, value_cache))
     block_tables, context_lens = block_tables.contiguous(), context_lens.contiguous()
+    _debug_check_tables(block_tables, context_lens, key_cache.size(0))
     out = torch.empty_like(query)
     max_blocks = block_tables.size(1)
     ws, nbytes = _workspace(_lib.load().ca_decode_workspace_bytes(n, hq, d, max_blocks * 16),
@@ -323,6 +335,7 @@ def fp8_paged_attention_forward(query, key_cache_fp8, value_cache_fp8, k_scale, 
     kc = _aligned(key_cache_fp8.contiguous())
     vc = _aligned(value_cache_fp8.contiguous())
     block_tables, context_lens = block_tables.contiguous(), context_lens.contiguous()
+    _debug_check_tables(block_tables, context_lens, num_blocks)
     out = torch.empty_like(query)
     max_blocks = block_tables.size(1)
     ws, nbytes = _workspace(_lib.load().ca_decode_workspace_bytes(n, hq, d, max_blocks * 16),

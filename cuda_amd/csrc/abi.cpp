@@ -11,6 +11,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <algorithm>
+#include <vector>
 
 #include "../../include/cuda_llm_abi.h"
 #include "launch.h"
@@ -390,6 +392,38 @@ ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const voi
                                           softmax_scale, is_causal != 0, workspace,
                                           (hipStream_t)stream),
                   what);
+}
+
+ca_status ca_check_block_tables(const int32_t* block_tables, const int32_t* context_lens,
+                                int num_seqs, int max_blocks_per_seq, int num_blocks,
+                                int page_size, void* stream) {
+  const char* what = "check_block_tables";
+  if (num_seqs < 0 || max_blocks_per_seq < 0 || num_blocks < 0 || page_size <= 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: negative size or page size", what);
+  if (num_seqs == 0) return CA_OK;
+  if (!context_lens || (max_blocks_per_seq > 0 && !block_tables))
+    return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  // the tables may still be being written on `stream`
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  std::vector<int32_t> lens((size_t)num_seqs), tab((size_t)num_seqs * max_blocks_per_seq);
+  if (e == hipSuccess)
+    e = hipMemcpy(lens.data(), context_lens, lens.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && !tab.empty())
+    e = hipMemcpy(tab.data(), block_tables, tab.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e != hipSuccess)
+    return fail(CA_LAUNCH_FAILED, "%s: copy failed: %s", what, hipGetErrorString(e));
+  for (int n = 0; n < num_seqs; ++n) {
+    const long long len = lens[n] < 0 ? 0 : lens[n];
+    const long long used = std::min<long long>((len + page_size - 1) / page_size, max_blocks_per_seq);
+    for (long long j = 0; j < used; ++j) {
+      const int32_t id = tab[(size_t)n * max_blocks_per_seq + j];
+      if (id < 0 || id >= num_blocks)
+        return fail(CA_INVALID_ARGUMENT,
+                    "%s: block_tables[%d][%lld] = %d is outside the pool [0, %d) (context length %lld)",
+                    what, n, j, (int)id, num_blocks, len);
+    }
+  }
+  return CA_OK;
 }
 
 ca_status ca_stream_read(const void* p, size_t bytes, void* sink, void* stream) {

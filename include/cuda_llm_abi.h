@@ -151,7 +151,8 @@ ca_status ca_flash_decode(ca_dtype dtype, const void* q, const void* k, const vo
  * [num_blocks, num_kv_heads, head_dim, page_size] (page axis innermost);
  * block_tables: int32 [num_seqs, max_blocks_per_seq]; context_lens: int32
  * [num_seqs]. page_size must be 16. A sequence with context_len <= 0 gets a
- * zero output row. Block ids outside [0, num_blocks) are clamped.
+ * zero output row. Block ids outside [0, num_blocks) are clamped
+ * (ca_check_block_tables reports them).
  * Replaces dispatch_paged_attention<T> (kernels_api.h:35-41).
  * workspace: ca_decode_workspace_bytes(num_seqs, num_q_heads, head_dim,
  * max_blocks_per_seq * page_size). */
@@ -230,6 +231,18 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, c
  * shape or scale kind). */
 size_t ca_mx_workspace_bytes(ca_scale_kind scale_kind, int batch, int num_heads, int seq_len,
                              int head_dim);
+
+/* Debug check of a paged-cache block table (no counterpart in the reference,
+ * which reads through the table unchecked, paged_attention_kernel.cuh:69):
+ * returns CA_INVALID_ARGUMENT, naming the first offender, if an entry that a
+ * sequence uses (index < ceil(context_lens[n] / page_size), within the
+ * table's width) lies outside [0, num_blocks). The paged decode entry points
+ * clamp such ids instead, so a corrupt table gives plausible but wrong
+ * output; callers that want the error run this first. Synchronous: it waits
+ * for `stream` and copies the table and lengths to the host. */
+ca_status ca_check_block_tables(const int32_t* block_tables, const int32_t* context_lens,
+                                int num_seqs, int max_blocks_per_seq, int num_blocks,
+                                int page_size, void* stream);
 
 /* Bytes of workspace the decode entry points need (0 if none). max_tokens is
  * kv_len for ca_flash_decode and max_blocks_per_seq * page_size for the paged

@@ -251,3 +251,12 @@ def test_reference_module_name_imports():
     q = torch.randn(1, 2, 8, 64)
     with pytest.raises(RuntimeError, match="Inputs must be on CUDA"):
         m.flash_attention_forward(q, q, q)
+
+
+def test_check_block_tables_argument_checks():
+    """ca_check_block_tables rejects bad sizes before touching device memory."""
+    assert _status("ca_check_block_tables", P, P, -1, 4, 10, 16, None) == L.CA_INVALID_ARGUMENT
+    assert _status("ca_check_block_tables", P, P, 2, 4, 10, 0, None) == L.CA_INVALID_ARGUMENT
+    assert _status("ca_check_block_tables", None, None, 2, 4, 10, 16, None) == L.CA_INVALID_ARGUMENT
+    assert b"null" in L.load().ca_last_error()
+    assert _status("ca_check_block_tables", None, None, 0, 4, 10, 16, None) == L.CA_OK

@@ -186,3 +186,30 @@ def test_stream_read_measurement_kernel(dev, nbytes):
               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     torch.cuda.synchronize()
     assert torch.equal(x, keep)
+
+
+def test_block_table_debug_check(dev, monkeypatch):
+    """An id outside the pool in a used table entry: clamped by default (no
+    error); with CUDA_LLM_CHECK_BLOCK_TABLES=1 the paged entry points raise,
+    naming the entry. Unused entries past a sequence's pages are ignored."""
+    case = build_paged([40, 300], 8, 2, 128, torch.bfloat16, dev, pool=64)
+    nb = case["key_cache"].shape[0]
+    case["block_tables"][0, 2] = nb + 5          # used: 40 tokens -> pages 0..2
+    case["block_tables"][0, 10] = -7             # unused entry: never checked
+    args = (case["query"], case["key_cache"], case["value_cache"], case["block_tables"],
+            case["context_lens"])
+    monkeypatch.delenv("CUDA_LLM_CHECK_BLOCK_TABLES", raising=False)
+    out = cuda_llm.paged_attention_forward(*args)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    monkeypatch.setenv("CUDA_LLM_CHECK_BLOCK_TABLES", "1")
+    with pytest.raises(RuntimeError, match=r"block_tables\[0\]\[2\]"):
+        cuda_llm.paged_attention_forward(*args)
+    f8 = build_paged([40, 300], 8, 2, 128, torch.bfloat16, dev, fp8=True, pool=64)
+    f8["block_tables"][1, 18] = -1               # 300 tokens -> pages 0..18
+    with pytest.raises(RuntimeError, match=r"block_tables\[1\]\[18\]"):
+        cuda_llm.fp8_paged_attention_forward(f8["query"], f8["key_cache"], f8["value_cache"],
+                                             f8["k_scale"], f8["v_scale"], f8["block_tables"],
+                                             f8["context_lens"])
+    case["block_tables"][0, 2] = 3               # repaired: passes the check
+    cuda_llm.paged_attention_forward(*args)
