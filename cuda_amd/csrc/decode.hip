@@ -349,6 +349,8 @@ void decode_split_kernel(
 // once per launch, so it is streamed rather than retained.
 template <int KIND>
 struct DmaCfg {
+  // (rings of 3 / 2 fp8 steps or 2 16-bit steps, which let more waves share
+  // a CU, measured within +-1 % on C4 / C3)
   static constexpr int kRing = KIND == kKindPagedFp8 ? 4 : 3;
   static constexpr int kPages = KIND == kKindPagedFp8 ? 128 : kPagesPerWave;
   // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
