@@ -166,6 +166,11 @@ def _gen(seed=0):
 # ---------------------------------------------------------------------------
 # workloads: each returns dict(ms, value, unit, bound, peak, state...)
 # ---------------------------------------------------------------------------
+# --no-cold: skip the cold-cache timing (profiling runs, whose summaries take
+# the last `steps` dispatches of each kernel as the timed ones)
+SKIP_COLD = False
+
+
 def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
     import torch
     import cuda_llm
@@ -173,13 +178,14 @@ def w_prefill(steps, warmup, causal=True, B=4, H=32, S=4096, D=128):
     q, k, v = (torch.randn(B, H, S, D, device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
     fn = lambda: cuda_llm.flash_attention(q, k, v, is_causal=causal)
     ms = time_steps(fn, steps, warmup, "prefill" if causal else "prefill_nc")
-    cold = time_cold(fn)
     flops = (2.0 if causal else 4.0) * B * H * S * S * D
     tf = flops / (ms * 1e-3) / 1e12
+    cold = None if SKIP_COLD else time_cold(fn)
     return dict(ms=ms, value=tf, unit="TFLOP/s", bound="mfma", peak=PEAK_BF16_TFLOPS,
                 work=flops, qkv=(q, k, v), causal=causal,
-                cold={"ms_per_step": round(cold, 4), "value": round(flops / (cold * 1e-3) / 1e12, 2),
-                      "note": "median of 20 single calls, each after a pass over a 1 GiB buffer"},
+                cold=None if cold is None else
+                {"ms_per_step": round(cold, 4), "value": round(flops / (cold * 1e-3) / 1e12, 2),
+                 "note": "median of 20 single calls, each after a pass over a 1 GiB buffer"},
                 config={"workload": f"C2{'' if causal else chr(39)} bf16 {'causal' if causal else 'non-causal'} prefill (flash_attention)",
                         "batch": B, "heads": H, "seq_len": S, "head_dim": D, "causal": causal})
 
@@ -557,7 +563,7 @@ WORKLOADS = {
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
                "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5",
-               "backward": ("backward_c2_dkv", "backward_c2_dq")}
+               "backward": ("backward_c2_dkv", "backward_c2_dq"), "c1": "prefill_c1_f32"}
 
 
 def summary(name, r, read_gbs=None):
@@ -569,7 +575,7 @@ def summary(name, r, read_gbs=None):
            "roofline": {"bound": r["bound"], "achieved": round(r["value"], 2), "peak": r["peak"],
                         "unit": r["unit"], "frac": round(r["value"] / r["peak"], 4),
                         "traffic": _traffic(TRAFFIC_KEY.get(name, name))}}
-    if "cold" in r:
+    if r.get("cold"):
         out["cold"] = r["cold"]
     if name in WARM_LOG:
         out["warmup_run"] = WARM_LOG[name]
@@ -583,6 +589,61 @@ def summary(name, r, read_gbs=None):
     return out
 
 
+# ---------------------------------------------------------------------------
+# profile summaries (rocprofv3 CSV output of a bench.py run -> text)
+# ---------------------------------------------------------------------------
+def _kernel_short_name(name):
+    """'void ca::foo<...>(args)' -> 'ca::foo<...>'."""
+    n = name[5:] if name.startswith("void ") else name
+    n = n.replace("(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            return n[:i]
+    return n
+
+
+def trace_summary(path, last):
+    """Per-kernel durations from a rocprofv3 --kernel-trace CSV over the last
+    `last` dispatches of each of this library's kernels: in a bench.py run of
+    one workload with --no-cold those are the timed launches (the warm-up
+    launches come first), so the averages are comparable with the run's
+    ms_per_step. Prints one markdown table."""
+    import csv
+    by = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = _kernel_short_name(r["Kernel_Name"])
+            if name.startswith("ca::"):
+                by.setdefault(name, []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    print("| kernel | dispatches | timed (last) | avg µs | median µs | min µs | max µs |")
+    print("|---|---|---|---|---|---|---|")
+    for name, ts in sorted(by.items(), key=lambda kv: kv[1][0][0]):
+        ts.sort()
+        d = sorted((e - s) / 1e3 for s, e in ts[-last:])
+        print(f"| `{name}` | {len(ts)} | {len(d)} | {sum(d) / len(d):.1f} | {d[len(d) // 2]:.1f} | "
+              f"{d[0]:.1f} | {d[-1]:.1f} |")
+
+
+def pmc_summary(path):
+    """Per-kernel averages of every counter of a rocprofv3 --pmc CSV (this
+    library's kernels only), printed as one JSON object."""
+    import csv
+    acc = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = _kernel_short_name(r["Kernel_Name"])
+            if name.startswith("ca::") or "copyBuffer" in name:
+                c = acc.setdefault(name, {}).setdefault(r["Counter_Name"], [0.0, 0])
+                c[0] += float(r["Counter_Value"])
+                c[1] += 1
+    print(json.dumps({k: {c: v[0] / v[1] for c, v in d.items()} for k, d in acc.items()}, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser(description="attention forward hot path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -593,7 +654,22 @@ def main():
     ap.add_argument("--workload", default="all", choices=["all"] + list(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cold", action="store_true",
+                    help="skip the cold-cache prefill timing (profiling runs)")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarise a rocprofv3 kernel-trace CSV over each kernel's last --steps "
+                         "dispatches (no GPU needed)")
+    ap.add_argument("--pmc-summary", metavar="CSV",
+                    help="average a rocprofv3 --pmc CSV per kernel (no GPU needed)")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps)
+        return
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
+    global SKIP_COLD
+    SKIP_COLD = args.no_cold
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
               "requested). Run with --gpus 1.", file=sys.stderr)
