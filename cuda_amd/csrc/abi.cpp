@@ -68,6 +68,17 @@ ca_status check_head_dim(int d, const char* what) {
               what, d);
 }
 
+// Total elements and one (batch, head) slice: the kernels address a slice
+// with 32-bit byte offsets, so its float32 size stays below 2 GiB.
+ca_status check_sizes(int batch, int heads, int seq_len, int head_dim, const char* what) {
+  if ((long long)batch * heads * seq_len * head_dim > (1LL << 40))
+    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  if ((long long)seq_len * head_dim * 4 >= (1LL << 31))
+    return fail(CA_INVALID_ARGUMENT, "%s: seq_len too long (one head's slice must stay below 2 GiB)",
+                what);
+  return CA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -94,8 +105,7 @@ static ca_status prefill_entry(const char* what, ca_dtype dtype, const void* q, 
   if (!q || !k || !v || !o) return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
-  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
-    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  if ((st = check_sizes(batch, num_q_heads, seq_len, head_dim, what)) != CA_OK) return st;
   return from_hip(ca::launch_prefill((int)dtype, q, k, v, o, lse, batch, num_q_heads,
                                      num_kv_heads, seq_len, head_dim, softmax_scale,
                                      is_causal != 0, (hipStream_t)stream),
@@ -143,8 +153,7 @@ ca_status ca_flash_attention_bwd(ca_dtype dtype, const void* q, const void* k, c
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* p : ptrs)
     if (!aligned16(p)) return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
-  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
-    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  if ((st = check_sizes(batch, num_q_heads, seq_len, head_dim, what)) != CA_OK) return st;
   const size_t need = ca::bwd_workspace_bytes(batch, num_q_heads, seq_len);
   if (workspace_bytes < need || !workspace)
     return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
@@ -334,14 +343,14 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, c
     return fail(CA_INVALID_ARGUMENT, "%s: float scales must be 4-byte aligned", what);
   if ((reinterpret_cast<uintptr_t>(k_scale) & 3u) != 0)
     return fail(CA_INVALID_ARGUMENT, "%s: k_scale must be 4-byte aligned", what);
-  if ((long long)batch * num_heads * seq_len * head_dim > (1LL << 40))
-    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  ca_status st;
+  if ((st = check_sizes(batch, num_heads, seq_len, head_dim, what)) != CA_OK) return st;
   const size_t need = ca::mx_workspace_bytes((int)scale_kind, batch, num_heads, seq_len, head_dim);
   if (workspace_bytes < need || !workspace)
     return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
                 workspace_bytes);
   bool bad_scales = false;
-  const ca_status st = from_hip(
+  st = from_hip(
       ca::launch_mxfp8((int)out_dtype, (int)scale_kind, q, q_scale, k, k_scale, v, v_scale, out,
                        batch, num_heads, seq_len, head_dim, softmax_scale, is_causal != 0, workspace,
                        workspace_bytes, &bad_scales, (hipStream_t)stream),
@@ -380,8 +389,7 @@ ca_status ca_fused_rope_flash_attention(ca_dtype dtype, const void* q, const voi
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(workspace) ||
       !aligned16(cos_tab) || !aligned16(sin_tab))
     return fail(CA_INVALID_ARGUMENT, "%s: pointers must be 16-byte aligned", what);
-  if ((long long)batch * num_q_heads * seq_len * head_dim > (1LL << 40))
-    return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
+  if ((st = check_sizes(batch, num_q_heads, seq_len, head_dim, what)) != CA_OK) return st;
   const size_t need = ca::rope_workspace_bytes((int)dtype, batch, num_q_heads, num_kv_heads,
                                                seq_len, head_dim);
   if (workspace_bytes < need || !workspace)

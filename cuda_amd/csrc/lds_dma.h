@@ -122,12 +122,17 @@ __device__ __forceinline__ void dma4_buf(__amdgpu_buffer_rsrc_t rsrc, CA_LDS voi
 // Resource over bytes [off, size) of `base` (none when off >= size): a tile
 // walk moves the resource rather than the per-lane offsets, which costs
 // scalar instructions only. The arguments are wave-uniform; readfirstlane
-// says so to the compiler, which would otherwise compute the clamped size in
-// a vector register and wrap every load in a loop over distinct resources.
+// on the inputs says so to the compiler, which then computes the clamped
+// size with scalar instructions (clamping after the readfirstlane instead
+// costs a saturating vector subtract, a readfirstlane and its wait states
+// per load) and does not wrap the load in a loop over distinct resources.
+// Sizes are below 2^31 bytes (one (b, head) slice).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_at(const void* base, uint32_t off,
                                                                uint32_t size) {
-  const uint32_t left = __builtin_amdgcn_readfirstlane(size > off ? size - off : 0u);
-  return make_rsrc((const char*)base + off, left);
+  const int o = __builtin_amdgcn_readfirstlane((int)off);
+  const int s = __builtin_amdgcn_readfirstlane((int)size);
+  const int left = s > o ? s - o : 0;
+  return make_rsrc((const char*)base + o, (uint32_t)left);
 }
 
 // Orders later uses of `x` after the preceding wait (the asm "rewrites" it).

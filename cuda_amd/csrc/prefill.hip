@@ -311,14 +311,14 @@ __device__ CA_INLINE void prefill_dma_qtile(
     const typename Tr::vec2 pk = Tr::pack2(p0, p1);
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
+    // pairs 0 and 1 start the two chains (an add of 0.f is not folded away)
     if constexpr (MX)
       psum[j & 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), ones2,
-                                                    psum[j & 1], false);
+                                                    p < 2 ? 0.f : psum[j & 1], false);
     else
-      psum[j & 1] += p0 + p1;
+      psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
   };
   auto exp_all = [&]() CA_INLINE {
-    psum[0] = psum[1] = 0.f;
 #pragma unroll
     for (int p = 0; p < 16; ++p) exp_pair(p);
   };
@@ -395,10 +395,10 @@ __device__ CA_INLINE void prefill_dma_qtile(
   };
 
   // S^T(tn) = K(tn) Q^T, K fragments kPfKDepth steps ahead of the MFMAs.
-  // The wave's loads of tile tn + kStages - kPfGroup (if past the first
-  // kStages tiles, which are issued up front) go out between its QK steps,
-  // one after every kQkSteps / kLoads of them: issued all at once after the
-  // barrier, the 8 waves' loads queue behind each other (C2 +1.8 %).
+  // The wave's loads of tile tn + kStages - kPfGroup go out between its QK
+  // steps, one after every kQkSteps / kLoads of them: issued all at once
+  // after the barrier, the 8 waves' loads queue behind each other (C2
+  // +1.8 %).
   constexpr int kAhead = kStages - kPfGroup;
   auto qk = [&](int tn) CA_INLINE {
 #pragma unroll
@@ -457,7 +457,7 @@ __device__ CA_INLINE void prefill_dma_qtile(
           __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
         }
       }
-      if (st % (kQkSteps / kLoads) == kQkSteps / kLoads - 1 && tn + kAhead >= kStages)
+      if (st % (kQkSteps / kLoads) == kQkSteps / kLoads - 1)
         issue_one(tn + kAhead, st / (kQkSteps / kLoads));
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -508,23 +508,24 @@ __device__ CA_INLINE void prefill_dma_qtile(
   // tiles the stale-max step.
   using T_ = std::true_type;
   using F_ = std::false_type;
+  // Tiles 0 .. kAhead - 1 go out up front; tile t + kAhead with tile t: a
+  // wave that computes on tile t issues its loads inside qk(t), one that
+  // does not in sync(t, true), so the steady-state walk has no condition on
+  // them. Tiles past the walk's end (short walks) read zeros into their
+  // slots without a memory access.
 #pragma unroll
-  for (int tt = 0; tt < kStages; ++tt) issue(tt);
+  for (int tt = 0; tt < kAhead; ++tt) issue(tt);
   // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
   // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
-  // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead .. A
-  // wave that computes on tile t issues tile t + kAhead's loads inside qk(t);
-  // one that does not, in sync(t, true). Loads issued after the group's:
-  // kStages - kPfGroup tiles at t = 0 (the up-front ones), kStages -
-  // 2 kPfGroup after that.
+  // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
+  // The wave has issued tiles up to t + kAhead - 1 by then, so the loads of
+  // kAhead - kPfGroup tiles may still be in flight.
   auto sync = [&](int t, bool load_here) CA_INLINE {
     if (t % kPfGroup == 0) {
-      // this wave's loads of the group landed ...
-      if (t == 0) wait_vmcnt<kLoads * (kStages - kPfGroup)>();
-      else wait_vmcnt<kLoads * (kStages - 2 * kPfGroup)>();
-      __builtin_amdgcn_s_barrier();  // ... and every wave's
+      wait_vmcnt<kLoads * (kAhead - kPfGroup)>();  // this wave's loads of the group landed ...
+      __builtin_amdgcn_s_barrier();                // ... and every wave's
     }
-    if (load_here && t + kAhead >= kStages) issue(t + kAhead);
+    if (load_here) issue(t + kAhead);
   };
   int t = 0;
   if (w_tiles > 1) {
