@@ -113,6 +113,12 @@ constexpr int kPfVDepth = 2;   // V^T fragments read ahead of the PV MFMAs (step
 // SIMD's two waves drift apart within the pair instead of meeting after
 // every PV (C2 +1.5 % over one barrier per tile, same box).
 constexpr int kPfGroup = 2;
+// Ping-pong walk: tile t + kPpAhead is loaded with tile t (its slot held
+// tile t - 2, released by the barrier of tile t).
+constexpr int kPpAhead = 2;
+#ifndef CA_PF_DOT2
+#define CA_PF_DOT2 0
+#endif
 // 24 wait states: longer than any MFMA-result -> VALU and VALU -> MFMA-operand
 // hazard of gfx950, so MFMAs issued before it have written their results.
 __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
@@ -168,6 +174,10 @@ __device__ CA_INLINE void prefill_dma_qtile(
   // QK steps (MFMAs issued after one K fragment wait): bf16 k-steps of 16 d;
   // MX (key block, k-step of 64 d) pairs
   constexpr int kQkSteps = MX ? 4 : Gv::kNKS;
+  // The ping-pong walk (below) for 16-bit head dim 128: same-box C2 +6.6 %,
+  // C2' +4.9 %; at head dim 64 (-5 to -7 %) and MX (-5 %) the MFMA blocks
+  // are too short to hide the partner's softmax and the lockstep walk stays.
+  constexpr bool kPingPong = D == 128 && !MX;
   static_assert(kQkSteps % kLoads == 0, "loads spread over the QK steps");
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
@@ -302,7 +312,6 @@ __device__ CA_INLINE void prefill_dma_qtile(
   // wide-range data gives peaked rows, where normalising by the unrounded
   // sum would leave the dominant key's rounding (2^-9 of |v|) in the output.
   float psum[2];
-  const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
   auto exp_pair = [&](int p) CA_INLINE {
     const int kk = p >> 2, j = p & 3;
     const int i0 = 8 * kk + 2 * j;
@@ -312,9 +321,8 @@ __device__ CA_INLINE void prefill_dma_qtile(
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
     // pairs 0 and 1 start the two chains (an add of 0.f is not folded away)
-    if constexpr (MX)
-      psum[j & 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), ones2,
-                                                    p < 2 ? 0.f : psum[j & 1], false);
+    if constexpr (MX || CA_PF_DOT2)
+      psum[j & 1] = Tr::sum2(pk, p < 2 ? 0.f : psum[j & 1]);
     else
       psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
   };
@@ -500,6 +508,102 @@ __device__ CA_INLINE void prefill_dma_qtile(
     __builtin_amdgcn_s_setprio(0);
   };
 
+  // ---- MFMA block M(s) = PV(s-1) then QK(s) --------------------------------
+  // One MFMA per step: PV steps (O^T block i / 4, P^T k-step i % 4; V^T
+  // fragment = two tr16 reads) then QK steps (key block j % 2, k-step j / 2;
+  // K fragment = one b128 read, two for MX). Fragments stream kMD steps
+  // ahead across the PV -> QK boundary, so a wave keeps the matrix pipe fed
+  // on its own while its partner runs the softmax. The loads of tile s +
+  // kAhead go out between the QK steps.
+  constexpr int kNPV = 4 * kNOB;
+  constexpr int kNQK = MX ? 4 : 2 * Gv::kNKS;
+  constexpr int kRQK = MX ? 2 : 1;  // LDS reads per QK step
+  constexpr int kMD = 4;            // steps read ahead
+  static_assert(kNQK % kLoads == 0, "loads spread over the QK steps");
+  constexpr int kKK = 16 * kVRowB;  // bytes per P^T k-step of V rows
+  auto mblock = [&](int s, auto pv_tag, auto qk_tag) CA_INLINE {
+    constexpr bool DPV = decltype(pv_tag)::value, DQK = decltype(qk_tag)::value;
+    constexpr int NPV = DPV ? kNPV : 0, N = NPV + (DQK ? kNQK : 0);
+    __builtin_amdgcn_s_setprio(1);
+    const uint32_t va1 = stage(s + kStages - 1) + vofs1, va2 = stage(s + kStages - 1) + vofs2;
+    const uint32_t ka = stage(s) + kofs;
+    uint32_t ksw[2] = {0u, 0u};  // MX: the scale words of the lane's two key rows
+    if constexpr (MX && DQK) {
+      ksw[0] = lds_read_b32<0>(stage(s) + sofs);
+      ksw[1] = lds_read_b32<128>(stage(s) + sofs);
+    }
+    if constexpr (DQK) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[mb][r] = 0.f;
+    }
+    u32x4 fr[kMD + 1][kRQK];
+    auto nreads = [&](int i) CA_INLINE { return i < NPV ? 2 : kRQK; };
+    auto fread = [&](int i) CA_INLINE {
+      const int b = i % (kMD + 1);
+      if (i < NPV) {
+        const uint32_t x = 64 * (i >> 2);
+        u32x2 a, c;
+        switch (i & 3) {
+          case 0: a = lds_read_tr16<0>(va1 ^ x); c = lds_read_tr16<0>(va2 ^ x); break;
+          case 1: a = lds_read_tr16<kKK>(va1 ^ x); c = lds_read_tr16<kKK>(va2 ^ x); break;
+          case 2: a = lds_read_tr16<2 * kKK>(va1 ^ x); c = lds_read_tr16<2 * kKK>(va2 ^ x); break;
+          default: a = lds_read_tr16<3 * kKK>(va1 ^ x); c = lds_read_tr16<3 * kKK>(va2 ^ x); break;
+        }
+        fr[b][0] = u32x4{a[0], a[1], c[0], c[1]};
+      } else {
+        const int j = i - NPV, mb = j & 1, ks = j >> 1;
+        if constexpr (MX) {
+          const uint32_t an = ka + 32 * kKRowB * mb;
+          fr[b][0] = lds_read_b128<0>(an ^ (32 * (2 * ks)));
+          fr[b][kRQK - 1] = lds_read_b128<0>(an ^ (32 * (2 * ks + 1)));
+        } else if (mb == 0) {
+          fr[b][0] = lds_read_b128<0>(ka ^ (32 * ks));
+        } else {
+          fr[b][0] = lds_read_b128<32 * kKRowB>(ka ^ (32 * ks));
+        }
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < kMD && i < N; ++i) fread(i);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int b = i % (kMD + 1);
+      if (i + kMD < N) fread(i + kMD);
+      int pending = 0;  // reads issued after step i's
+#pragma unroll
+      for (int k = i + 1; k <= i + kMD && k < N; ++k) pending += nreads(k);
+      wait_lgkm_n(pending);
+#pragma unroll
+      for (int r = 0; r < kRQK; ++r) after_wait(fr[b][r]);
+      if (i < NPV) {
+        const int ob = i >> 2, kk = i & 3;
+        o[ob] = Tr::mfma32(__builtin_bit_cast(vec8, fr[b][0]), pb[kk], o[ob]);
+      } else {
+        const int j = i - NPV, mb = j & 1, ks = j >> 1;
+        if constexpr (MX) {
+          if (j == 0) {
+            after_wait(ksw[0]);
+            after_wait(ksw[1]);
+          }
+          const i32x8 a = {(int)fr[b][0][0], (int)fr[b][0][1], (int)fr[b][0][2], (int)fr[b][0][3],
+                           (int)fr[b][kRQK - 1][0], (int)fr[b][kRQK - 1][1],
+                           (int)fr[b][kRQK - 1][2], (int)fr[b][kRQK - 1][3]};
+          const int ksc = (ksw[mb] >> (8 * (2 * ks + hl))) & 0xff;
+          sacc[mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qx[ks], sacc[mb], 0, 0, 0,
+                                                                    ksc, 0, qsc[ks]);
+        } else {
+          sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, fr[b][0]), qv[ks], sacc[mb]);
+        }
+        if (j % (kNQK / kLoads) == kNQK / kLoads - 1) issue_one(s + kPpAhead, j / (kNQK / kLoads));
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
   // ---- the tile walk ----------------------------------------------------------
   // Every wave walks all n_tiles tiles (it loads its share of each and meets
   // the others at the barrier of every tile pair). Only a wave's last tile
@@ -508,48 +612,112 @@ __device__ CA_INLINE void prefill_dma_qtile(
   // tiles the stale-max step.
   using T_ = std::true_type;
   using F_ = std::false_type;
-  // Tiles 0 .. kAhead - 1 go out up front; tile t + kAhead with tile t: a
-  // wave that computes on tile t issues its loads inside qk(t), one that
-  // does not in sync(t, true), so the steady-state walk has no condition on
-  // them. Tiles past the walk's end (short walks) read zeros into their
-  // slots without a memory access.
+  if constexpr (kPingPong) {
+    // Ping-pong walk. Each wave alternates its MFMA block M(s) and its softmax
+    // V(s); the waves of a SIMD (w and w + 4) run half a tile apart, so one
+    // wave's softmax runs under the other's MFMAs: waves 0-3 meet the barrier
+    // of tile t before M(t), waves 4-7 right after M(t - 1). Barrier t (every
+    // tile): every wave has tile t resident (its own loads waited on, the
+    // others' by the barrier) and is past its last read of tile t - 2 (PV(t -
+    // 2) is in M(t - 1), before either placement), whose slot takes tile t +
+    // 2, issued in M(t) or, for a wave with no QK(t), right after it. Before
+    // every barrier a wave has issued tiles up to t + 1, so one tile's loads
+    // may still be in flight.
+    const bool lead = wave < 4;
+    auto bar = [&](int t) CA_INLINE {
+      if (t < n_tiles) {
+        wait_vmcnt<kLoads>();
+        __builtin_amdgcn_s_barrier();
+      }
+    };
 #pragma unroll
-  for (int tt = 0; tt < kAhead; ++tt) issue(tt);
-  // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
-  // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
-  // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
-  // The wave has issued tiles up to t + kAhead - 1 by then, so the loads of
-  // kAhead - kPfGroup tiles may still be in flight.
-  auto sync = [&](int t, bool load_here) CA_INLINE {
-    if (t % kPfGroup == 0) {
-      wait_vmcnt<kLoads * (kAhead - kPfGroup)>();  // this wave's loads of the group landed ...
-      __builtin_amdgcn_s_barrier();                // ... and every wave's
+    for (int tt = 0; tt < kPpAhead; ++tt) issue(tt);
+    if (!lead) bar(0);
+    int s = 0;
+    if (w_tiles > 0) {
+      // tile 0: QK only, the full row max
+      if (lead) bar(0);
+      mblock(0, F_{}, T_{});
+      if (!lead) bar(1);
+      if (w_tiles > 1) first_softmax(0, F_{});
+      else first_softmax(0, T_{});
+      // steady tiles: PV(s - 1) + QK(s), the stale-max softmax
+      for (s = 1; s + 1 < w_tiles; ++s) {
+        if (lead) bar(s);
+        mblock(s, T_{}, T_{});
+        if (!lead) bar(s + 1);
+        stale_softmax(s, F_{});
+      }
+      if (s < w_tiles) {  // the wave's last tile, masked
+        if (lead) bar(s);
+        mblock(s, T_{}, T_{});
+        if (!lead) bar(s + 1);
+        stale_softmax(s, T_{});
+        ++s;
+      }
+      // PV of the last tile
+      if (lead) bar(s);
+      mblock(s, T_{}, F_{});
+      if (s < n_tiles) issue(s + kPpAhead);
+      if (!lead) bar(s + 1);
+    } else {
+      if (lead) bar(0);
+      issue(kPpAhead);
+      if (!lead) bar(1);
     }
-    if (load_here) issue(t + kAhead);
-  };
-  int t = 0;
-  if (w_tiles > 1) {
-    sync(0, false);
-    qk(0);
-    first_softmax(0, F_{});
-    pv(0);
-    t = 1;
+    int t = s + 1;  // w_tiles + 1: the walk met barriers 0 .. w_tiles (lead) or 0 .. w_tiles + 1
+    if (!lead) {
+      if (t < n_tiles) issue(t + kPpAhead);
+      ++t;
+    }
+    for (; t < n_tiles; ++t) {
+      bar(t);
+      issue(t + kPpAhead);
+    }
+  } else {
+    // Tiles 0 .. kAhead - 1 go out up front; tile t + kAhead with tile t: a
+    // wave that computes on tile t issues its loads inside qk(t), one that
+    // does not in sync(t, true), so the steady-state walk has no condition on
+    // them. Tiles past the walk's end (short walks) read zeros into their
+    // slots without a memory access.
+#pragma unroll
+    for (int tt = 0; tt < kAhead; ++tt) issue(tt);
+    // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
+    // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
+    // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
+    // The wave has issued tiles up to t + kAhead - 1 by then, so the loads of
+    // kAhead - kPfGroup tiles may still be in flight.
+    auto sync = [&](int t, bool load_here) CA_INLINE {
+      if (t % kPfGroup == 0) {
+        wait_vmcnt<kLoads * (kAhead - kPfGroup)>();  // this wave's loads of the group landed ...
+        __builtin_amdgcn_s_barrier();                // ... and every wave's
+      }
+      if (load_here) issue(t + kAhead);
+    };
+    int t = 0;
+    if (w_tiles > 1) {
+      sync(0, false);
+      qk(0);
+      first_softmax(0, F_{});
+      pv(0);
+      t = 1;
+    }
+    for (; t + 1 < w_tiles; ++t) {
+      sync(t, false);
+      qk(t);
+      stale_softmax(t, F_{});
+      pv(t);
+    }
+    if (t + 1 == w_tiles) {  // the wave's last tile, masked
+      sync(t, false);
+      qk(t);
+      if (t == 0) first_softmax(t, T_{});
+      else stale_softmax(t, T_{});
+      pv(t);
+      ++t;
+    }
+    for (; t < n_tiles; ++t) sync(t, true);
   }
-  for (; t + 1 < w_tiles; ++t) {
-    sync(t, false);
-    qk(t);
-    stale_softmax(t, F_{});
-    pv(t);
-  }
-  if (t + 1 == w_tiles) {  // the wave's last tile, masked
-    sync(t, false);
-    qk(t);
-    if (t == 0) first_softmax(t, T_{});
-    else stale_softmax(t, T_{});
-    pv(t);
-    ++t;
-  }
-  for (; t < n_tiles; ++t) sync(t, true);
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
   acc_gap();
 
