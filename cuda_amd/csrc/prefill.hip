@@ -201,34 +201,34 @@ __device__ CA_INLINE void prefill_dma_qtile(
   vec8 qv[MX ? 1 : Gv::kNKS];  // 16-bit Q, k-step ks: d = 16 ks + 8 hl + [0, 8)
   i32x8 qx[2];                  // MX codes, k-step s (layout above)
   int qsc[2];                   // MX scale bytes of blocks 2s + hl
-  if constexpr (MX) {
-    const uint8_t* Qr = (const uint8_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
+  // Issued after the first K/V tiles' loads, so that their latencies overlap.
+  // Rows outside [0, S) load row 0 and are zeroed.
+  auto load_q = [&]() CA_INLINE {
+    if constexpr (MX) {
+      const uint8_t* Qr = (const uint8_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      if (q_in) {
+      for (int st = 0; st < 2; ++st) {
         const u32x4 lo = *(const u32x4*)(Qr + 64 * st + 16 * hl);
         const u32x4 hi = *(const u32x4*)(Qr + 64 * st + 32 + 16 * hl);
+        const int sc = QS[(qhead + (q_in ? myq : 0)) * 4 + 2 * st + hl];
         qx[st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        qsc[st] = QS[(qhead + myq) * 4 + 2 * st + hl];
-      } else {
-        qx[st] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-        qsc[st] = 127;
+        qsc[st] = q_in ? sc : 127;
+        if (!q_in) qx[st] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
-    }
-  } else {
-    const uint16_t* Qp = (const uint16_t*)Qv + qhead * D;
+    } else {
+      const uint16_t* Qr = (const uint16_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
 #pragma unroll
-    for (int ks = 0; ks < Gv::kNKS; ++ks) {
-      if (q_in) {
-        qv[ks] = *(const vec8*)(Qp + (size_t)myq * D + 16 * ks + 8 * hl);
-      } else {
+      for (int ks = 0; ks < Gv::kNKS; ++ks) qv[ks] = *(const vec8*)(Qr + 16 * ks + 8 * hl);
+      if (!q_in) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
+        for (int ks = 0; ks < Gv::kNKS; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
       }
+      if (rq.cos && q_in) rope_q<Tr, D>(qv, rq, myq, hl);
     }
-    if (rq.cos && q_in) rope_q<Tr, D>(qv, rq, myq, hl);
-  }
+  };
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
   const int n_tiles = (kv_end + kBN - 1) / kBN;
@@ -521,6 +521,28 @@ __device__ CA_INLINE void prefill_dma_qtile(
   constexpr int kMD = 4;            // steps read ahead
   static_assert(kNQK % kLoads == 0, "loads spread over the QK steps");
   constexpr int kKK = 16 * kVRowB;  // bytes per P^T k-step of V rows
+  // A wave's LDS reads run at ~1 KB per 35-40 cycles, slower than its MFMAs
+  // consume them, and its softmax block issues none: the V^T fragments of
+  // the first kNPF PV steps of M(s + 1) are read during softmax(s) (tile s
+  // is resident from barrier s until barrier s + 2, which follows M(s + 1)).
+  constexpr int kNPF = 4;
+  u32x4 pvf[kNPF];
+  auto pv_read = [&](uint32_t va1, uint32_t va2, int i) CA_INLINE {
+    const uint32_t x = 64 * (i >> 2);
+    u32x2 a, c;
+    switch (i & 3) {
+      case 0: a = lds_read_tr16<0>(va1 ^ x); c = lds_read_tr16<0>(va2 ^ x); break;
+      case 1: a = lds_read_tr16<kKK>(va1 ^ x); c = lds_read_tr16<kKK>(va2 ^ x); break;
+      case 2: a = lds_read_tr16<2 * kKK>(va1 ^ x); c = lds_read_tr16<2 * kKK>(va2 ^ x); break;
+      default: a = lds_read_tr16<3 * kKK>(va1 ^ x); c = lds_read_tr16<3 * kKK>(va2 ^ x); break;
+    }
+    return u32x4{a[0], a[1], c[0], c[1]};
+  };
+  auto pv_prefetch = [&](int t) CA_INLINE {
+    const uint32_t va1 = stage(t) + vofs1, va2 = stage(t) + vofs2;
+#pragma unroll
+    for (int i = 0; i < kNPF; ++i) pvf[i] = pv_read(va1, va2, i);
+  };
   auto mblock = [&](int s, auto pv_tag, auto qk_tag) CA_INLINE {
     constexpr bool DPV = decltype(pv_tag)::value, DQK = decltype(qk_tag)::value;
     constexpr int NPV = DPV ? kNPV : 0, N = NPV + (DQK ? kNQK : 0);
@@ -539,19 +561,14 @@ __device__ CA_INLINE void prefill_dma_qtile(
         for (int r = 0; r < 16; ++r) sacc[mb][r] = 0.f;
     }
     u32x4 fr[kMD + 1][kRQK];
+    // steps [0, P0) take the fragments read during the softmax; the ring
+    // streams steps [P0, N)
+    constexpr int P0 = DPV ? kNPF : 0;
     auto nreads = [&](int i) CA_INLINE { return i < NPV ? 2 : kRQK; };
     auto fread = [&](int i) CA_INLINE {
       const int b = i % (kMD + 1);
       if (i < NPV) {
-        const uint32_t x = 64 * (i >> 2);
-        u32x2 a, c;
-        switch (i & 3) {
-          case 0: a = lds_read_tr16<0>(va1 ^ x); c = lds_read_tr16<0>(va2 ^ x); break;
-          case 1: a = lds_read_tr16<kKK>(va1 ^ x); c = lds_read_tr16<kKK>(va2 ^ x); break;
-          case 2: a = lds_read_tr16<2 * kKK>(va1 ^ x); c = lds_read_tr16<2 * kKK>(va2 ^ x); break;
-          default: a = lds_read_tr16<3 * kKK>(va1 ^ x); c = lds_read_tr16<3 * kKK>(va2 ^ x); break;
-        }
-        fr[b][0] = u32x4{a[0], a[1], c[0], c[1]};
+        fr[b][0] = pv_read(va1, va2, i);
       } else {
         const int j = i - NPV, mb = j & 1, ks = j >> 1;
         if constexpr (MX) {
@@ -566,20 +583,31 @@ __device__ CA_INLINE void prefill_dma_qtile(
       }
     };
 #pragma unroll
-    for (int i = 0; i < kMD && i < N; ++i) fread(i);
+    for (int i = P0; i < P0 + kMD && i < N; ++i) fread(i);
+    if constexpr (P0 > 0) {
+      int pending = 0;  // the ring reads just issued; the prefetched ones are older
+#pragma unroll
+      for (int k = P0; k < P0 + kMD && k < N; ++k) pending += nreads(k);
+      wait_lgkm_n(pending);
+#pragma unroll
+      for (int i = 0; i < P0; ++i) after_wait(pvf[i]);
+    }
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       const int b = i % (kMD + 1);
-      if (i + kMD < N) fread(i + kMD);
-      int pending = 0;  // reads issued after step i's
+      if (i >= P0) {
+        if (i + kMD < N) fread(i + kMD);
+        int pending = 0;  // reads issued after step i's
 #pragma unroll
-      for (int k = i + 1; k <= i + kMD && k < N; ++k) pending += nreads(k);
-      wait_lgkm_n(pending);
+        for (int k = i + 1; k <= i + kMD && k < N; ++k) pending += nreads(k);
+        wait_lgkm_n(pending);
 #pragma unroll
-      for (int r = 0; r < kRQK; ++r) after_wait(fr[b][r]);
+        for (int r = 0; r < kRQK; ++r) after_wait(fr[b][r]);
+      }
       if (i < NPV) {
         const int ob = i >> 2, kk = i & 3;
-        o[ob] = Tr::mfma32(__builtin_bit_cast(vec8, fr[b][0]), pb[kk], o[ob]);
+        const u32x4 va = i < P0 ? pvf[i < P0 ? i : 0] : fr[b][0];
+        o[ob] = Tr::mfma32(__builtin_bit_cast(vec8, va), pb[kk], o[ob]);
       } else {
         const int j = i - NPV, mb = j & 1, ks = j >> 1;
         if constexpr (MX) {
@@ -632,6 +660,7 @@ __device__ CA_INLINE void prefill_dma_qtile(
     };
 #pragma unroll
     for (int tt = 0; tt < kPpAhead; ++tt) issue(tt);
+    load_q();
     if (!lead) bar(0);
     int s = 0;
     if (w_tiles > 0) {
@@ -639,6 +668,7 @@ __device__ CA_INLINE void prefill_dma_qtile(
       if (lead) bar(0);
       mblock(0, F_{}, T_{});
       if (!lead) bar(1);
+      pv_prefetch(0);
       if (w_tiles > 1) first_softmax(0, F_{});
       else first_softmax(0, T_{});
       // steady tiles: PV(s - 1) + QK(s), the stale-max softmax
@@ -646,12 +676,14 @@ __device__ CA_INLINE void prefill_dma_qtile(
         if (lead) bar(s);
         mblock(s, T_{}, T_{});
         if (!lead) bar(s + 1);
+        pv_prefetch(s);
         stale_softmax(s, F_{});
       }
       if (s < w_tiles) {  // the wave's last tile, masked
         if (lead) bar(s);
         mblock(s, T_{}, T_{});
         if (!lead) bar(s + 1);
+        pv_prefetch(s);
         stale_softmax(s, T_{});
         ++s;
       }
@@ -682,6 +714,7 @@ __device__ CA_INLINE void prefill_dma_qtile(
     // slots without a memory access.
 #pragma unroll
     for (int tt = 0; tt < kAhead; ++tt) issue(tt);
+    load_q();
     // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
     // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
     // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
