@@ -10,7 +10,10 @@
 //   one workgroup = 8 waves = 256 query rows of one (b, h);
 //   each wave owns 32 query rows for the whole KV walk;
 //   KV tiles of 64 keys travel HBM -> LDS by buffer loads into a ring of 4
-//   tiles (one barrier per two tiles) shared by the 8 waves.
+//   tiles shared by the 8 waves; the two waves of a SIMD run the ping-pong
+//   walk (16-bit head dim 128: one waits at the per-tile barrier before its
+//   MFMA block, the other after it, so one's softmax runs under the other's
+//   MFMAs) or the lockstep walk (head dim 64, MX: one barrier per two tiles).
 // Per wave and KV tile (32x32x16 MFMAs):
 //   S^T[64 keys x 32 q] = K Q^T   (A = K rows from LDS, B = Q from registers)
 //   softmax over keys: keys live in the registers of a lane (16 per 32-key
@@ -75,7 +78,7 @@ __device__ __forceinline__ void rope_q(typename Tr::vec8 (&qv)[D / 16], RopeQ rq
 // One workgroup = 256 query rows of one (b, h) = 8 waves of 32 rows, two per
 // SIMD (waves w and w+4 share one). K/V tiles of 64 keys travel HBM -> LDS
 // with buffer loads into a ring of kStages tiles (every wave loads 1/8 of
-// every K and V tile; one barrier per two tiles). Tile layout: 64 rows x 2D bytes,
+// every K and V tile). Tile layout: 64 rows x 2D bytes,
 // unpadded; the 16-byte chunk c of row r is stored at position c ^ swz(r),
 // which makes both read patterns bank-conflict free:
 //   K, ds_read_b128: a 16-lane group reads one chunk of 16 consecutive rows
