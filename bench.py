@@ -22,7 +22,7 @@ synchronisation. ``cpu_baseline`` times the numpy oracle on a bounded sample
 of the same inputs on this host's cores (a reported baseline only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|backward|copy|read|refgrid]
+                       [--workload all|prefill|prefill_nc|decode_fp8|decode_bf16|mxfp8|backward|copy|read|refgrid|host]
 """
 import argparse
 import json
@@ -538,6 +538,76 @@ def w_refgrid(steps, warmup):
 _READ_CEILING = {}
 
 
+def w_host(steps, warmup):
+    """Host cost per call of the entry points on shapes whose kernels take a
+    few microseconds, so a loop of calls is bound by the host: the Python
+    API (argument checks, output and workspace allocation, ctypes call), the
+    C ABI through ctypes with preallocated buffers, and torch's own dispatch
+    of one small elementwise op as the yardstick. Microseconds per call
+    (wall clock over n calls, one synchronisation at the end)."""
+    import ctypes
+    import time
+    import torch
+    import cuda_llm
+    import cuda_amd._lib as L
+    n = max(200, steps * 10)
+    g = _gen()
+    rows = []
+
+    def timed(fn):
+        for _ in range(min(warmup, 50)):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e6
+
+    def gpu(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ts = []
+        for _ in range(20):
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return sorted(ts)[len(ts) // 2]
+
+    bf = torch.bfloat16
+    lib = L.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    # prefill: 1 x 1 x 64 x 128
+    q, k, v = (torch.randn(1, 1, 64, 128, device="cuda", generator=g).to(bf) for _ in range(3))
+    o = torch.empty_like(q)
+    args = (L.CA_BF16, p(q), p(k), p(v), p(o), 1, 1, 1, 64, 128, ctypes.c_float(128 ** -0.5), 1,
+            stream)
+    rows.append({"case": "flash_attention_forward 1x1x64x128 causal",
+                 "api_us": round(timed(lambda: cuda_llm.flash_attention_forward(q, k, v, is_causal=True)), 2),
+                 "abi_us": round(timed(lambda: lib.ca_flash_attention_fwd(*args)), 2),
+                 "gpu_us": round(gpu(lambda: lib.ca_flash_attention_fwd(*args)), 2)})
+    # paged decode: 1 sequence, 32 query / 8 kv heads, 16 tokens
+    c = make_paged(1, 32, 8, 128, torch.tensor([16]), False)
+    kc, vc, tb, ln, qq = c["kc"], c["vc"], c["tables"], c["lens"], c["query"]
+    ws_bytes = int(lib.ca_decode_workspace_bytes(1, 32, 128, tb.shape[1] * 16))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(qq)
+    pargs = (L.CA_BF16, p(qq), p(kc), p(vc), p(tb), p(ln), p(out), 1, 32, 8, 128, tb.shape[1], 16,
+             kc.shape[0], ctypes.c_float(128 ** -0.5), p(ws), ctypes.c_size_t(ws.numel()), stream)
+    rows.append({"case": "paged_attention_forward 1 seq x 32/8 heads x 16 tokens",
+                 "api_us": round(timed(lambda: cuda_llm.paged_attention_forward(qq, kc, vc, tb, ln)), 2),
+                 "abi_us": round(timed(lambda: lib.ca_paged_attention(*pargs)), 2),
+                 "gpu_us": round(gpu(lambda: lib.ca_paged_attention(*pargs)), 2)})
+    x = torch.zeros(64, device="cuda")
+    rows.append({"case": "torch yardstick: x.add_(1) on 64 floats",
+                 "api_us": round(timed(lambda: x.add_(1)), 2), "gpu_us": round(gpu(lambda: x.add_(1)), 2)})
+    for r in rows:
+        log(f"host: {r}")
+    return rows
+
+
 def read_ceiling(steps, warmup):
     """Measured streaming-read GB/s, once per process."""
     import torch
@@ -560,6 +630,7 @@ WORKLOADS = {
     "copy": w_copy,
     "read": w_read,
     "refgrid": w_refgrid,
+    "host": w_host,
 }
 TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
                "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5",
@@ -685,6 +756,12 @@ def main():
     if args.workload == "refgrid":
         rows = w_refgrid(args.steps, args.warmup)
         print(json.dumps({"metric": "reference benchmark grid (benchmark_pytorch.py)", "n_gpus": 1,
+                          "data": "synthetic, seeded", "device": props.name, "rows": rows}),
+              flush=True)
+        return
+    if args.workload == "host":
+        rows = w_host(args.steps, args.warmup)
+        print(json.dumps({"metric": "host microseconds per call (launch-bound shapes)", "n_gpus": 1,
                           "data": "synthetic, seeded", "device": props.name, "rows": rows}),
               flush=True)
         return

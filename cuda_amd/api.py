@@ -42,8 +42,15 @@ def _check(cond, msg):
         raise RuntimeError(msg)
 
 
-def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_getDevice"):
+    def _stream():
+        # The current device's current stream, as torch.cuda.current_stream()
+        # gives it, without building a Stream object (0.3 us instead of 3 us
+        # per call on the host).
+        return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice()))
+else:
+    def _stream():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
 def _ptr(t):

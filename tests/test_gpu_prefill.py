@@ -118,6 +118,23 @@ def test_every_row_written(dev):
     assert torch.isfinite(out).all()
 
 
+def test_runs_on_current_stream(dev):
+    """Calls enqueue on torch's current stream (a side stream here), as the
+    reference's binding does with getCurrentCUDAStream."""
+    from cuda_amd.api import _stream
+    q, k, v = qkv(2, 4, 300, 128, torch.bfloat16, dev)
+    ref = cuda_llm.flash_attention(q, k, v, is_causal=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert (_stream().value or 0) == side.cuda_stream
+        out = cuda_llm.flash_attention(q, k, v, is_causal=True)
+    assert (_stream().value or 0) == torch.cuda.current_stream().cuda_stream  # NULL = default
+    side.synchronize()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 def test_deterministic(dev):
     q, k, v = qkv(2, 8, 1000, 128, torch.bfloat16, dev)
     a = cuda_llm.flash_attention(q, k, v, is_causal=True)
