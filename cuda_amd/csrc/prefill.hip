@@ -126,13 +126,28 @@ constexpr int kPpAhead = 2;
 // hazard of gfx950, so MFMAs issued before it have written their results.
 __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
 
+// A query tile of a workgroup: 256 rows of head bh (qt < 0: none).
+struct PfItem {
+  int bh, qt;
+};
+
 // One query tile (256 rows of head bh) of the workgroup: the whole key walk
 // and the output store. Per wave and KV tile: QK (16 MFMAs at D = 128), the
 // softmax step, PV (16 MFMAs); the overlap of MFMA and VALU comes from the
 // other wave on the SIMD. MFMA blocks run at raised wave priority
 // (s_setprio), so a wave's MFMAs win issue over its partner wave's softmax
-// VALU. On return every wave has waited for its own HBM -> LDS loads, but
-// other waves may still read the ring.
+// VALU.
+//
+// A workgroup takes its tiles one after another, and the ring keeps
+// streaming across them: ring tiles are numbered from g0 (the tiles of the
+// earlier items), and in the ping-pong walk the two loads past this item's
+// last key tile fetch the first two key tiles of the next item `nx` instead
+// of zeros; its Q rows are loaded before this item's output store. The
+// return value says so (`pre` of the next call: its first tiles and Q rows
+// are in flight). Otherwise (lockstep walk, no next item, or a walk shorter
+// than kPpAhead tiles) every wave has waited for its own loads on return,
+// other waves may still read the ring, and the caller puts a barrier before
+// the next item.
 //
 // MX (MXFP8 attention, D = 128): Q and K are OCP e4m3 codes with one e8m0
 // scale byte per 32 elements along D (QS, KS: [rows][4]); V is its exact
@@ -149,11 +164,12 @@ __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\
 // code bytes (the swizzle of 128-byte rows), followed in the ring stage by
 // the V tile and the tile's 64 scale words (4 bytes per key).
 template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
-__device__ CA_INLINE void prefill_dma_qtile(
+__device__ CA_INLINE bool prefill_dma_qtile(
     const void* __restrict__ Qv, const void* __restrict__ Kv, const uint8_t* __restrict__ QS,
     const uint8_t* __restrict__ KS, const uint16_t* __restrict__ V, void* __restrict__ Ov,
     float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh, int qt, int q_shift,
-    RopeQ rq) {
+    RopeQ rq, PfItem nx, bool pre, int& g0, typename Tr::vec8 (&qv)[MX ? 1 : D / 16],
+    i32x8 (&qx)[2], int (&qsc)[2]) {
   static_assert(!MX || (D == 128 && std::is_same<Tr, BF16>::value), "MX: D = 128, bf16 PV");
   using Gv = PfGeom<D>;                   // V tile geometry (and K's for 16-bit K)
   using Gk = PfGeom<MX ? 64 : D>;         // K tile geometry: 128-byte rows for MX codes
@@ -182,13 +198,20 @@ __device__ CA_INLINE void prefill_dma_qtile(
   // are too short to hide the partner's softmax and the lockstep walk stays.
   constexpr bool kPingPong = D == 128 && !MX;
   static_assert(kQkSteps % kLoads == 0, "loads spread over the QK steps");
+  static_assert((kStages & (kStages - 1)) == 0, "ring slots: tile & (kStages - 1)");
 
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
+  // per wave: 32 output rows x 128 bytes, staging the output store
+  constexpr int kOStgB = 32 * 128;
+  __shared__ __attribute__((aligned(16))) unsigned char ostg[kNW * kOStgB];
 
-  const int b = bh / Hq, h = bh % Hq;
-  const int hk = h / (Hq / Hkv);
+  // the K (V, MX scale) rows of head bh's kv head
+  auto kv_rows = [&](int bx) CA_INLINE {
+    const int hx = bx % Hq;
+    return (size_t)((bx / Hq) * Hkv + hx / (Hq / Hkv)) * S;
+  };
   const int q0 = qt * kBM - q_shift;  // tile 0 may start before row 0 (rows < 0 are padding)
-  const size_t qhead = (size_t)(b * Hq + h) * S, khead = (size_t)(b * Hkv + hk) * S;
+  const size_t qhead = (size_t)bh * S, khead = kv_rows(bh);
   const unsigned char* Kp = (const unsigned char*)Kv + khead * kKRowB;
   const uint16_t* Vp = V + khead * D;
   const uint8_t* KSp = MX ? KS + khead * 4 : nullptr;
@@ -200,29 +223,39 @@ __device__ CA_INLINE void prefill_dma_qtile(
   const int myq = qw0 + l32;
   const bool q_in = myq >= 0 && myq < S;
 
-  // Q as the B operand of S^T = K Q^T
-  vec8 qv[MX ? 1 : Gv::kNKS];  // 16-bit Q, k-step ks: d = 16 ks + 8 hl + [0, 8)
-  i32x8 qx[2];                  // MX codes, k-step s (layout above)
-  int qsc[2];                   // MX scale bytes of blocks 2s + hl
-  // Issued after the first K/V tiles' loads, so that their latencies overlap.
-  // Rows outside [0, S) load row 0 and are zeroed.
-  auto load_q = [&]() CA_INLINE {
+  // Q as the B operand of S^T = K Q^T: qv, 16-bit Q, k-step ks: d = 16 ks +
+  // 8 hl + [0, 8); MX: qx codes of k-step s (layout above), qsc scale bytes
+  // of blocks 2s + hl. Loaded after the first K/V tiles' loads, so that
+  // their latencies overlap: the lane's row of tile (bx, qtx), row 0 for
+  // rows outside [0, S) ...
+  auto load_q_raw = [&](int bx, int qtx) CA_INLINE {
+    const int r = qtx * kBM - q_shift + wave * 32 + l32;
+    const size_t row = (size_t)bx * S + ((r >= 0 && r < S) ? r : 0);
     if constexpr (MX) {
-      const uint8_t* Qr = (const uint8_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
+      const uint8_t* Qr = (const uint8_t*)Qv + row * D;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const u32x4 lo = *(const u32x4*)(Qr + 64 * st + 16 * hl);
         const u32x4 hi = *(const u32x4*)(Qr + 64 * st + 32 + 16 * hl);
-        const int sc = QS[(qhead + (q_in ? myq : 0)) * 4 + 2 * st + hl];
+        qsc[st] = QS[row * 4 + 2 * st + hl];
         qx[st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        qsc[st] = q_in ? sc : 127;
+      }
+    } else {
+      const uint16_t* Qr = (const uint16_t*)Qv + row * D;
+#pragma unroll
+      for (int ks = 0; ks < Gv::kNKS; ++ks) qv[ks] = *(const vec8*)(Qr + 16 * ks + 8 * hl);
+    }
+  };
+  // ... then zeroed (MX: codes 0, scale 2^0) outside [0, S) and rotated (RoPE).
+  auto fix_q = [&]() CA_INLINE {
+    if constexpr (MX) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        qsc[st] = q_in ? qsc[st] : 127;
         if (!q_in) qx[st] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
       }
     } else {
-      const uint16_t* Qr = (const uint16_t*)Qv + (qhead + (q_in ? myq : 0)) * D;
-#pragma unroll
-      for (int ks = 0; ks < Gv::kNKS; ++ks) qv[ks] = *(const vec8*)(Qr + 16 * ks + 8 * hl);
       if (!q_in) {
 #pragma unroll
         for (int ks = 0; ks < Gv::kNKS; ++ks)
@@ -235,6 +268,14 @@ __device__ CA_INLINE void prefill_dma_qtile(
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
   const int n_tiles = (kv_end + kBN - 1) / kBN;
+  // The next item's first kPpAhead key tiles take the ring places of this
+  // item's tiles n_tiles .. n_tiles + kPpAhead - 1 (ping-pong walk, when this
+  // walk is at least that long: its own first tiles are then all real).
+  const bool redir = kPingPong && nx.qt >= 0 && n_tiles >= kPpAhead;
+  const size_t khead_n = kv_rows(nx.bh);
+  const unsigned char* Kp_n = (const unsigned char*)Kv + khead_n * kKRowB;
+  const uint16_t* Vp_n = V + khead_n * D;
+  const int kv_end_n = CAUSAL ? min(S, nx.qt * kBM - q_shift + kBM) : S;
   // tiles this wave computes on (it still loads and synchronises for all)
   const int w_end = CAUSAL ? min(kv_end, qw0 + 32) : kv_end;
   const int w_tiles = (qw0 + 32 > 0 && qw0 < S) ? (w_end + kBN - 1) / kBN : 0;
@@ -256,18 +297,23 @@ __device__ CA_INLINE void prefill_dma_qtile(
     const int row = Gv::kRpk * (kVL * wave + i) + lane / Gv::kLpr;
     v_off[i] = row * kVRowB + 16 * ((lane % Gv::kLpr) ^ Gv::swz(row));
   }
-  // load j of tile tt: K loads, then V loads, then (MX) the scale words
+  // load j of tile tt: K loads, then V loads, then (MX) the scale words.
+  // Ring slot (g0 + tt) mod kStages; past this item's last tile, the next
+  // item's tile tt - n_tiles when redirected (else rows past kv_end: zeros).
   auto issue_one = [&](int tt, int j) CA_INLINE {
-    unsigned char* st = lds + (tt % kStages) * kStageB;
+    unsigned char* st = lds + ((g0 + tt) & (kStages - 1)) * kStageB;
+    const bool o = redir && tt >= n_tiles;
+    const uint32_t lt = (uint32_t)(o ? tt - n_tiles : tt);
+    const uint32_t end = (uint32_t)(o ? kv_end_n : kv_end);
     if (j < kKL) {
-      dma16_buf(make_rsrc_at(Kp, (uint32_t)tt * kKTileB, (uint32_t)kv_end * kKRowB),
+      dma16_buf(make_rsrc_at(o ? Kp_n : Kp, lt * kKTileB, end * kKRowB),
                 (CA_LDS void*)(st + 1024 * (kKL * wave + j)), k_off[j]);
     } else if (j < kKL + kVL) {
       const int i = j - kKL;
-      dma16_buf(make_rsrc_at(Vp, (uint32_t)tt * kVTileB, (uint32_t)kv_end * kVRowB),
+      dma16_buf(make_rsrc_at(o ? Vp_n : Vp, lt * kVTileB, end * kVRowB),
                 (CA_LDS void*)(st + kKTileB + 1024 * (kVL * wave + i)), v_off[i]);
     } else if constexpr (MX) {
-      dma4_buf(make_rsrc_at(KSp, (uint32_t)tt * kScaleB, (uint32_t)kv_end * 4),
+      dma4_buf(make_rsrc_at(KSp, lt * kScaleB, end * 4),  // never redirected (lockstep)
                (CA_LDS void*)(st + kKTileB + kVTileB), 4 * lane);
     }
   };
@@ -295,7 +341,9 @@ __device__ CA_INLINE void prefill_dma_qtile(
       kKTileB + (tr_row + 4) * kVRowB + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
   const uint32_t sofs = kKTileB + kVTileB + 4 * krow;  // MX: the scale word of row krow
   const uint32_t lds0 = lds_off(lds);
-  auto stage = [&](int tt) CA_INLINE { return lds0 + (uint32_t)((tt % kStages) * kStageB); };
+  auto stage = [&](int tt) CA_INLINE {
+    return lds0 + (uint32_t)(((g0 + tt) & (kStages - 1)) * kStageB);
+  };
 
   f32x16 o[kNOB];   // O^T accumulators
   f32x16 sacc[2];   // S^T accumulators [key block] of the tile being multiplied
@@ -661,9 +709,12 @@ __device__ CA_INLINE void prefill_dma_qtile(
         __builtin_amdgcn_s_barrier();
       }
     };
+    if (!pre) {  // else the previous item issued them
 #pragma unroll
-    for (int tt = 0; tt < kPpAhead; ++tt) issue(tt);
-    load_q();
+      for (int tt = 0; tt < kPpAhead; ++tt) issue(tt);
+      load_q_raw(bh, qt);
+    }
+    fix_q();
     if (!lead) bar(0);
     int s = 0;
     if (w_tiles > 0) {
@@ -717,7 +768,8 @@ __device__ CA_INLINE void prefill_dma_qtile(
     // slots without a memory access.
 #pragma unroll
     for (int tt = 0; tt < kAhead; ++tt) issue(tt);
-    load_q();
+    load_q_raw(bh, qt);
+    fix_q();
     // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
     // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
     // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
@@ -754,27 +806,51 @@ __device__ CA_INLINE void prefill_dma_qtile(
     }
     for (; t < n_tiles; ++t) sync(t, true);
   }
-  wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
+  // Unless the next item's first tiles are in flight into the ring, no load
+  // may still target it when the next item drains it or the workgroup exits.
+  if (!redir) wait_vmcnt<0>();
   acc_gap();
+  if constexpr (kPingPong) {
+    if (redir) load_q_raw(nx.bh, nx.qt);  // this item's Q is dead after its last QK
+  }
 
   const float l_tot = pair32_sum(l_run);
   const float inv = (l_tot > 0.f) ? 1.f / l_tot : 0.f;
   if (Lse && hl == 0 && q_in) Lse[qhead + myq] = row_lse(m_run, l_tot);
-  if (q_in) {
-    uint16_t* Orow = (uint16_t*)Ov + (qhead + myq) * D;
+  // The output rows go out through the wave's LDS block, 64 d (128 bytes)
+  // of its 32 rows per pass: O^T spreads a row over two lanes, 4 d per
+  // register group, so stores straight from registers would write 16 bytes
+  // of 32 rows per instruction; from the block, each store instruction
+  // writes 8 whole rows of the pass (8 full 128-byte lines). Block layout:
+  // row r at 128 r, 16-byte chunk c at position c ^ (r % 8). A wave's LDS
+  // accesses complete in order, so the passes need no barrier.
+  constexpr int kPassOb = 2;  // O^T blocks (32 d each) per pass
+  unsigned char* const ob_base = ostg + wave * kOStgB;
 #pragma unroll
-    for (int ob = 0; ob < kNOB; ++ob) {
+  for (int p = 0; p < kNOB / kPassOb; ++p) {
+#pragma unroll
+    for (int j = 0; j < kPassOb; ++j) {
+      const int ob = kPassOb * p + j;
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const int d = 32 * ob + 8 * a + 4 * hl;
         const ovec2 lo = OutTr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
         const ovec2 hi = OutTr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
         ovec4 w;
         w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
-        *(ovec4*)(Orow + d) = w;
+        const int c = 4 * j + a;  // d = 64 p + 8 c + 4 hl + [0, 4)
+        *(ovec4*)(ob_base + 128 * l32 + 16 * (c ^ (l32 & 7)) + 8 * hl) = w;
       }
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 8 * k + (lane >> 3), c = lane & 7;
+      const u32x4 w = *(const u32x4*)(ob_base + 128 * r + 16 * (c ^ (r & 7)));
+      const int row = qw0 + r;
+      if (row >= 0 && row < S) *(u32x4*)((uint16_t*)Ov + (qhead + row) * D + 64 * p + 8 * c) = w;
+    }
   }
+  g0 += n_tiles;
+  return redir;
 }
 
 // Operands of a prefill launch: Q, K as 16-bit rows or (MX) e4m3 codes with
@@ -793,19 +869,47 @@ template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
 __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
     PfArgs a, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired,
     int q_shift, RopeQ rq) {
-  const QTileWork wk =
-      prefill_work(xcd_remap(__builtin_amdgcn_workgroup_id_x(), n_work), n_qt, n_bh, paired);
-  const int n_pass = wk.qt1 < 0 ? 1 : 2;
-  // A pair's long tile runs first: the pair workgroups of a head then start
-  // their walks together over the same keys and share their L2 lines
+  // Work items v = blockIdx.x, + gridDim.x, ... (a persistent launch when the
+  // grid is smaller than n_work; gridDim.x is then a multiple of 8, so every
+  // item keeps the XCD that xcd_remap gives it). A paired item is two query
+  // tiles; a pair's long tile runs first: the pair workgroups of a head then
+  // start their walks together over the same keys and share their L2 lines
   // (short tile first measured -1 % on C2, with 1.2x the HBM fetches).
+  typename Tr::vec8 qv[MX ? 1 : D / 16];
+  i32x8 qx[2];
+  int qsc[2];
+  int g0 = 0;  // ring tiles taken by the earlier query tiles
+  bool pre = false;
+  int v = __builtin_amdgcn_workgroup_id_x(), pass = 0;
+  QTileWork wk = prefill_work(xcd_remap(v, n_work), n_qt, n_bh, paired);
 #pragma clang loop unroll(disable)
-  for (int pass = 0; pass < n_pass; ++pass) {
-    // the second tile refills the LDS ring: every wave must be done reading it
-    if (pass) __builtin_amdgcn_s_barrier();
-    prefill_dma_qtile<Tr, OutTr, D, CAUSAL, POS, MX>(a.q, a.k, a.qs, a.ks, a.v, a.o, a.lse, S, Hq,
-                                                     Hkv, scale_log2, pass ? wk.bh1 : wk.bh0,
-                                                     pass ? wk.qt1 : wk.qt0, q_shift, rq);
+  for (;;) {
+    // the tile after this one: the pair's second, else the next item's first
+    int v2 = v, pass2 = pass + 1;
+    QTileWork wk2 = wk;
+    if (pass2 == 2 || wk.qt1 < 0) {
+      v2 = v + (int)gridDim.x;
+      pass2 = 0;
+      if (v2 < n_work) wk2 = prefill_work(xcd_remap(v2, n_work), n_qt, n_bh, paired);
+    }
+    // Item indices and g0 are uniform; readfirstlane says so (else the
+    // compiler may keep them in vector registers and wrap every buffer load
+    // built from them in a loop over lanes).
+    const int bh = __builtin_amdgcn_readfirstlane(pass ? wk.bh1 : wk.bh0);
+    const int qt = __builtin_amdgcn_readfirstlane(pass ? wk.qt1 : wk.qt0);
+    const PfItem nx0 = v2 < n_work ? PfItem{pass2 ? wk2.bh1 : wk2.bh0, pass2 ? wk2.qt1 : wk2.qt0}
+                                   : PfItem{0, -1};
+    const PfItem nx{__builtin_amdgcn_readfirstlane(nx0.bh), __builtin_amdgcn_readfirstlane(nx0.qt)};
+    g0 = __builtin_amdgcn_readfirstlane(g0);
+    pre = prefill_dma_qtile<Tr, OutTr, D, CAUSAL, POS, MX>(a.q, a.k, a.qs, a.ks, a.v, a.o, a.lse, S,
+                                                           Hq, Hkv, scale_log2, bh, qt, q_shift, rq,
+                                                           nx, pre, g0, qv, qx, qsc);
+    if (nx.qt < 0) break;
+    // a drained ring is refilled by the next tile: every wave must be done reading it
+    if (!pre) __builtin_amdgcn_s_barrier();
+    v = v2;
+    pass = pass2;
+    wk = wk2;
   }
 }
 
@@ -820,18 +924,25 @@ static hipError_t launch_prefill_kernel(const PfArgs& a, int B, int Hq, int Hkv,
   // the first one, whose causal key walk is the shortest
   const int q_shift = (n_qt * kPfRows - S) / Gm::kBN * Gm::kBN;
   int paired = 0;
-  const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, 1, &paired);
-  if (grid == 0) return hipSuccess;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  const long long n_work = prefill_grid(B, Hq, n_qt, CAUSAL, 1, &paired);
+  if (n_work == 0) return hipSuccess;
+  if (n_work > 0x7fffffffLL) return hipErrorInvalidValue;
+  // Items of equal work (non-causal tiles, causal pairs): one workgroup per
+  // CU (the ring's LDS admits one) takes items v, v + grid, ..., so a
+  // workgroup's next tile streams into the ring behind its current one.
+  // Unpaired causal tiles differ in length and keep one workgroup each,
+  // longest first, for the hardware dispatcher to balance.
+  const long long slots = device_cus() / 8 * 8;
+  const long long grid = ((!CAUSAL || paired) && slots > 0 && n_work > slots) ? slots : n_work;
   const float sl2 = scale * kLog2e;
   const dim3 block(64 * kPfWaves);
   if (sl2 >= 0.f) {
     hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, true, MX>), dim3((unsigned)grid),
-                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired,
+                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)n_work, paired,
                        q_shift, rq);
   } else {
     hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, false, MX>), dim3((unsigned)grid),
-                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)grid, paired,
+                       block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)n_work, paired,
                        q_shift, rq);
   }
   return hipGetLastError();
