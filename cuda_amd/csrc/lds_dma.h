@@ -59,6 +59,12 @@ __device__ __forceinline__ u32x4 lds_read_b128(uint32_t a) {
   CA_DEVICE_ASM("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(a), "n"(OFF));
   return r;
 }
+// LDS write by hand, for LDS the compiler would otherwise not write before
+// every LDS DMA in flight has landed (it cannot tell the regions apart).
+template <int OFF>
+__device__ __forceinline__ void lds_write_b64(uint32_t a, u32x2 v) {
+  CA_DEVICE_ASM("ds_write_b64 %0, %1 offset:%2" ::"v"(a), "v"(v), "n"(OFF));
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   CA_DEVICE_ASM("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");

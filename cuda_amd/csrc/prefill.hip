@@ -823,9 +823,11 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   // of 32 rows per instruction; from the block, each store instruction
   // writes 8 whole rows of the pass (8 full 128-byte lines). Block layout:
   // row r at 128 r, 16-byte chunk c at position c ^ (r % 8). A wave's LDS
-  // accesses complete in order, so the passes need no barrier.
+  // accesses complete in order, so the passes need no barrier; they are
+  // issued by hand, so that they need not wait for the next tile's K/V
+  // loads into the ring.
   constexpr int kPassOb = 2;  // O^T blocks (32 d each) per pass
-  unsigned char* const ob_base = ostg + wave * kOStgB;
+  const uint32_t ob_base = lds_off(ostg) + (uint32_t)(wave * kOStgB);
 #pragma unroll
   for (int p = 0; p < kNOB / kPassOb; ++p) {
 #pragma unroll
@@ -838,15 +840,23 @@ __device__ CA_INLINE bool prefill_dma_qtile(
         ovec4 w;
         w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
         const int c = 4 * j + a;  // d = 64 p + 8 c + 4 hl + [0, 4)
-        *(ovec4*)(ob_base + 128 * l32 + 16 * (c ^ (l32 & 7)) + 8 * hl) = w;
+        lds_write_b64<0>(ob_base + 128 * l32 + 16 * (c ^ (l32 & 7)) + 8 * hl,
+                         __builtin_bit_cast(u32x2, w));
       }
     }
+    u32x4 rows[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = 8 * k + (lane >> 3), c = lane & 7;
-      const u32x4 w = *(const u32x4*)(ob_base + 128 * r + 16 * (c ^ (r & 7)));
+      rows[k] = lds_read_b128<0>(ob_base + 128 * r + 16 * (c ^ (r & 7)));
+    }
+    wait_lgkm<0>();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      after_wait(rows[k]);
+      const int r = 8 * k + (lane >> 3), c = lane & 7;
       const int row = qw0 + r;
-      if (row >= 0 && row < S) *(u32x4*)((uint16_t*)Ov + (qhead + row) * D + 64 * p + 8 * c) = w;
+      if (row >= 0 && row < S) *(u32x4*)((uint16_t*)Ov + (qhead + row) * D + 64 * p + 8 * c) = rows[k];
     }
   }
   g0 += n_tiles;
