@@ -165,20 +165,24 @@ def test_baseline_c2_shapes(dev, cfg):
 
 
 @pytest.mark.parametrize("dtype,d,b,hq,hkv,s", [
-    (torch.bfloat16, 128, 2, 32, 8, 3072),   # 8 query tiles of 384 rows: 4 pairs per head
-    (torch.float16, 128, 2, 32, 32, 3456),   # 9 tiles of 384: 4 pairs + middle tiles of 2 heads
-    (torch.bfloat16, 128, 2, 32, 8, 3800),   # 15 tiles of 256 (ragged): 7 pairs + middle tiles
-    (torch.float16, 128, 2, 32, 32, 4096),   # 16 tiles of 256: 8 pairs
-    (torch.bfloat16, 128, 7, 7, 1, 2800),    # 11 tiles of 256, 49 heads: one lone middle tile
-    (torch.bfloat16, 64, 4, 32, 8, 1900),    # 15 tiles of 128
+    (torch.bfloat16, 128, 2, 32, 8, 3072),   # 12 query tiles of 256 rows: 6 pairs per head
+    (torch.float16, 128, 2, 32, 32, 3456),   # 14 tiles (first one 128 rows): 7 pairs
+    (torch.bfloat16, 128, 2, 32, 8, 3800),   # 15 tiles: 7 pairs + middle tiles of 2 heads
+    (torch.float16, 128, 2, 32, 32, 4096),   # 16 tiles: 8 pairs
+    (torch.bfloat16, 128, 7, 7, 1, 2800),    # 11 tiles, 49 heads: one lone middle tile
+    (torch.bfloat16, 64, 4, 32, 8, 1900),    # head dim 64: 8 tiles (first one 128 rows)
+    (torch.bfloat16, 128, 2, 24, 8, 3640),   # 15 tiles, the first one 64 rows (one key tile)
+    (torch.float16, 64, 2, 24, 8, 3640),     # the same at head dim 64
 ])
 def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
     """Causal grids big enough that each workgroup takes two query tiles
     (tiles n_qt-1-p and p of a head; for an odd n_qt the middle tiles of two
-    heads), for equal work per workgroup on a 256-CU device: sampled heads
-    (including the last head, whose middle tile may be alone) against the
-    oracle, every head through row 0 (which sees key 0 only) and through
-    finiteness."""
+    heads), for equal work per workgroup on a 256-CU device; every grid here
+    also exceeds 256 such items, so each workgroup of the persistent launch
+    takes several, its key ring running on from one tile into the next (a
+    one-key-tile first tile, S = 3640, stops that). Sampled heads (including
+    the last head, whose middle tile may be alone) against the oracle, every
+    head through row 0 (which sees key 0 only) and through finiteness."""
     q, k, v = qkv(b, hq, s, d, dtype, dev, hkv=hkv)
     out = cuda_llm.flash_attention(q, k, v, is_causal=True)
     torch.cuda.synchronize()
@@ -192,13 +196,13 @@ def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
     assert (out[:, :, 0].float() - kv0).abs().max().item() <= 1e-2
 
 
-@pytest.mark.parametrize("s", [1536, 4096])
-def test_tall_workgroups_noncausal(dev, s):
-    """Large non-causal grids: S = 1536 and S = 4096 (the shapes that take
-    384-row workgroups in builds without the stale-max softmax; 256-row
-    workgroups with it, the last tile partial at S = 1536 + 256k)."""
+@pytest.mark.parametrize("s,d", [(1536, 128), (4096, 128), (3640, 128), (3640, 64)])
+def test_persistent_noncausal(dev, s, d):
+    """Non-causal grids of more than 256 query tiles: the persistent launch,
+    whose workgroups take several tiles each, the key ring running on from
+    one tile into the next; S = 3640 is ragged (the first tile holds 64 rows)."""
     b, hq, hkv = (4, 32, 8) if s == 1536 else (2, 32, 8)
-    q, k, v = qkv(b, hq, s, 128, torch.bfloat16, dev, hkv=hkv)
+    q, k, v = qkv(b, hq, s, d, torch.bfloat16, dev, hkv=hkv)
     out = cuda_llm.flash_attention(q, k, v, is_causal=False)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
