@@ -72,23 +72,55 @@ __global__ __launch_bounds__(256) void bwd_rowdot_kernel(const uint16_t* __restr
   }
 }
 
-// Store the transposed accumulators acc[ob] (rows d = 32 ob + 8 a + 4 h + 0..3,
-// column = this lane's row index l32) as row `row` of a [.., D] 16-bit tensor.
-template <typename Tr, int NOB>
-__device__ __forceinline__ void store_rowT(uint16_t* dst_row, const f32x16 (&acc)[NOB], int hl,
-                                           float mul = 1.f) {
+// Store the transposed accumulators acc[ob] (lane (l32, hl) holds d = 32 ob +
+// 8 a + 4 hl + [0, 4) of row l32) as the wave's 32 rows row0 + l32 (rows
+// outside [0, n) skipped) of the [.., D] tensor at `head`, through the wave's
+// LDS block at byte offset `stg` (32 rows x RB bytes, RB / 2 d per pass; row
+// r's 16-byte chunk c at position c ^ (r % (RB / 16))). Stored from
+// registers, a row's d are spread over two lanes, so every store instruction
+// would write 16 bytes of 32 rows; from the block, each writes 64 / (RB / 16)
+// whole RB-byte row pieces. The LDS accesses are hand-issued and in wave
+// order, so the passes need no barrier.
+template <typename Tr, int NOB, int RB>
+__device__ __forceinline__ void store_rowsT_lds(uint16_t* head, int row0, int n,
+                                                const f32x16 (&acc)[NOB], float mul, uint32_t stg,
+                                                int lane) {
   using vec4 = typename Tr::vec4;
   using vec2 = typename Tr::vec2;
+  constexpr int D = 32 * NOB;
+  constexpr int NCH = RB / 16;   // 16-byte chunks per staged row
+  constexpr int OBP = RB / 64;   // accumulator blocks (32 d) per pass
+  constexpr int RPI = 64 / NCH;  // rows per LDS read / store instruction
+  static_assert(NOB % OBP == 0 && 32 % RPI == 0, "store passes");
+  const int l32 = lane & 31, hl = lane >> 5;
 #pragma unroll
-  for (int ob = 0; ob < NOB; ++ob) {
+  for (int p = 0; p < NOB / OBP; ++p) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int d = 32 * ob + 8 * a + 4 * hl;
-      const vec2 lo = Tr::pack2(acc[ob][4 * a] * mul, acc[ob][4 * a + 1] * mul);
-      const vec2 hi = Tr::pack2(acc[ob][4 * a + 2] * mul, acc[ob][4 * a + 3] * mul);
-      vec4 w;
-      w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
-      *(vec4*)(dst_row + d) = w;
+    for (int j = 0; j < OBP; ++j) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const int ob = OBP * p + j, c = 4 * j + a;  // d = 32 ob + 8 a + 4 hl + [0, 4)
+        const vec2 lo = Tr::pack2(acc[ob][4 * a] * mul, acc[ob][4 * a + 1] * mul);
+        const vec2 hi = Tr::pack2(acc[ob][4 * a + 2] * mul, acc[ob][4 * a + 3] * mul);
+        vec4 w;
+        w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
+        lds_write_b64<0>(stg + RB * l32 + 16 * (c ^ (l32 % NCH)) + 8 * hl,
+                         __builtin_bit_cast(u32x2, w));
+      }
+    }
+    u32x4 t[32 / RPI];
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      const int r = RPI * k + lane / NCH, c = lane % NCH;
+      t[k] = lds_read_b128<0>(stg + RB * r + 16 * (c ^ (r % NCH)));
+    }
+    wait_lgkm<0>();
+#pragma unroll
+    for (int k = 0; k < 32 / RPI; ++k) {
+      after_wait(t[k]);
+      const int r = RPI * k + lane / NCH, c = lane % NCH;
+      const int row = row0 + r;
+      if (row >= 0 && row < n) *(u32x4*)(head + (size_t)row * D + (RB / 2) * p + 8 * c) = t[k];
     }
   }
 }
@@ -184,6 +216,8 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
   constexpr int kDma = kTileB / 1024 / kNW;    // 1-KB loads per wave per K (and V) tile
   static_assert(kDma * 1024 * kNW == kTileB, "whole 1-KB loads per wave");
   __shared__ __attribute__((aligned(1024))) unsigned char lds[kStages * kStageB];
+  // per wave: 32 dQ rows x 128 bytes, staging the dQ store
+  __shared__ __attribute__((aligned(16))) unsigned char qstg[kNW * 32 * 128];
 
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
@@ -340,7 +374,8 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
     }
   }
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
-  if (qvalid) store_rowT<Tr, kNOB>(dQ + (qoff + myq) * D, acc, hl, scale);
+  store_rowsT_lds<Tr, kNOB, 128>(dQ + qoff * D, qw0, S, acc, scale,
+                                 lds_off(qstg) + (uint32_t)(wave * 32 * 128), lane);
 }
 
 template <typename Tr, int D, bool CAUSAL>
@@ -569,11 +604,9 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
     }
   }
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
-  if (kvalid) {
-    const size_t koff = (kvoff + mykey) * D;
-    store_rowT<Tr, kNOB>(dK + koff, dk, hl, scale);
-    store_rowT<Tr, kNOB>(dV + koff, dv, hl, 1.f);
-  }
+  // the wave's V rows are no longer read: their LDS block stages dK, then dV
+  store_rowsT_lds<Tr, kNOB, kRowB>(dK + kvoff * D, kw0, S, dk, scale, lds_off(vw), lane);
+  store_rowsT_lds<Tr, kNOB, kRowB>(dV + kvoff * D, kw0, S, dv, 1.f, lds_off(vw), lane);
 }
 
 template <typename Tr, int D, bool CAUSAL>
