@@ -40,8 +40,12 @@ def test_rope_reference_grid(dev, dtype, head_dim, is_causal):
     assert_close(to_np(out), ref, **tol, name="rope")
 
 
-@pytest.mark.parametrize("b,hq,hkv,s,d", [(2, 8, 2, 1024, 128), (1, 4, 4, 777, 64), (2, 32, 8, 2048, 128)])
+@pytest.mark.parametrize("b,hq,hkv,s,d", [(2, 8, 2, 1024, 128), (1, 4, 4, 777, 64), (2, 32, 8, 2048, 128),
+                                           (2, 32, 8, 4096, 128)])
 def test_rope_longer_and_gqa(dev, b, hq, hkv, s, d):
+    """Longer sequences and GQA; at S = 4096 the grid is persistent (512
+    causal pairs), so the rotated Q of a query tile is often loaded by the
+    workgroup's previous tile, of another head."""
     q, k, v = qkv(b, hq, s, d, torch.bfloat16, dev, hkv=hkv)
     cos, sin = rope_tables(s, d, dev)
     out = cuda_llm.fused_rope_flash_attention(q, k, v, cos, sin)  # default causal
