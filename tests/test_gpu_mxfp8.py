@@ -106,6 +106,22 @@ def test_mx_fp16_output(dev):
     assert_close(to_np(out), oracle.attention(d["q"], d["k"], d["v"]), **TOL_FP8, name="fp16 out")
 
 
+@pytest.mark.parametrize("b,h,s,causal", [(1, 64, 2048, False), (2, 24, 3640, True)])
+def test_mx_persistent_grid(dev, b, h, s, causal):
+    """Grids of more than 256 work items (512 non-causal query tiles; 360
+    causal pairs, the first tile of each head 64 rows): each workgroup of the
+    persistent launch takes several, draining and refilling its ring between
+    them. Sampled heads against the oracle."""
+    x = mx_inputs(b, h, s, 128, dev, seed=s)
+    out = _run(x, causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    for (bi, hi) in [(0, 0), (b - 1, h - 1)]:
+        d = _ref(x, heads=(bi, hi))
+        ref = oracle.attention(d["q"], d["k"], d["v"], is_causal=causal)
+        assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_FP8, name=f"head {bi},{hi}")
+
+
 def test_baseline_c5_shape(dev):
     """C5: B=1, H=16, S=8192, D=128, causal; sampled heads vs the oracle."""
     x = mx_inputs(1, 16, 8192, 128, dev, seed=0)
