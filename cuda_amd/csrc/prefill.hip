@@ -7,7 +7,9 @@
 // 82-83 causal tile bound, 179-229 online softmax, 223 l == 0 -> 0).
 //
 // Work decomposition
-//   one workgroup = 8 waves = 256 query rows of one (b, h);
+//   one query tile = 256 query rows of one (b, h), taken by 8 waves; a
+//   workgroup takes one query tile, a causal pair of them, or (persistent
+//   launch, one workgroup per CU) every grid-th such item in turn;
 //   each wave owns 32 query rows for the whole KV walk;
 //   KV tiles of 64 keys travel HBM -> LDS by buffer loads into a ring of 4
 //   tiles shared by the 8 waves; the two waves of a SIMD run the ping-pong
@@ -884,7 +886,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
   // item keeps the XCD that xcd_remap gives it). A paired item is two query
   // tiles; a pair's long tile runs first: the pair workgroups of a head then
   // start their walks together over the same keys and share their L2 lines
-  // (short tile first measured -1 % on C2, with 1.2x the HBM fetches).
+  // (short tile first measured slower on C2, with more HBM fetches).
   typename Tr::vec8 qv[MX ? 1 : D / 16];
   i32x8 qx[2];
   int qsc[2];
