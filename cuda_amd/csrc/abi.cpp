@@ -12,6 +12,8 @@
 #include <cstdio>
 #include <string>
 #include <algorithm>
+#include <climits>
+#include <initializer_list>
 #include <vector>
 
 #include "../../include/cuda_llm_abi.h"
@@ -68,10 +70,23 @@ ca_status check_head_dim(int d, const char* what) {
               what, d);
 }
 
+// Whether the product of non-negative factors is at most `limit`, found
+// without forming a product that could overflow.
+bool product_at_most(long long limit, std::initializer_list<long long> factors) {
+  for (long long f : factors)
+    if (f == 0) return true;
+  long long p = 1;
+  for (long long f : factors) {
+    if (p > limit / f) return false;
+    p *= f;
+  }
+  return true;
+}
+
 // Total elements and one (batch, head) slice: the kernels address a slice
 // with 32-bit byte offsets, so its float32 size stays below 2 GiB.
 ca_status check_sizes(int batch, int heads, int seq_len, int head_dim, const char* what) {
-  if ((long long)batch * heads * seq_len * head_dim > (1LL << 40))
+  if (!product_at_most(1LL << 40, {batch, heads, seq_len, head_dim}))
     return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
   if ((long long)seq_len * head_dim * 4 >= (1LL << 31))
     return fail(CA_INVALID_ARGUMENT, "%s: seq_len too long (one head's slice must stay below 2 GiB)",
@@ -203,6 +218,9 @@ static ca_status paged_common_checks(const char* what, const void* query, const 
   if (num_seqs < 0 || max_blocks < 0 || num_blocks < 0)
     return fail(CA_INVALID_ARGUMENT, "%s: negative size", what);
   if (num_seqs == 0) return CA_OK;
+  if (max_blocks > INT_MAX / page_size)
+    return fail(CA_INVALID_ARGUMENT, "%s: block table too wide (%d entries per sequence)", what,
+                max_blocks);
   if (num_blocks == 0 && max_blocks > 0)
     return fail(CA_INVALID_ARGUMENT, "%s: empty cache with a non-empty block table", what);
   if (!query || !out || !lens || (max_blocks > 0 && (!kc || !vc || !bt)))
@@ -465,7 +483,7 @@ ca_status ca_paged_kv_append(ca_dtype dtype, int cache_kind, const void* key, co
     return fail(CA_INVALID_ARGUMENT, "%s: caches must be 16-byte aligned", what);
   if (cache_kind == 1 && (!k_scale || !v_scale))
     return fail(CA_INVALID_ARGUMENT, "%s: FP8 caches need k_scale and v_scale", what);
-  if ((long long)num_seqs * num_kv_heads * max_new_tokens * head_dim > (1LL << 40))
+  if (!product_at_most(1LL << 40, {num_seqs, num_kv_heads, max_new_tokens, head_dim}))
     return fail(CA_INVALID_ARGUMENT, "%s: tensor too large", what);
   const int kind = cache_kind == 0 ? 0 : (per_block_scales ? 2 : 1);
   return from_hip(ca::launch_kv_append((int)dtype, kind, key, value, key_cache, value_cache,

@@ -705,8 +705,9 @@ static size_t split_partials_bytes(int N, int Hq, int D, int max_splits) {
 }
 
 size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
-  const int pages = (max_tokens + kDecodePage - 1) / kDecodePage;
-  return split_partials_bytes(N, Hq, D, (pages + kPagesPerWave - 1) / kPagesPerWave);
+  // rounded up without forming max_tokens + page - 1 (no overflow near INT_MAX)
+  const int pages = max_tokens / kDecodePage + (max_tokens % kDecodePage != 0);
+  return split_partials_bytes(N, Hq, D, pages / kPagesPerWave + (pages % kPagesPerWave != 0));
 }
 
 template <typename Tr, int D, int KIND>
@@ -1122,7 +1123,8 @@ size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int
   const int pages_per_split = (dtype == kDtypeF32) ? kPagesPerWave
                               : cache_kind == 0    ? DmaCfg<kKindPaged16>::kPages
                                                    : DmaCfg<kKindPagedFp8>::kPages;
-  return split_partials_bytes(N, Hq, D, (max_blocks_per_seq + pages_per_split - 1) / pages_per_split);
+  return split_partials_bytes(N, Hq, D, max_blocks_per_seq / pages_per_split +
+                                            (max_blocks_per_seq % pages_per_split != 0));
 }
 
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,

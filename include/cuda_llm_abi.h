@@ -36,14 +36,24 @@
 extern "C" {
 #endif
 
-typedef enum {
+/* The enums are int-sized in C and C++; in C++ they have int as their fixed
+ * underlying type, so any int a caller passes (an unknown dtype from a
+ * binding, say) is a valid value that the checks reject, not undefined
+ * behaviour. */
+#ifdef __cplusplus
+#define CA_ENUM_INT : int
+#else
+#define CA_ENUM_INT
+#endif
+
+typedef enum CA_ENUM_INT {
   CA_OK = 0,
   CA_INVALID_ARGUMENT = 1,
   CA_UNSUPPORTED = 2,
   CA_LAUNCH_FAILED = 3
 } ca_status;
 
-typedef enum { CA_F32 = 0, CA_F16 = 1, CA_BF16 = 2 } ca_dtype;
+typedef enum CA_ENUM_INT { CA_F32 = 0, CA_F16 = 1, CA_BF16 = 2 } ca_dtype;
 
 /* Prefill forward: O = softmax(Q K^T * scale [+ causal mask]) V.
  * q, o: [batch, num_q_heads, seq_len, head_dim]; k, v: [batch, num_kv_heads,
@@ -205,7 +215,7 @@ ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
 /* Scale formats of the MXFP8 entry point: e8m0 bytes (the MX storage
  * format, value 2^(byte - 127), 0xFF = NaN) or float32 powers of two (the
  * reference's `const float*` form, kernels_api.h:103-108). */
-typedef enum { CA_SCALE_E8M0 = 0, CA_SCALE_F32 = 1 } ca_scale_kind;
+typedef enum CA_ENUM_INT { CA_SCALE_E8M0 = 0, CA_SCALE_F32 = 1 } ca_scale_kind;
 
 /* MXFP8 attention: q, k, v are OCP e4m3 codes [batch, num_heads, seq_len,
  * head_dim] with one scale per 32 elements along head_dim ([batch, num_heads,
