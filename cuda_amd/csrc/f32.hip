@@ -212,6 +212,227 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small grids: the key walk of one 32-row query block split over the 4 waves.
+//
+// When (b, h) x 128-row tiles would not give every CU a workgroup (BASELINE
+// C1: 16 heads x 8 tiles = 128 workgroups on 256 CUs, the longest walking 32
+// key tiles on each SIMD), a workgroup takes one 32-row query block and its
+// waves take key tiles w, w + 4, ... of it, each with its own online-softmax
+// state; the four states are merged through LDS at the end (O = sum_w a_w O_w /
+// sum_w a_w l_w with a_w = 2^(m_w - max m)). The critical path shrinks four
+// times and the grid grows four times. Causal launches pair blocks p and
+// n_qb-1-p in one workgroup (their walks add up to n_qb + 1 tiles for every p)
+// and deal the second block's tiles on from where the first block's left off,
+// so the four waves stay within one tile of each other.
+//
+// No wave shares a tile, so there is nothing to stage: every lane loads its
+// MFMA operands straight from global memory (L2) into registers. S^T = K Q^T
+// needs K row 16 h' + r (the key permutation above) at head-dim elements
+// (D/2) h + step: HD contiguous floats per lane, D/8 float4 loads per tile;
+// O^T += V^T P^T needs V[key 16 h + step][32 ob + l32]: one dword per lane and
+// step, 32 lanes reading one 128-byte row segment. The next tile's K loads go
+// out once this tile's S MFMAs have read K, and its V loads once the PV MFMAs
+// have read V, so each is in flight behind half a tile of MFMA work.
+// ---------------------------------------------------------------------------
+template <int D>
+struct SplitStage {
+  static constexpr int OS = D + 4;  // row stride (floats) of a wave's O block
+  float o[4][32 * OS];
+  float m[4][32];
+  float l[4][32];
+};
+
+// One 32-row query block: this wave's share of the key walk (tiles t with
+// (t + rot) % 4 == wave), the merge of the four waves' states and the store.
+template <int D, bool CAUSAL>
+__device__ CA_INLINE void prefill_f32_split_block(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh,
+    int qb, int rot, SplitStage<D>& stg) {
+  constexpr int HD = D / 2;
+  constexpr int NOB = D / 32;
+  constexpr int OS = SplitStage<D>::OS;
+
+  const int b = bh / Hq, h = bh % Hq;
+  const int hk = h / (Hq / Hkv);
+  const int q0 = qb * 32;
+  const float* Qp = Q + (size_t)(b * Hq + h) * S * D;
+  float* Op = O + (size_t)(b * Hq + h) * S * D;
+  const float* Kp = K + (size_t)(b * Hkv + hk) * S * D;
+  const float* Vp = V + (size_t)(b * Hkv + hk) * S * D;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int myq = q0 + l32;
+
+  float qv[HD];
+#pragma unroll
+  for (int k4 = 0; k4 < HD; k4 += 4) {
+    float4 x = {0.f, 0.f, 0.f, 0.f};
+    if (myq < S) x = *(const float4*)(Qp + (size_t)myq * D + HD * hl + k4);
+    qv[k4] = x.x; qv[k4 + 1] = x.y; qv[k4 + 2] = x.z; qv[k4 + 3] = x.w;
+  }
+
+  const int kv_end = CAUSAL ? min(S, q0 + 32) : S;
+  const int n_tiles = (kv_end + 31) / 32;
+  const int krow = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
+
+  // key rows past S are clamped to S - 1 (finite data; their logits are masked)
+  float4 kr[HD / 4];
+  float vr[NOB][16];
+  auto load_k = [&](int t) {
+    const float* kp = Kp + (size_t)min(t * 32 + krow, S - 1) * D + HD * hl;
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) kr[j] = *(const float4*)(kp + 4 * j);
+  };
+  auto load_v = [&](int t) {
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const float* vp = Vp + (size_t)min(t * 32 + 16 * hl + st, S - 1) * D + l32;
+#pragma unroll
+      for (int ob = 0; ob < NOB; ++ob) vr[ob][st] = vp[32 * ob];
+    }
+  };
+
+  f32x16 o[NOB];
+#pragma unroll
+  for (int i = 0; i < NOB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+  float m_run = kNegInf, l_run = 0.f;
+
+  int t = (wave - rot) & 3;
+  if (t < n_tiles) {
+    load_k(t);
+    load_v(t);
+  }
+#pragma clang loop unroll(disable)
+  for (; t < n_tiles; t += 4) {
+    const int k0 = t * 32;
+    const bool more = t + 4 < n_tiles;
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) {
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].x, qv[4 * j], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].y, qv[4 * j + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].z, qv[4 * j + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].w, qv[4 * j + 3], s, 0, 0, 0);
+    }
+    if (more) load_k(t + 4);
+
+    // online softmax in the log2 domain; register r holds key k0 + 16 hl + r
+    float x[16];
+    float tm = kNegInf;
+    const bool need_mask = CAUSAL ? (k0 + 31 > q0) : (k0 + 32 > S);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      x[r] = s[r] * scale_log2;
+      if (need_mask) {
+        const int key = k0 + 16 * hl + r;
+        if (key >= S || (CAUSAL && key > myq)) x[r] = kNegInf;
+      }
+      tm = __builtin_fmaxf(tm, x[r]);
+    }
+    const float m_new = __builtin_fmaxf(m_run, pair32_max(tm));
+    const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+#pragma unroll
+    for (int i = 0; i < NOB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+    m_run = m_new;
+    const float msub = (m_run == kNegInf) ? 0.f : m_run;
+    float p[16];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp2(x[r] - msub);
+      psum += p[r];
+    }
+    l_run = l_run * alpha + psum;
+
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+      for (int st = 0; st < 16; ++st)
+        o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[ob][st], p[st], o[ob], 0, 0, 0);
+    if (more) load_v(t + 4);
+  }
+
+  // this wave's state: unnormalised O rows, row max (log2 units) and row sum
+  const float l_tot = pair32_sum(l_run);
+  float* ow = stg.o[wave] + l32 * OS;
+#pragma unroll
+  for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      *(float4*)(ow + 32 * ob + 8 * a + 4 * hl) =
+          float4{o[ob][4 * a], o[ob][4 * a + 1], o[ob][4 * a + 2], o[ob][4 * a + 3]};
+  if (hl == 0) {
+    stg.m[wave][l32] = m_run;
+    stg.l[wave][l32] = l_tot;
+  }
+  __syncthreads();
+
+  // merge: thread -> row tid / 8, columns (D / 8) (tid % 8) ...
+  constexpr int CW = D / 8;
+  const int row = tid >> 3, c0 = (tid & 7) * CW;
+  float mw[4], aw[4];
+  float M = kNegInf;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = stg.m[w][row];
+    M = __builtin_fmaxf(M, mw[w]);
+  }
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    aw[w] = (mw[w] == kNegInf) ? 0.f : fast_exp2(mw[w] - M);
+    L += aw[w] * stg.l[w][row];
+  }
+  const float inv = (L > 0.f) ? 1.f / L : 0.f;
+  const int q = q0 + row;
+  if (q < S) {
+#pragma unroll
+    for (int j = 0; j < CW; j += 4) {
+      float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float4 x = *(const float4*)(stg.o[w] + row * OS + c0 + j);
+        acc.x += aw[w] * x.x;
+        acc.y += aw[w] * x.y;
+        acc.z += aw[w] * x.z;
+        acc.w += aw[w] * x.w;
+      }
+      *(float4*)(Op + (size_t)q * D + c0 + j) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    }
+    if (Lse && (tid & 7) == 0) Lse[(size_t)(b * Hq + h) * S + q] = row_lse(M, L);
+  }
+  // the next block overwrites the stage
+  __syncthreads();
+}
+
+// One workgroup per work item: (b, h) and block p, or (causal) blocks p and
+// n_qb-1-p. per_head = work items per (b, h).
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 1) void prefill_f32_split_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int n_qb,
+    int per_head, int n_work) {
+  __shared__ __attribute__((aligned(16))) SplitStage<D> stg;
+  const int item = xcd_remap(blockIdx.x, n_work);
+  const int bh = item / per_head, p = item % per_head;
+  prefill_f32_split_block<D, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, bh, p, 0, stg);
+  if (CAUSAL && n_qb - 1 - p != p) {
+    // deal on from where block p's p + 1 tiles left off
+    prefill_f32_split_block<D, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, bh, n_qb - 1 - p,
+                                       (p + 1) & 3, stg);
+  }
+}
+
 template <int D, bool CAUSAL>
 static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void* v, void* o, float* lse,
                                        int B, int Hq, int Hkv, int S, float scale,
@@ -222,6 +443,16 @@ static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void*
   const long long grid = prefill_grid(B, Hq, n_qt, CAUSAL, 2, &paired);
   if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (grid < device_cus()) {
+    // fewer 128-row tiles than CUs: split each 32-row block's key walk
+    const int n_qb = (S + 31) / 32;
+    const int per_head = CAUSAL ? (n_qb + 1) / 2 : n_qb;
+    const long long grid_s = (long long)B * Hq * per_head;
+    hipLaunchKernelGGL((prefill_f32_split_kernel<D, CAUSAL>), dim3((unsigned)grid_s), dim3(256), 0,
+                       stream, (const float*)q, (const float*)k, (const float*)v, (float*)o, lse, S,
+                       Hq, Hkv, scale * kLog2e, n_qb, per_head, (int)grid_s);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((prefill_f32_kernel<D, CAUSAL>), dim3((unsigned)grid), dim3(256), 0, stream,
                      (const float*)q, (const float*)k, (const float*)v, (float*)o, lse, S, Hq, Hkv,
                      scale * kLog2e, n_qt, B * Hq, (int)grid, paired);

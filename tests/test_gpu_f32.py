@@ -139,6 +139,41 @@ def test_causal_paired_query_tiles_f32(dev, head_dim):
         assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_F32, name=f"head {bi},{hi}")
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("is_causal", [False, True])
+@pytest.mark.parametrize("b,hq,hkv,s", [(1, 8, 2, 1000), (1, 2, 1, 2047), (3, 1, 1, 993),
+                                        (1, 1, 1, 33)])
+def test_split_key_walk_f32(dev, head_dim, is_causal, b, hq, hkv, s):
+    """Grids of fewer 128-row tiles than CUs: each 32-row query block's key
+    walk is split over the four waves of a workgroup and their softmax states
+    merged. Walks of 2 to 64 key tiles (16 per wave), even and odd block
+    counts (causal pairs and the lone middle block), ragged S, GQA; O and the
+    LSE against the oracle, and O identical with and without the LSE store."""
+    q, k, v = qkv(b, hq, s, head_dim, F32, dev, hkv=hkv)
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal)
+    plain = cuda_llm.flash_attention_forward(q, k, v, is_causal=is_causal)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=is_causal, dtype=np.float64)
+    assert_close(to_np(out), ref, **TOL_F32, name=f"split {b}x{hq}/{hkv}x{s}")
+    ref_lse = oracle.attention_lse(to_np(q), to_np(k), is_causal=is_causal, dtype=np.float64)
+    assert np.abs(to_np(lse) - ref_lse).max() <= 1e-4
+    assert torch.equal(out, plain)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_full_grid_noncausal_f32(dev, head_dim):
+    """A non-causal grid with a 128-row tile for every CU and more (2 x 16
+    heads x 9 tiles): the unsplit kernel, sampled heads."""
+    q, k, v = qkv(2, 16, 1100, head_dim, F32, dev, hkv=4)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=False)
+    torch.cuda.synchronize()
+    for (bi, hi) in [(0, 0), (1, 9), (1, 15)]:
+        kh = hi // 4
+        ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
+                               to_np(v[bi:bi + 1, kh:kh + 1]), dtype=np.float64)
+        assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_F32, name=f"head {bi},{hi}")
+
+
 def test_baseline_c1(dev):
     """BASELINE configs[0] (C1): fp32 q, k, v ~ N(0,1) [2, 8, 1024, 64], causal,
     scale 1/8, seeded, through cuda_llm.flash_attention."""
