@@ -33,7 +33,12 @@ COMMON = [
 # with the IEEE mode bit on, every fmaxf operand that does not come from an
 # arithmetic instruction (MFMA results do not count) is first quieted with an
 # extra v_max. The kernels there have no NaN-dependent logic.
-EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"]}
+# f32: MFMA accumulators in ordinary VGPRs. The fp32 split-walk kernel's VALU
+# reads its S and O accumulators every tile; allocated in AGPRs they cost a
+# v_accvgpr_read/write per element and tile (measured: ~130-190 per tile at
+# D = 64), which a wave pays in series with its MFMAs.
+EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
+         "f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _compile(src):

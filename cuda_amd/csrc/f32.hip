@@ -213,106 +213,161 @@ __global__ __launch_bounds__(256, 2) void prefill_f32_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Small grids: the key walk of one 32-row query block split over the 4 waves.
+// Small grids: the key walk of one 32-row query block split over the waves
+// of a workgroup.
 //
 // When (b, h) x 128-row tiles would not give every CU a workgroup (BASELINE
 // C1: 16 heads x 8 tiles = 128 workgroups on 256 CUs, the longest walking 32
 // key tiles on each SIMD), a workgroup takes one 32-row query block and its
-// waves take key tiles w, w + 4, ... of it, each with its own online-softmax
-// state; the four states are merged through LDS at the end (O = sum_w a_w O_w /
-// sum_w a_w l_w with a_w = 2^(m_w - max m)). The critical path shrinks four
-// times and the grid grows four times. Causal launches pair blocks p and
-// n_qb-1-p in one workgroup (their walks add up to n_qb + 1 tiles for every p)
-// and deal the second block's tiles on from where the first block's left off,
-// so the four waves stay within one tile of each other.
+// four waves (one per SIMD) take key tiles w, w + 4, ... of it, each with its
+// own online-softmax state; the states are merged through LDS at the end (O =
+// sum_w a_w O_w / sum_w a_w l_w with a_w = 2^(m_w - max m)). Causal launches
+// give a workgroup blocks p and n_qb-1-p (their walks add up to n_qb + 1 tiles
+// for every p), non-causal launches with more blocks than CUs blocks p and
+// p + n_qb/2, as one list of tiles dealt round-robin, so the waves stay within
+// one tile of each other, and a wave goes on from its last tile of the first
+// block to its first of the second without waiting for the others: each block
+// has its own LDS region for the states, and one barrier precedes the merge
+// of both.
 //
 // No wave shares a tile, so there is nothing to stage: every lane loads its
 // MFMA operands straight from global memory (L2) into registers. S^T = K Q^T
-// needs K row 16 h' + r (the key permutation above) at head-dim elements
-// (D/2) h + step: HD contiguous floats per lane, D/8 float4 loads per tile;
+// needs K row 16 h' + r (the key permutation above); lane half h contracts
+// head-dim elements 8 j + 4 h + c at step 4 j + c, so the two halves of a
+// float4 load read 32 adjacent bytes of a row (D/8 loads per tile);
 // O^T += V^T P^T needs V[key 16 h + step][32 ob + l32]: one dword per lane and
-// step, 32 lanes reading one 128-byte row segment. The next tile's K loads go
-// out once this tile's S MFMAs have read K, and its V loads once the PV MFMAs
-// have read V, so each is in flight behind half a tile of MFMA work.
+// step, 32 lanes reading one 128-byte row segment.
+//
+// Measured on gfx950 (one wave per SIMD): a wave's VALU and memory
+// instructions issue between its own fp32 MFMAs, not beside them (16 FMAs
+// between two v_mfma_f32_32x32x2_f32 take 64 + ~77 cycles; a 16-byte load with
+// the CU's four waves loading, ~60), and a second wave on the SIMD recovers
+// little of that. So the tile time is MFMA time plus the wave's own VALU and
+// load time: the walk keeps both small (no AGPR copies, masks and rescales
+// only where needed, full-tile V loads from one address) rather than trying to
+// hide them. Per 32-key tile at D = 64: 4096 MFMA cycles, ~5.3k measured.
 // ---------------------------------------------------------------------------
 template <int D>
 struct SplitStage {
+  static constexpr int NW = 4;      // waves per workgroup
   static constexpr int OS = D + 4;  // row stride (floats) of a wave's O block
-  float o[4][32 * OS];
-  float m[4][32];
-  float l[4][32];
+  float o[2][NW][32 * OS];          // [block][wave]: unnormalised O rows
+  float m[2][NW][32];               // row reference max m, log2 units (-inf: no tile)
+  float l[2][NW][32];               // row sum of 2^(x - m)
 };
 
-// One 32-row query block: this wave's share of the key walk (tiles t with
-// (t + rot) % 4 == wave), the merge of the four waves' states and the store.
+// This wave's share of the key walks of query blocks qa and (qb2 >= 0) qb2:
+// items g = wave, wave + NW, ... of the list [qa's tiles, qb2's tiles]; the
+// state of each block goes to its stage region (zeros, -inf and 0 for a block
+// in which the wave has no tile). The next item's K is loaded once this
+// item's S MFMAs have read K, its V once the PV MFMAs have read V, and at the
+// switch from block qa to qb2 the new Q once the last S MFMAs of qa have read
+// Q, so the walk runs on from one block into the other.
 template <int D, bool CAUSAL>
-__device__ CA_INLINE void prefill_f32_split_block(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh,
-    int qb, int rot, SplitStage<D>& stg) {
+__device__ CA_INLINE void prefill_f32_split_walk(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V, int S,
+    int Hq, int Hkv, float scale_log2, int bh, int qa, int qb2, SplitStage<D>& stg) {
   constexpr int HD = D / 2;
   constexpr int NOB = D / 32;
+  constexpr int NW = SplitStage<D>::NW;
   constexpr int OS = SplitStage<D>::OS;
 
   const int b = bh / Hq, h = bh % Hq;
   const int hk = h / (Hq / Hkv);
-  const int q0 = qb * 32;
   const float* Qp = Q + (size_t)(b * Hq + h) * S * D;
-  float* Op = O + (size_t)(b * Hq + h) * S * D;
   const float* Kp = K + (size_t)(b * Hkv + hk) * S * D;
   const float* Vp = V + (size_t)(b * Hkv + hk) * S * D;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // wave index made scalar: the item loop and its branches are uniform
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, hl = lane >> 5;
-  const int myq = q0 + l32;
-
-  float qv[HD];
-#pragma unroll
-  for (int k4 = 0; k4 < HD; k4 += 4) {
-    float4 x = {0.f, 0.f, 0.f, 0.f};
-    if (myq < S) x = *(const float4*)(Qp + (size_t)myq * D + HD * hl + k4);
-    qv[k4] = x.x; qv[k4 + 1] = x.y; qv[k4 + 2] = x.z; qv[k4 + 3] = x.w;
-  }
-
-  const int kv_end = CAUSAL ? min(S, q0 + 32) : S;
-  const int n_tiles = (kv_end + 31) / 32;
   const int krow = 16 * ((l32 >> 2) & 1) + 4 * (l32 >> 3) + (l32 & 3);
+
+  auto n_tiles_of = [&](int qb) { return CAUSAL ? qb + 1 : (S + 31) / 32; };
+  const int na = n_tiles_of(qa);
+  const int n_all = na + (qb2 >= 0 ? n_tiles_of(qb2) : 0);
+  // item -> first key of its tile (items past the list clamp to valid rows)
+  auto key0 = [&](int g) { return (g < na ? g : g - na) * 32; };
+
+  f32x16 o[NOB];
+  float m_run, l_run;
+  auto reset = [&]() {
+#pragma unroll
+    for (int i = 0; i < NOB; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
+    m_run = kNegInf;
+    l_run = 0.f;
+  };
+  auto put_state = [&](int blk) {
+    const float l_tot = pair32_sum(l_run);
+    float* ow = stg.o[blk][wave] + l32 * OS;
+#pragma unroll
+    for (int ob = 0; ob < NOB; ++ob)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        *(float4*)(ow + 32 * ob + 8 * a + 4 * hl) =
+            float4{o[ob][4 * a], o[ob][4 * a + 1], o[ob][4 * a + 2], o[ob][4 * a + 3]};
+    if (hl == 0) {
+      stg.m[blk][wave][l32] = m_run;
+      stg.l[blk][wave][l32] = l_tot;
+    }
+  };
+  reset();
+
+  int g = wave;
+  if (g >= n_all) {
+    put_state(0);
+    if (qb2 >= 0) put_state(1);
+    return;
+  }
+  if (g >= na) put_state(0);  // no tile of block qa
+
+  // Q as the B operand; lane half h contracts head-dim elements 8 j + 4 h + c
+  // at step 4 j + c, so the two halves of a float4 K load read 32 adjacent
+  // bytes of a row
+  float qv[HD];
+  auto load_q = [&](float (&dst)[HD], int qb) {
+    const int row = qb * 32 + l32;
+#pragma unroll
+    for (int k4 = 0; k4 < HD; k4 += 4) {
+      float4 x = {0.f, 0.f, 0.f, 0.f};
+      if (row < S) x = *(const float4*)(Qp + (size_t)row * D + 2 * k4 + 4 * hl);
+      dst[k4] = x.x * scale_log2;
+      dst[k4 + 1] = x.y * scale_log2;
+      dst[k4 + 2] = x.z * scale_log2;
+      dst[k4 + 3] = x.w * scale_log2;
+    }
+  };
+  load_q(qv, g < na ? qa : qb2);
 
   // key rows past S are clamped to S - 1 (finite data; their logits are masked)
   float4 kr[HD / 4];
   float vr[NOB][16];
-  auto load_k = [&](int t) {
-    const float* kp = Kp + (size_t)min(t * 32 + krow, S - 1) * D + HD * hl;
+  auto load_k = [&](int gi) {
+    const float* kp = Kp + (size_t)min(key0(gi) + krow, S - 1) * D + 4 * hl;
 #pragma unroll
-    for (int j = 0; j < HD / 4; ++j) kr[j] = *(const float4*)(kp + 4 * j);
+    for (int j = 0; j < HD / 4; ++j) kr[j] = *(const float4*)(kp + 8 * j);
   };
-  auto load_v = [&](int t) {
+  auto load_v = [&](int gi) {
+    const int k0 = key0(gi);
+    if (k0 + 32 <= S) {  // whole tile: one address, immediate offsets
+      const float* vp = Vp + (size_t)(k0 + 16 * hl) * D + l32;
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const float* vp = Vp + (size_t)min(t * 32 + 16 * hl + st, S - 1) * D + l32;
+      for (int st = 0; st < 16; ++st)
 #pragma unroll
-      for (int ob = 0; ob < NOB; ++ob) vr[ob][st] = vp[32 * ob];
+        for (int ob = 0; ob < NOB; ++ob) vr[ob][st] = vp[st * D + 32 * ob];
+    } else {
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const float* vp = Vp + (size_t)min(k0 + 16 * hl + st, S - 1) * D + l32;
+#pragma unroll
+        for (int ob = 0; ob < NOB; ++ob) vr[ob][st] = vp[32 * ob];
+      }
     }
   };
-
-  f32x16 o[NOB];
-#pragma unroll
-  for (int i = 0; i < NOB; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m_run = kNegInf, l_run = 0.f;
-
-  int t = (wave - rot) & 3;
-  if (t < n_tiles) {
-    load_k(t);
-    load_v(t);
-  }
-#pragma clang loop unroll(disable)
-  for (; t < n_tiles; t += 4) {
-    const int k0 = t * 32;
-    const bool more = t + 4 < n_tiles;
-    f32x16 s;
+  auto qk = [&](f32x16& s) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
@@ -322,115 +377,152 @@ __device__ CA_INLINE void prefill_f32_split_block(
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].z, qv[4 * j + 2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j].w, qv[4 * j + 3], s, 0, 0, 0);
     }
-    if (more) load_k(t + 4);
-
-    // online softmax in the log2 domain; register r holds key k0 + 16 hl + r
-    float x[16];
-    float tm = kNegInf;
-    const bool need_mask = CAUSAL ? (k0 + 31 > q0) : (k0 + 32 > S);
+  };
+  // Online softmax of item gi in the log2 domain (Q carries the scale;
+  // register r holds key k0 + 16 hl + r). A wave's VALU instructions issue
+  // between its own MFMAs, not beside them, so every one of them lengthens the
+  // tile: masks are applied only on a diagonal or ragged tile, and the running
+  // max m is raised (and O, l rescaled) only when some row's tile max exceeds
+  // it by more than 8, so p = 2^(x - m) <= 256 and most tiles skip the rescale.
+  float p[16];
+  auto softmax = [&](f32x16& s, int gi) {
+    const int q0 = (gi < na ? qa : qb2) * 32;
+    const int k0 = key0(gi);
+    if ((CAUSAL && k0 == q0) || k0 + 32 > S) {
+      const int lim = CAUSAL ? min(q0 + l32, S - 1) : S - 1;  // last visible key of this row
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      x[r] = s[r] * scale_log2;
-      if (need_mask) {
-        const int key = k0 + 16 * hl + r;
-        if (key >= S || (CAUSAL && key > myq)) x[r] = kNegInf;
-      }
-      tm = __builtin_fmaxf(tm, x[r]);
+      for (int r = 0; r < 16; ++r)
+        if (k0 + 16 * hl + r > lim) s[r] = kNegInf;
     }
-    const float m_new = __builtin_fmaxf(m_run, pair32_max(tm));
-    const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+    float tm = s[0];
 #pragma unroll
-    for (int i = 0; i < NOB; ++i)
+    for (int r = 1; r < 16; ++r) tm = __builtin_fmaxf(tm, s[r]);
+    tm = pair32_max(tm);
+    if (wave_any(tm > m_run + 8.f)) {
+      const float m_new = __builtin_fmaxf(m_run, tm);
+      const float alpha = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
-    m_run = m_new;
+      for (int i = 0; i < NOB; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      l_run *= alpha;
+      m_run = m_new;
+    }
     const float msub = (m_run == kNegInf) ? 0.f : m_run;
-    float p[16];
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = fast_exp2(x[r] - msub);
+      p[r] = fast_exp2(s[r] - msub);
       psum += p[r];
     }
-    l_run = l_run * alpha + psum;
-
+    l_run += psum;
+  };
+  auto pv = [&]() {
 #pragma unroll
     for (int ob = 0; ob < NOB; ++ob)
 #pragma unroll
       for (int st = 0; st < 16; ++st)
         o[ob] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[ob][st], p[st], o[ob], 0, 0, 0);
-    if (more) load_v(t + 4);
-  }
+  };
 
-  // this wave's state: unnormalised O rows, row max (log2 units) and row sum
-  const float l_tot = pair32_sum(l_run);
-  float* ow = stg.o[wave] + l32 * OS;
-#pragma unroll
-  for (int ob = 0; ob < NOB; ++ob)
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-      *(float4*)(ow + 32 * ob + 8 * a + 4 * hl) =
-          float4{o[ob][4 * a], o[ob][4 * a + 1], o[ob][4 * a + 2], o[ob][4 * a + 3]};
-  if (hl == 0) {
-    stg.m[wave][l32] = m_run;
-    stg.l[wave][l32] = l_tot;
+  f32x16 s;
+  // Start the waves a few hundred cycles apart: a wave's loads issue between
+  // its own MFMAs, each taking its share of the CU's L1 path, and four waves
+  // in lockstep issue their loads at the same time (a lone wave's 16-byte
+  // loads go through about three times faster); offset, their load phases
+  // fall into one another's MFMA phases (measured: C1 -4.5 %).
+  if (wave == 1) __builtin_amdgcn_s_sleep(10);
+  if (wave == 2) __builtin_amdgcn_s_sleep(20);
+  if (wave == 3) __builtin_amdgcn_s_sleep(30);
+  load_k(g);
+  load_v(g);
+#pragma clang loop unroll(disable)
+  for (;; g += NW) {
+    const bool more = g + NW < n_all;
+    const bool switch_blk = g < na && g + NW >= na && more;  // next item is in block qb2
+    qk(s);
+    if (switch_blk) load_q(qv, qb2);
+    if (more) load_k(g + NW);
+    softmax(s, g);
+    pv();
+    if (!more) break;
+    load_v(g + NW);
+    if (switch_blk) {
+      put_state(0);
+      reset();
+    }
   }
-  __syncthreads();
+  put_state(g < na ? 0 : 1);
+  if (qb2 >= 0 && g < na) {  // no tile of block qb2
+    reset();
+    put_state(1);
+  }
+}
 
-  // merge: thread -> row tid / 8, columns (D / 8) (tid % 8) ...
-  constexpr int CW = D / 8;
-  const int row = tid >> 3, c0 = (tid & 7) * CW;
-  float mw[4], aw[4];
+// Merge of the NW wave states of stage region blk into the output rows of
+// query block qb: thread -> row, D / (2 NW) consecutive columns.
+template <int D>
+__device__ CA_INLINE void prefill_f32_split_merge(float* __restrict__ O, float* __restrict__ Lse,
+                                                  int S, int bh, int qb, int blk,
+                                                  const SplitStage<D>& stg) {
+  constexpr int NW = SplitStage<D>::NW;
+  constexpr int OS = SplitStage<D>::OS;
+  constexpr int TPR = 2 * NW;  // threads per row
+  constexpr int CW = D / TPR;  // columns per thread
+  static_assert(CW % 4 == 0, "float4 columns");
+  const int tid = threadIdx.x;
+  const int row = tid / TPR, c0 = (tid % TPR) * CW;
+  float mw[NW], aw[NW];
   float M = kNegInf;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    mw[w] = stg.m[w][row];
+  for (int w = 0; w < NW; ++w) {
+    mw[w] = stg.m[blk][w][row];
     M = __builtin_fmaxf(M, mw[w]);
   }
   float L = 0.f;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NW; ++w) {
     aw[w] = (mw[w] == kNegInf) ? 0.f : fast_exp2(mw[w] - M);
-    L += aw[w] * stg.l[w][row];
+    L += aw[w] * stg.l[blk][w][row];
   }
   const float inv = (L > 0.f) ? 1.f / L : 0.f;
-  const int q = q0 + row;
-  if (q < S) {
+  const int q = qb * 32 + row;
+  if (q >= S) return;
+  float* Op = O + ((size_t)bh * S + q) * D;
 #pragma unroll
-    for (int j = 0; j < CW; j += 4) {
-      float4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < CW; j += 4) {
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float4 x = *(const float4*)(stg.o[w] + row * OS + c0 + j);
-        acc.x += aw[w] * x.x;
-        acc.y += aw[w] * x.y;
-        acc.z += aw[w] * x.z;
-        acc.w += aw[w] * x.w;
-      }
-      *(float4*)(Op + (size_t)q * D + c0 + j) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    for (int w = 0; w < NW; ++w) {
+      const float4 x = *(const float4*)(stg.o[blk][w] + row * OS + c0 + j);
+      acc.x += aw[w] * x.x;
+      acc.y += aw[w] * x.y;
+      acc.z += aw[w] * x.z;
+      acc.w += aw[w] * x.w;
     }
-    if (Lse && (tid & 7) == 0) Lse[(size_t)(b * Hq + h) * S + q] = row_lse(M, L);
+    *(float4*)(Op + c0 + j) = float4{acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
   }
-  // the next block overwrites the stage
-  __syncthreads();
+  if (Lse && tid % TPR == 0) Lse[(size_t)bh * S + q] = row_lse(M, L);
 }
 
-// One workgroup per work item: (b, h) and block p, or (causal) blocks p and
-// n_qb-1-p. per_head = work items per (b, h).
+// One workgroup per work item of a (b, h): block p, or two blocks: causal
+// p and n_qb-1-p (equal total walks); non-causal, when the launch has more
+// blocks than CUs, p and p + per_head (one round of workgroups instead of
+// two). per_head = work items per (b, h).
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void prefill_f32_split_kernel(
+__global__ __launch_bounds__(64 * SplitStage<D>::NW, 1) void prefill_f32_split_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int n_qb,
     int per_head, int n_work) {
   __shared__ __attribute__((aligned(16))) SplitStage<D> stg;
   const int item = xcd_remap(blockIdx.x, n_work);
   const int bh = item / per_head, p = item % per_head;
-  prefill_f32_split_block<D, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, bh, p, 0, stg);
-  if (CAUSAL && n_qb - 1 - p != p) {
-    // deal on from where block p's p + 1 tiles left off
-    prefill_f32_split_block<D, CAUSAL>(Q, K, V, O, Lse, S, Hq, Hkv, scale_log2, bh, n_qb - 1 - p,
-                                       (p + 1) & 3, stg);
-  }
+  int p2 = CAUSAL ? n_qb - 1 - p : p + per_head;
+  if (p2 == p || p2 >= n_qb) p2 = -1;
+  prefill_f32_split_walk<D, CAUSAL>(Q, K, V, S, Hq, Hkv, scale_log2, bh, p, p2, stg);
+  __syncthreads();
+  prefill_f32_split_merge<D>(O, Lse, S, bh, p, 0, stg);
+  if (p2 >= 0) prefill_f32_split_merge<D>(O, Lse, S, bh, p2, 1, stg);
 }
 
 template <int D, bool CAUSAL>
@@ -446,10 +538,11 @@ static hipError_t launch_prefill_f32_t(const void* q, const void* k, const void*
   if (grid < device_cus()) {
     // fewer 128-row tiles than CUs: split each 32-row block's key walk
     const int n_qb = (S + 31) / 32;
-    const int per_head = CAUSAL ? (n_qb + 1) / 2 : n_qb;
+    const bool two = CAUSAL || (long long)B * Hq * n_qb > device_cus();
+    const int per_head = two ? (n_qb + 1) / 2 : n_qb;
     const long long grid_s = (long long)B * Hq * per_head;
-    hipLaunchKernelGGL((prefill_f32_split_kernel<D, CAUSAL>), dim3((unsigned)grid_s), dim3(256), 0,
-                       stream, (const float*)q, (const float*)k, (const float*)v, (float*)o, lse, S,
+    hipLaunchKernelGGL((prefill_f32_split_kernel<D, CAUSAL>), dim3((unsigned)grid_s),
+                       dim3(64 * SplitStage<D>::NW), 0, stream, (const float*)q, (const float*)k, (const float*)v, (float*)o, lse, S,
                        Hq, Hkv, scale * kLog2e, n_qb, per_head, (int)grid_s);
     return hipGetLastError();
   }

@@ -142,13 +142,14 @@ def test_causal_paired_query_tiles_f32(dev, head_dim):
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("is_causal", [False, True])
 @pytest.mark.parametrize("b,hq,hkv,s", [(1, 8, 2, 1000), (1, 2, 1, 2047), (3, 1, 1, 993),
-                                        (1, 1, 1, 33)])
+                                        (1, 1, 1, 33), (2, 8, 2, 970)])
 def test_split_key_walk_f32(dev, head_dim, is_causal, b, hq, hkv, s):
     """Grids of fewer 128-row tiles than CUs: each 32-row query block's key
     walk is split over the four waves of a workgroup and their softmax states
     merged. Walks of 2 to 64 key tiles (16 per wave), even and odd block
-    counts (causal pairs and the lone middle block), ragged S, GQA; O and the
-    LSE against the oracle, and O identical with and without the LSE store."""
+    counts (causal pairs and the lone middle block; 2 x 8 x 970 also pairs
+    non-causal blocks, 31 of them per head), ragged S, GQA; O and the LSE
+    against the oracle, and O identical with and without the LSE store."""
     q, k, v = qkv(b, hq, s, head_dim, F32, dev, hkv=hkv)
     out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal)
     plain = cuda_llm.flash_attention_forward(q, k, v, is_causal=is_causal)
