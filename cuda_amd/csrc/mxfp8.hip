@@ -42,10 +42,11 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
   return __uint_as_float(e << 23);
 }
 
-// One lane per 8 codes (16 lanes per row of D = 128): V row -> bf16 row; with
-// float scales (F32SC) lanes 16r..16r+3 of each row also convert q's, k's
-// scale of block (lane % 16) into e8m0 bytes and any invalid scale raises
-// *bad.
+// One lane per 16 codes (8 lanes per row of D = 128; a 16-byte load and two
+// 16-byte stores): V row -> bf16 row; with float scales (F32SC) lanes
+// 8r..8r+3 of each row also convert q's, k's scale of block (lane % 8) into
+// e8m0 bytes and any invalid scale raises *bad. (8 codes per lane ran C5's
+// 50 MB of traffic at ~3.5 TB/s.)
 template <bool F32SC>
 __global__ __launch_bounds__(256) void mx_prepare_kernel(
     const uint8_t* __restrict__ V, const void* __restrict__ VS, const void* __restrict__ QSf,
@@ -53,10 +54,10 @@ __global__ __launch_bounds__(256) void mx_prepare_kernel(
     uint8_t* __restrict__ KSb, uint32_t* __restrict__ bad, long long n_rows) {
   constexpr int D = 128, NB = D / 32;
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long row = gid >> 4;
-  const int part = (int)(gid & 15);
+  const long long row = gid >> 3;
+  const int part = (int)(gid & 7);
   if (row >= n_rows) return;
-  const int blk = part >> 2;  // MX block of the lane's 8 codes
+  const int blk = part >> 1;  // MX block of the lane's 16 codes
   float sc;
   bool ok = true;
   if (F32SC) {
@@ -74,13 +75,15 @@ __global__ __launch_bounds__(256) void mx_prepare_kernel(
   } else {
     sc = e8m0_to_float(((const uint8_t*)VS)[row * NB + blk]);
   }
-  const uint2 c = *(const uint2*)(V + row * D + 8 * part);
-  u32x4 w;
-  w[0] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(c.x, sc));
-  w[1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(c.x, sc));
-  w[2] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(c.y, sc));
-  w[3] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(c.y, sc));
-  *(u32x4*)(Vb + row * D + 8 * part) = w;
+  const u32x4 c = *(const u32x4*)(V + row * D + 16 * part);
+  u32x4 w[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i >> 1][2 * (i & 1)] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(c[i], sc));
+    w[i >> 1][2 * (i & 1) + 1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(c[i], sc));
+  }
+  *(u32x4*)(Vb + row * D + 16 * part) = w[0];
+  *(u32x4*)(Vb + row * D + 16 * part + 8) = w[1];
 }
 
 __global__ void mx_clear_flag_kernel(uint32_t* flag) { *flag = 0u; }
@@ -110,7 +113,7 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
   w += align256((size_t)rows * D * 2);
   const uint8_t* qs8 = (const uint8_t*)qs;
   const uint8_t* ks8 = (const uint8_t*)ks;
-  const long long blocks = (rows * 16 + 255) / 256;
+  const long long blocks = (rows * 8 + 255) / 256;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   if (scale_kind == 1) {
     uint8_t* qsb = w;
