@@ -7,21 +7,25 @@
 // O = softmax(Q K^T * scale [+ causal mask]) V per (b, q head), GQA by
 // kv_head = q_head / (Hq / Hkv), O = 0 for a row with no visible key.
 //
-// Work decomposition: one workgroup = 4 waves x 32 query rows of one (b, h);
-// K/V tiles of 32 keys, double-buffered in LDS (register-staged loads, one
-// barrier per tile). Per wave and tile, on v_mfma_f32_32x32x2_f32 (one fp32
-// element of each operand per lane, k = lane / 32):
+// Two kernels. prefill_f32_kernel: one workgroup = 4 waves x 32 query rows of
+// one (b, h); K/V tiles of 32 keys, double-buffered in LDS (register-staged
+// loads, one barrier per tile). prefill_f32_split_kernel (launches with fewer
+// 128-row tiles than CUs): one workgroup per pair of 32-row query blocks, its
+// 4 waves splitting the pair's key tiles and merging their softmax states
+// (described at the kernel). Per wave and tile, both on
+// v_mfma_f32_32x32x2_f32 (one fp32 element of each operand per lane,
+// k = lane / 32):
 //   S^T[32 keys x 32 q] = K Q^T   over D/2 steps; lane half h contracts
-//     head-dim elements (D/2) h + step, so a lane's K row and Q row are read
-//     as contiguous float4s;
+//     head-dim elements (D/2) h + step (the split kernel: 8 j + 4 h + c at
+//     step 4 j + c), so a lane's K row and Q row are read as float4s;
 //   O^T[D x 32 q] += V^T P^T       over 16 steps of two keys.
 // Key permutation: accumulator register r of lane half h holds S^T row
 // 8 (r/4) + 4 h + r%4 (the 32x32 accumulator layout); the A-operand lane for
 // that row reads key 16 h + r, so register r of half h is exactly the PV
 // B-operand element for key 16 h + r at step r: P never leaves its registers.
-// LDS: K row-major with row stride D + 4 floats, V transposed ([D][32 keys])
-// with row stride 36 floats; both make the float4 operand reads of a 16-lane
-// group hit 16 distinct 4-bank groups.
+// LDS (prefill_f32_kernel): K row-major with row stride D + 4 floats, V
+// transposed ([D][32 keys]) with row stride 36 floats; both make the float4
+// operand reads of a 16-lane group hit 16 distinct 4-bank groups.
 #include "common.h"
 #include "launch.h"
 
