@@ -162,6 +162,25 @@ def test_split_key_walk_f32(dev, head_dim, is_causal, b, hq, hkv, s):
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("is_causal", [False, True])
+@pytest.mark.parametrize("s", [300, 1111])
+def test_zero_scale_is_running_mean_f32(dev, head_dim, is_causal, s):
+    """softmax_scale = 0 weighs every visible key equally: row i is the mean
+    of V over keys 0..i (causal) or over all keys, a closed form that needs
+    no oracle; every logit is 0, so the split walk's running max never
+    rises after its first tile."""
+    q, k, v = qkv(2, 3, s, head_dim, F32, dev)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal, softmax_scale=0.0)
+    torch.cuda.synchronize()
+    v64 = v.double()
+    if is_causal:
+        ref = v64.cumsum(2) / torch.arange(1, s + 1, device=dev, dtype=torch.float64)[:, None]
+    else:
+        ref = v64.mean(2, keepdim=True).expand_as(v64)
+    assert_close(to_np(out), to_np(ref), **TOL_F32, name=f"zero scale s={s}")
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
 def test_full_grid_noncausal_f32(dev, head_dim):
     """A non-causal grid with a 128-row tile for every CU and more (2 x 16
     heads x 9 tiles): the unsplit kernel, sampled heads."""
