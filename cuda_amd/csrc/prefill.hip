@@ -364,12 +364,20 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   // pair, exact in fp32), so the weights of a row sum to exactly 1: its
   // wide-range data gives peaked rows, where normalising by the unrounded
   // sum would leave the dominant key's rounding (2^-9 of |v|) in the output.
+  // On a masked tile a masked logit gets weight 0 directly: its exponent
+  // kMaskVal * scale_log2 - msub is -inf for every nonzero scale, but NaN for
+  // scale 0 (softmax_scale = 0: equal weights for the visible keys).
   float psum[2];
-  auto exp_pair = [&](int p) CA_INLINE {
+  auto exp_pair = [&](int p, auto mask_tag) CA_INLINE {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int kk = p >> 2, j = p & 3;
     const int i0 = 8 * kk + 2 * j;
-    const float p0 = fast_exp2(__builtin_fmaf(sv[i0], scale_log2, -msub));
-    const float p1 = fast_exp2(__builtin_fmaf(sv[i0 + 1], scale_log2, -msub));
+    float p0 = fast_exp2(__builtin_fmaf(sv[i0], scale_log2, -msub));
+    float p1 = fast_exp2(__builtin_fmaf(sv[i0 + 1], scale_log2, -msub));
+    if constexpr (MASK) {
+      p0 = sv[i0] == kMaskVal ? 0.f : p0;
+      p1 = sv[i0 + 1] == kMaskVal ? 0.f : p1;
+    }
     const typename Tr::vec2 pk = Tr::pack2(p0, p1);
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
@@ -379,9 +387,9 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     else
       psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
   };
-  auto exp_all = [&]() CA_INLINE {
+  auto exp_all = [&](auto mask_tag) CA_INLINE {
 #pragma unroll
-    for (int p = 0; p < 16; ++p) exp_pair(p);
+    for (int p = 0; p < 16; ++p) exp_pair(p, mask_tag);
   };
   // copy logit pair p (logits 2p, 2p+1) out of the accumulators into sv
   // (masked if MASK: a masked logit becomes the value whose exponential is 0)
@@ -407,7 +415,8 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   // running max, lazy O rescale, exponent offset for the tile now in sv
   auto settle_max = [&]() CA_INLINE {
     const float t2 = POS ? __builtin_fmaxf(tm[0], tm[1]) : __builtin_fminf(tm[0], tm[1]);
-    const float tmax = pair32_max(t2 * scale_log2);
+    // a row all masked in this tile has no max (also for scale 0)
+    const float tmax = pair32_max(t2 == kMaskVal ? kNegInf : t2 * scale_log2);
     if (__builtin_expect(wave_any(tmax > m_run + 8.0f), 0)) {  // rare: the max rose by > 2^8
       acc_gap();
       const float m_new = __builtin_fmaxf(m_run, tmax);
@@ -429,7 +438,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
       fold_max(p);
     }
     settle_max();
-    exp_all();
+    exp_all(mask_tag);
     l_run += psum[0] + psum[1];
   };
   // Softmax step of a tile after the wave's first, without its row max: the
@@ -444,13 +453,13 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   auto stale_softmax = [&](int tn, auto mask_tag) CA_INLINE {
 #pragma unroll
     for (int p = 0; p < 16; ++p) copy_pair(p, tn * kBN, mask_tag);
-    exp_all();
+    exp_all(mask_tag);
     if (__builtin_expect(wave_any(!(psum[0] + psum[1] <= kStaleMax)), 0)) {
       tm[0] = tm[1] = kMaskVal;
 #pragma unroll
       for (int p = 0; p < 16; ++p) fold_max(p);
       settle_max();
-      exp_all();
+      exp_all(mask_tag);
     }
     l_run += psum[0] + psum[1];
   };

@@ -66,6 +66,27 @@ def test_ragged_lengths(dev, seq_len, is_causal):
     assert_close(to_np(out), ref, **TOL_16BIT, name=f"S={seq_len}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_zero_scale_is_running_mean(dev, dtype, head_dim, is_causal):
+    """softmax_scale = 0 weighs every visible key equally: row i is the mean
+    of V over keys 0..i (causal) or over all keys, a closed form that needs
+    no oracle. Every weight is exactly 1 in the P operand, so only the fp32
+    sums and the output rounding separate the kernels from it; 8 x 8 heads
+    of 2100 rows give the persistent launch several items per workgroup."""
+    q, k, v = qkv(8, 8, 2100, head_dim, dtype, dev)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal, softmax_scale=0.0)
+    torch.cuda.synchronize()
+    v64 = v.double()
+    s = v.shape[2]
+    if is_causal:
+        ref = v64.cumsum(2) / torch.arange(1, s + 1, device=dev, dtype=torch.float64)[:, None]
+    else:
+        ref = v64.mean(2, keepdim=True).expand_as(v64)
+    assert_close(to_np(out), ref.cpu().numpy(), **TOL_16BIT, name=f"zero scale {dtype}")
+
+
 def test_custom_scale_and_large_logits(dev):
     """Scaled-up queries drive the lazy-rescale path (row max jumps by > 8 in
     log2 units between tiles)."""
