@@ -94,6 +94,33 @@ def test_forward_lse(dev, dtype, head_dim, hq, hkv, s, is_causal):
     assert torch.equal(out, plain)  # the LSE store does not change O
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_zero_scale_closed_forms(dev, dtype, head_dim, is_causal):
+    """softmax_scale = 0, end to end through the kernels' own forward (with
+    LSE) and backward, against closed forms that need no oracle: P[i, j] =
+    1 / n_i over the n_i visible keys of row i, so O = that running mean of
+    V, LSE = ln n_i, dV = P^T dO, and dQ = dK = 0 (every logit gradient is
+    multiplied by the scale)."""
+    s = 300
+    q, k, v = qkv(1, 2, s, head_dim, dtype, dev)
+    dout = torch.randn(1, 2, s, head_dim, device=dev).to(dtype)
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal, softmax_scale=0.0)
+    dq, dk, dv = cuda_llm.flash_attention_backward(dout, q, k, v, out, lse, is_causal=is_causal,
+                                                   softmax_scale=0.0)
+    torch.cuda.synchronize()
+    n = torch.arange(1, s + 1, device=dev, dtype=torch.float64) if is_causal else \
+        torch.full((s,), float(s), device=dev, dtype=torch.float64)
+    p = (torch.tril(torch.ones(s, s, device=dev, dtype=torch.float64)) if is_causal else
+         torch.ones(s, s, device=dev, dtype=torch.float64)) / n[:, None]
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert (out.double() - p @ v.double()).abs().max() <= tol
+    assert (lse.double() - torch.log(n)).abs().max() <= 1e-4
+    assert (dv.double() - p.t() @ dout.double()).abs().max() <= (1e-3 if dtype == torch.float32 else 5e-2)
+    assert torch.count_nonzero(dq) == 0 and torch.count_nonzero(dk) == 0
+
+
 def test_forward_lse_float32(dev):
     q, k, v = qkv(2, 4, 300, 128, torch.float32, dev)
     _, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=True)
