@@ -101,6 +101,64 @@ def test_fp8_cache_as_float8_dtype(dev):
     assert_close(to_np(out), ref, **TOL_FP8, name="float8 dtype")
 
 
+def _paged_value_mean(case, hq):
+    """Mean of each sequence's visible V rows per query head (zeros for an
+    empty context), from the paged layout [blocks, Hkv, D, page] and, for an
+    FP8 cache, its e4m3 codes times their per-block or per-head scales."""
+    vc = case["value_cache"]
+    fp8 = "v_scale" in case
+    lens = case["context_lens"].tolist()
+    tables = case["block_tables"]
+    hkv, d, page = vc.shape[1], vc.shape[2], vc.shape[3]
+    out = torch.zeros(len(lens), hq, d, dtype=torch.float64, device=vc.device)
+    for i, n in enumerate(lens):
+        if n <= 0:
+            continue
+        t = torch.arange(n, device=vc.device)
+        blk = tables[i, t // page].long()
+        x = vc[blk, :, :, t % page]  # [n, Hkv, D]
+        if fp8:
+            x = x.view(torch.float8_e4m3fn).double()
+            vs = case["v_scale"]
+            x = x * (vs[blk][:, :, None] if vs.dim() == 2 else vs[None, :, None]).double()
+        out[i] = x.double().mean(0).repeat_interleave(hq // hkv, dim=0)
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_zero_scale_is_value_mean(dev, dtype, fp8):
+    """softmax_scale = 0: every visible token weighs the same, so each head's
+    output is the mean of its sequence's V rows; a closed form that needs no
+    oracle, over split-K lengths and an empty context."""
+    lens = [0, 1, 17, 1030, 3000]
+    case = build_paged(lens, 8, 2, 128, dtype, dev, fp8=fp8)
+    args = (case["query"], case["key_cache"], case["value_cache"])
+    if fp8:
+        out = cuda_llm.fp8_paged_attention_forward(*args, case["k_scale"], case["v_scale"],
+                                                   case["block_tables"], case["context_lens"],
+                                                   softmax_scale=0.0)
+    else:
+        out = cuda_llm.paged_attention_forward(*args, case["block_tables"], case["context_lens"],
+                                               softmax_scale=0.0)
+    torch.cuda.synchronize()
+    ref = _paged_value_mean(case, 8)
+    tol = 1e-4 if dtype == torch.float32 else TOL_16BIT["max_abs"]
+    assert (out.double() - ref).abs().max() <= tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_zero_scale_is_value_mean(dev, dtype):
+    q = torch.randn(2, 8, 1, 128, device=dev).to(dtype)
+    k = torch.randn(2, 2, 2500, 128, device=dev).to(dtype)
+    v = torch.randn(2, 2, 2500, 128, device=dev).to(dtype)
+    out = cuda_llm.flash_decode(q, k, v, softmax_scale=0.0)
+    torch.cuda.synchronize()
+    ref = v.double().mean(2, keepdim=True).repeat_interleave(4, dim=1)
+    tol = 1e-4 if dtype == torch.float32 else TOL_16BIT["max_abs"]
+    assert (out.double() - ref).abs().max() <= tol
+
+
 def test_golden_paged(dev):
     g = np.load(GOLDEN, allow_pickle=False)
     c = {k.split("/", 1)[1]: g[k] for k in g.files if k.startswith("paged_d64/")}
