@@ -98,6 +98,22 @@ def test_mx_scale_formats_agree(dev):
     assert torch.equal(a, b) and torch.equal(a, c)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_mx_zero_scale_is_running_mean(dev, causal):
+    """softmax_scale = 0: O is the running mean (causal) or the mean of the
+    dequantised V rows, a closed form that needs no oracle."""
+    x = mx_inputs(1, 2, 700, 128, dev)
+    out = _run(x, causal, softmax_scale=0.0)
+    torch.cuda.synchronize()
+    v = torch.from_numpy(_ref(x)["v"]).to(dev).double()
+    s = v.shape[2]
+    if causal:
+        ref = v.cumsum(2) / torch.arange(1, s + 1, device=dev, dtype=torch.float64)[:, None]
+    else:
+        ref = v.mean(2, keepdim=True).expand_as(v)
+    assert_close(to_np(out), ref.cpu().numpy(), **TOL_FP8, name=f"mx zero scale causal={causal}")
+
+
 def test_mx_fp16_output(dev):
     x = mx_inputs(1, 2, 64, 128, dev, seed=4)
     out = _run(x, False, out_dtype=torch.float16)
