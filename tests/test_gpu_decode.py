@@ -159,6 +159,32 @@ def test_decode_zero_scale_is_value_mean(dev, dtype):
     assert (out.double() - ref).abs().max() <= tol
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_negative_scale(dev, fp8):
+    """A negative softmax_scale through the paged kernels, against the oracle."""
+    case = build_paged([1, 17, 1030, 3000], 8, 2, 128, torch.bfloat16, dev, fp8=fp8)
+    args = (case["query"], case["key_cache"], case["value_cache"])
+    if fp8:
+        out = cuda_llm.fp8_paged_attention_forward(*args, case["k_scale"], case["v_scale"],
+                                                   case["block_tables"], case["context_lens"],
+                                                   softmax_scale=-0.1)
+    else:
+        out = cuda_llm.paged_attention_forward(*args, case["block_tables"], case["context_lens"],
+                                               softmax_scale=-0.1)
+    torch.cuda.synchronize()
+    lens = case["context_lens"].cpu().numpy()
+    tables = case["block_tables"].cpu().numpy()
+    if fp8:
+        ref = oracle.paged_decode(to_np(case["query"]), case["key_cache"].cpu().numpy(),
+                                  case["value_cache"].cpu().numpy(), tables, lens, scale=-0.1,
+                                  k_scale=case["k_scale"].cpu().numpy(),
+                                  v_scale=case["v_scale"].cpu().numpy())
+    else:
+        ref = oracle.paged_decode(to_np(case["query"]), to_np(case["key_cache"]),
+                                  to_np(case["value_cache"]), tables, lens, scale=-0.1)
+    assert_close(to_np(out), ref, **(TOL_FP8 if fp8 else TOL_16BIT), name=f"negative scale fp8={fp8}")
+
+
 def test_golden_paged(dev):
     g = np.load(GOLDEN, allow_pickle=False)
     c = {k.split("/", 1)[1]: g[k] for k in g.files if k.startswith("paged_d64/")}

@@ -87,6 +87,20 @@ def test_zero_scale_is_running_mean(dev, dtype, head_dim, is_causal):
     assert_close(to_np(out), ref.cpu().numpy(), **TOL_16BIT, name=f"zero scale {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_negative_scale(dev, dtype, head_dim, is_causal):
+    """A negative softmax_scale (the kernels' second instantiation, which
+    tracks a running minimum of the raw logits) against the oracle, over
+    ragged and multi-tile walks."""
+    q, k, v = qkv(2, 4, 777, head_dim, dtype, dev)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal, softmax_scale=-0.15)
+    torch.cuda.synchronize()
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=is_causal, scale=-0.15)
+    assert_close(to_np(out), ref, **TOL_16BIT, name=f"negative scale {dtype}")
+
+
 def test_custom_scale_and_large_logits(dev):
     """Scaled-up queries drive the lazy-rescale path (row max jumps by > 8 in
     log2 units between tiles)."""
