@@ -87,6 +87,25 @@ def test_zero_scale_is_running_mean(dev, dtype, head_dim, is_causal):
     assert_close(to_np(out), ref.cpu().numpy(), **TOL_16BIT, name=f"zero scale {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_long_ragged_sequence_zero_scale(dev, dtype, is_causal):
+    """One head of 65573 rows (a ragged end far past the sizes the oracle
+    checks): with softmax_scale = 0 the output is the running mean of V,
+    checked on every row."""
+    s = 65573
+    q, k, v = qkv(1, 1, s, 128, dtype, dev)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal, softmax_scale=0.0)
+    torch.cuda.synchronize()
+    v64 = v.double()
+    if is_causal:
+        ref = v64.cumsum(2) / torch.arange(1, s + 1, device=dev, dtype=torch.float64)[:, None]
+    else:
+        ref = v64.mean(2, keepdim=True).expand_as(v64)
+    tol = 1e-4 if dtype == torch.float32 else TOL_16BIT["max_abs"]
+    assert (out.double() - ref).abs().max().item() <= tol
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("is_causal", [False, True])
