@@ -121,6 +121,36 @@ def test_zero_scale_closed_forms(dev, dtype, head_dim, is_causal):
     assert torch.count_nonzero(dq) == 0 and torch.count_nonzero(dk) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("is_causal", [False, True])
+def test_zero_scale_long_ragged(dev, dtype, is_causal):
+    """The zero-scale closed forms at a ragged length of 8197 rows, far past
+    the sizes the oracle checks, without forming P: O is the running mean of
+    V, LSE = ln n_i, dV[j] = sum over the rows i that see key j of
+    dO[i] / n_i (a reversed cumulative sum when causal), dQ = dK = 0."""
+    s, d = 8197, 128
+    q, k, v = qkv(1, 1, s, d, dtype, dev)
+    dout = torch.randn(1, 1, s, d, device=dev).to(dtype)
+    out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal, softmax_scale=0.0)
+    dq, dk, dv = cuda_llm.flash_attention_backward(dout, q, k, v, out, lse, is_causal=is_causal,
+                                                   softmax_scale=0.0)
+    torch.cuda.synchronize()
+    v64, g64 = v.double()[0, 0], dout.double()[0, 0]
+    if is_causal:
+        n = torch.arange(1, s + 1, device=dev, dtype=torch.float64)
+        o_ref = v64.cumsum(0) / n[:, None]
+        dv_ref = (g64 / n[:, None]).flip(0).cumsum(0).flip(0)
+    else:
+        n = torch.full((s,), float(s), device=dev, dtype=torch.float64)
+        o_ref = v64.mean(0, keepdim=True).expand(s, d)
+        dv_ref = g64.sum(0, keepdim=True).expand(s, d) / s
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert (out.double()[0, 0] - o_ref).abs().max() <= tol
+    assert (lse.double()[0, 0] - torch.log(n)).abs().max() <= 1e-4
+    assert (dv.double()[0, 0] - dv_ref).abs().max() <= (1e-3 if dtype == torch.float32 else 5e-2)
+    assert torch.count_nonzero(dq) == 0 and torch.count_nonzero(dk) == 0
+
+
 def test_forward_lse_float32(dev):
     q, k, v = qkv(2, 4, 300, 128, torch.float32, dev)
     _, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=True)

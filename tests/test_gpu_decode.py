@@ -147,6 +147,25 @@ def test_paged_zero_scale_is_value_mean(dev, dtype, fp8):
     assert (out.double() - ref).abs().max() <= tol
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_paged_zero_scale_long_context(dev, fp8):
+    """A 70001-token context (4376 pages: 35 FP8 or 69 16-bit splits merged)
+    beside a short one, against the closed-form value mean of softmax_scale
+    = 0."""
+    case = build_paged([70001, 5], 8, 2, 128, torch.bfloat16, dev, fp8=fp8)
+    args = (case["query"], case["key_cache"], case["value_cache"])
+    if fp8:
+        out = cuda_llm.fp8_paged_attention_forward(*args, case["k_scale"], case["v_scale"],
+                                                   case["block_tables"], case["context_lens"],
+                                                   softmax_scale=0.0)
+    else:
+        out = cuda_llm.paged_attention_forward(*args, case["block_tables"], case["context_lens"],
+                                               softmax_scale=0.0)
+    torch.cuda.synchronize()
+    ref = _paged_value_mean(case, 8)
+    assert (out.double() - ref).abs().max() <= TOL_16BIT["max_abs"]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_decode_zero_scale_is_value_mean(dev, dtype):
     q = torch.randn(2, 8, 1, 128, device=dev).to(dtype)
