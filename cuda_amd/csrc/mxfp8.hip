@@ -42,48 +42,56 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
   return __uint_as_float(e << 23);
 }
 
-// One lane per 16 codes (8 lanes per row of D = 128; a 16-byte load and two
-// 16-byte stores): V row -> bf16 row; with float scales (F32SC) lanes
-// 8r..8r+3 of each row also convert q's, k's scale of block (lane % 8) into
-// e8m0 bytes and any invalid scale raises *bad. (8 codes per lane ran C5's
-// 50 MB of traffic at ~3.5 TB/s.)
+// One wave per 8 rows of V (1024 codes -> 2 KB of bf16): lane l converts
+// codes 8l .. 8l + 7 and 512 + 8l .. 512 + 8l + 7 of the wave's rows, so every
+// load instruction reads one contiguous 512 B and every store instruction
+// writes one contiguous 1 KB. (16 codes per lane, two 16-byte stores 32 bytes
+// apart, ran C5's 50 MB at ~3.4 TB/s.) With float scales (F32SC) lane l also
+// converts one of the rows' q or k scales (row l / 8, block l % 4; q when
+// (l / 4) % 2 == 0) into e8m0, and any invalid scale raises *bad.
 template <bool F32SC>
 __global__ __launch_bounds__(256) void mx_prepare_kernel(
     const uint8_t* __restrict__ V, const void* __restrict__ VS, const void* __restrict__ QSf,
     const void* __restrict__ KSf, uint16_t* __restrict__ Vb, uint8_t* __restrict__ QSb,
     uint8_t* __restrict__ KSb, uint32_t* __restrict__ bad, long long n_rows) {
   constexpr int D = 128, NB = D / 32;
-  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long row = gid >> 3;
-  const int part = (int)(gid & 7);
-  if (row >= n_rows) return;
-  const int blk = part >> 1;  // MX block of the lane's 16 codes
-  float sc;
+  const int lane = threadIdx.x & 63;
+  const long long row0 = (((long long)blockIdx.x * 256 + threadIdx.x) >> 6) * 8;
+  if (row0 >= n_rows) return;
   bool ok = true;
   if (F32SC) {
-    uint32_t e;
-    ok = float_to_e8m0(((const float*)VS)[row * NB + blk], &e);
-    sc = e8m0_to_float(e);
-    if (part < NB) {
-      uint32_t eq, ek;
-      ok &= float_to_e8m0(((const float*)QSf)[row * NB + part], &eq);
-      ok &= float_to_e8m0(((const float*)KSf)[row * NB + part], &ek);
-      QSb[row * NB + part] = (uint8_t)eq;
-      KSb[row * NB + part] = (uint8_t)ek;
+    const long long r = row0 + (lane >> 3);
+    const int blk = lane & 3;
+    if (r < n_rows) {
+      const bool isq = ((lane >> 2) & 1) == 0;
+      uint32_t e;
+      ok = float_to_e8m0(((const float*)(isq ? QSf : KSf))[r * NB + blk], &e);
+      (isq ? QSb : KSb)[r * NB + blk] = (uint8_t)e;
     }
-    if (!ok) *bad = 1u;  // every writer stores the same value
-  } else {
-    sc = e8m0_to_float(((const uint8_t*)VS)[row * NB + blk]);
   }
-  const u32x4 c = *(const u32x4*)(V + row * D + 16 * part);
-  u32x4 w[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i >> 1][2 * (i & 1)] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(c[i], sc));
-    w[i >> 1][2 * (i & 1) + 1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(c[i], sc));
+  for (int h = 0; h < 2; ++h) {
+    const long long c = row0 * D + 512 * h + 8 * lane;  // the lane's first code
+    const long long r = row0 + 4 * h + (lane >> 4);
+    if (r >= n_rows) continue;
+    const int blk = (lane & 15) >> 2;  // MX block of the 8 codes
+    float sc;
+    if (F32SC) {
+      uint32_t e;
+      ok &= float_to_e8m0(((const float*)VS)[r * NB + blk], &e);
+      sc = e8m0_to_float(e);
+    } else {
+      sc = e8m0_to_float(((const uint8_t*)VS)[r * NB + blk]);
+    }
+    const u32x2 cc = *(const u32x2*)(V + c);
+    u32x4 w;
+    w[0] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[0], sc));
+    w[1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[0], sc));
+    w[2] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[1], sc));
+    w[3] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[1], sc));
+    *(u32x4*)(Vb + c) = w;
   }
-  *(u32x4*)(Vb + row * D + 16 * part) = w[0];
-  *(u32x4*)(Vb + row * D + 16 * part + 8) = w[1];
+  if (F32SC && !ok) *bad = 1u;  // every writer stores the same value
 }
 
 __global__ void mx_clear_flag_kernel(uint32_t* flag) { *flag = 0u; }
@@ -113,7 +121,7 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
   w += align256((size_t)rows * D * 2);
   const uint8_t* qs8 = (const uint8_t*)qs;
   const uint8_t* ks8 = (const uint8_t*)ks;
-  const long long blocks = (rows * 8 + 255) / 256;
+  const long long blocks = (rows + 31) / 32;  // 4 waves of 8 rows per block
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   if (scale_kind == 1) {
     uint8_t* qsb = w;
