@@ -111,13 +111,18 @@ struct PfGeom {
 
 constexpr int kPfRows = 256;   // query rows per workgroup
 constexpr int kPfWaves = 8;    // waves per workgroup (32 query rows each)
-constexpr int kPfStages = 4;   // K/V tiles in the LDS ring (32 KB each at D = 128)
+constexpr int kPfStages = 4;   // K/V tiles in the LDS ring (32 KB each at D = 128; D = 64: 8)
 constexpr int kPfKDepth = 1;   // K fragments read ahead of the QK MFMAs (k-steps)
 constexpr int kPfVDepth = 2;   // V^T fragments read ahead of the PV MFMAs (steps)
-// Key tiles per workgroup barrier: one barrier every two tiles lets a
-// SIMD's two waves drift apart within the pair instead of meeting after
-// every PV (C2 +1.5 % over one barrier per tile, same box).
+// Key tiles per workgroup barrier of the lockstep walk: one barrier every
+// two tiles lets a SIMD's two waves drift apart within the pair instead of
+// meeting after every PV (+1.5 % over one barrier per tile on the 16-bit
+// walk then in use, +3 % on MX, same box). Head dim 64, whose 16 KB tiles
+// let the ring hold eight, takes a barrier every four (+1.7 to +2.4 % on
+// the reference grid's fp16 shapes).
 constexpr int kPfGroup = 2;
+constexpr int pf_stages(int d) { return d == 64 ? 8 : kPfStages; }
+constexpr int pf_group(int d) { return d == 64 ? 4 : kPfGroup; }
 // Ping-pong walk: tile t + kPpAhead is loaded with tile t (its slot held
 // tile t - 2, released by the barrier of tile t).
 constexpr int kPpAhead = 2;
@@ -184,7 +189,8 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   constexpr int kScaleB = MX ? kBN * 4 : 0;                   // K scale words of a tile
   constexpr int kStageB = kKTileB + kVTileB + kScaleB;
   constexpr int kNOB = Gv::kNOB;
-  constexpr int kBM = kPfRows, kStages = kPfStages, kNW = kPfWaves;
+  constexpr int kBM = kPfRows, kStages = pf_stages(D), kNW = kPfWaves;
+  constexpr int kGroup = pf_group(D);
   constexpr int kKL = kKTileB / 1024 / kNW;  // 1 KB K loads per wave per tile
   constexpr int kVL = kVTileB / 1024 / kNW;  // 1 KB V loads per wave per tile
   constexpr int kSL = MX ? 1 : 0;            // scale loads (every wave loads the same 256 B)
@@ -465,11 +471,12 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   };
 
   // S^T(tn) = K(tn) Q^T, K fragments kPfKDepth steps ahead of the MFMAs.
-  // The wave's loads of tile tn + kStages - kPfGroup go out between its QK
+  // The wave's loads of tile tn + kStages - kGroup go out between its QK
   // steps, one after every kQkSteps / kLoads of them: issued all at once
   // after the barrier, the 8 waves' loads queue behind each other (C2
   // +1.8 %).
-  constexpr int kAhead = kStages - kPfGroup;
+  constexpr int kAhead = kStages - kGroup;
+  static_assert(kAhead >= kGroup, "a barrier group's tiles are issued before its barrier");
   auto qk = [&](int tn) CA_INLINE {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
@@ -781,14 +788,15 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     for (int tt = 0; tt < kAhead; ++tt) issue(tt);
     load_q_raw(bh, qt);
     fix_q();
-    // Barrier at tile t (t % kPfGroup == 0): every wave has its loads of tiles
-    // t .. t + kPfGroup - 1 resident and is past its last read of tile t - 1,
-    // so the slots of tiles t - kPfGroup .. t - 1 take tiles t + kAhead ..
+    // Barrier at tile t (t % kGroup == 0): every wave has its loads of tiles
+    // t .. t + kGroup - 1 resident and is past its last read of tile t - 1,
+    // so the slots of tiles t - kGroup .. t - 1 take tiles t + kAhead ..
     // The wave has issued tiles up to t + kAhead - 1 by then, so the loads of
-    // kAhead - kPfGroup tiles may still be in flight.
+    // kAhead - kGroup tiles may still be in flight (kAhead >= kGroup: the
+    // group's tiles were all issued before its barrier).
     auto sync = [&](int t, bool load_here) CA_INLINE {
-      if (t % kPfGroup == 0) {
-        wait_vmcnt<kLoads * (kAhead - kPfGroup)>();  // this wave's loads of the group landed ...
+      if (t % kGroup == 0) {
+        wait_vmcnt<kLoads * (kAhead - kGroup)>();  // this wave's loads of the group landed ...
         __builtin_amdgcn_s_barrier();                // ... and every wave's
       }
       if (load_here) issue(t + kAhead);
