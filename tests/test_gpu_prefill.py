@@ -88,13 +88,15 @@ def test_zero_scale_is_running_mean(dev, dtype, head_dim, is_causal):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("is_causal", [False, True])
-def test_long_ragged_sequence_zero_scale(dev, dtype, is_causal):
+def test_long_ragged_sequence_zero_scale(dev, dtype, head_dim, is_causal):
     """One head of 65573 rows (a ragged end far past the sizes the oracle
-    checks): with softmax_scale = 0 the output is the running mean of V,
+    checks; 1025 key tiles, so the head-dim-64 walk's groups of four end
+    mid-group): with softmax_scale = 0 the output is the running mean of V,
     checked on every row."""
     s = 65573
-    q, k, v = qkv(1, 1, s, 128, dtype, dev)
+    q, k, v = qkv(1, 1, s, head_dim, dtype, dev)
     out = cuda_llm.flash_attention(q, k, v, is_causal=is_causal, softmax_scale=0.0)
     torch.cuda.synchronize()
     v64 = v.double()
