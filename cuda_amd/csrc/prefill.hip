@@ -12,10 +12,11 @@
 //   launch, one workgroup per CU) every grid-th such item in turn;
 //   each wave owns 32 query rows for the whole KV walk;
 //   KV tiles of 64 keys travel HBM -> LDS by buffer loads into a ring of 4
-//   tiles shared by the 8 waves; the two waves of a SIMD run the ping-pong
-//   walk (16-bit head dim 128: one waits at the per-tile barrier before its
-//   MFMA block, the other after it, so one's softmax runs under the other's
-//   MFMAs) or the lockstep walk (head dim 64, MX: one barrier per two tiles).
+//   tiles (8 at head dim 64) shared by the 8 waves; the two waves of a SIMD
+//   run the ping-pong walk (16-bit head dim 128: one waits at the per-tile
+//   barrier before its MFMA block, the other after it, so one's softmax runs
+//   under the other's MFMAs) or the lockstep walk (MX: one barrier per two
+//   tiles; head dim 64: per four).
 // Per wave and KV tile (32x32x16 MFMAs):
 //   S^T[64 keys x 32 q] = K Q^T   (A = K rows from LDS, B = Q from registers)
 //   softmax over keys: keys live in the registers of a lane (16 per 32-key
