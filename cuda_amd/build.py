@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcuda_llm_amd.so")
-SOURCES = ["prefill.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "backward_f32.hip",
+SOURCES = ["prefill.hip", "prefill_w64.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "backward_f32.hip",
            "kv_append.hip", "rope.hip", "stream_read.hip", "abi.cpp"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 
@@ -41,9 +41,26 @@ EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
          "f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
+# Generated sources: the 64-row prefill's kernel body (hand-scheduled
+# assembly, checked for hazards by its generator) is written into the build
+# directory before the compile.
+GENERATED = {"prefill_w64.hip": ("gen_prefill_w64.py", "prefill_w64_body.inc")}
+
+
+def _generate(src):
+    gen, out = GENERATED[src]
+    r = subprocess.run([sys.executable, os.path.join(CSRC, gen), os.path.join(BUILD, out)],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{gen} failed:\n{r.stderr}")
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    if src in GENERATED:
+        _generate(src)
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-I", BUILD, "-x", "hip", "-c", os.path.join(CSRC, src),
+           "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

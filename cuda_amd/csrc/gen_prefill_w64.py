@@ -1,0 +1,1666 @@
+#!/usr/bin/env python3
+"""Generator of the 64-row prefill kernel body: hand-scheduled gfx950 assembly.
+
+The 16-bit head-dim-128 prefill (`prefill_w64.hip`) runs one wave per SIMD,
+64 query rows per wave. In the steady state each iteration issues 64
+v_mfma_f32_32x32x16_bf16 (PV of the previous key tile, QK of the next) and
+between them the whole softmax of the current tile, so the wave's own MFMAs
+hide its VALU work, and every K/V fragment read from LDS feeds two MFMAs.
+That walk needs O^T and Q in AGPRs and S^T, P in VGPRs with no copies; the
+register assignment is fixed here, by hand, and the instruction order with it.
+
+This script writes the kernel body as one string-literal macro per variant
+(causal, non-causal) for an inline-asm statement, plus the clobber list. It
+also checks its own output before writing it:
+
+* hazards: a forward dataflow over the body's control-flow graph tracks, for
+  every register, the wait states since its last MFMA / VALU / transcendental
+  / permlane write and since MFMA reads of it, and rejects any instruction
+  closer than the gfx950 requirement (taken conservatively: the 16-pass
+  figures of the MFMA tables, which are longer than what the 8-pass
+  32x32x16 needs);
+* counters: the LDS and vector-memory operations in flight are tracked in
+  order, and a use of a register whose load has not been waited on by an
+  s_waitcnt is rejected; at a control-flow join the in-flight lists of all
+  predecessors must agree.
+
+Usage: gen_prefill_w64.py OUT.inc
+"""
+import sys
+
+# ---------------------------------------------------------------------------
+# operands
+# ---------------------------------------------------------------------------
+
+
+class Reg:
+    """Contiguous register range: file 'v', 'a' or 's', first index, count."""
+
+    __slots__ = ("f", "i", "n")
+
+    def __init__(self, f, i, n=1):
+        self.f, self.i, self.n = f, i, n
+
+    def __str__(self):
+        return f"{self.f}{self.i}" if self.n == 1 else f"{self.f}[{self.i}:{self.i + self.n - 1}]"
+
+    def __getitem__(self, k):
+        assert 0 <= k < self.n, (self, k)
+        return Reg(self.f, self.i + k)
+
+    def sl(self, k, n):
+        assert 0 <= k and k + n <= self.n, (self, k, n)
+        return Reg(self.f, self.i + k, n)
+
+    def keys(self):
+        return [(self.f, self.i + j) for j in range(self.n)]
+
+
+class Sym:
+    """An operand of the inline-asm statement (a compiler-placed register)."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __str__(self):
+        return "%[" + self.name + "]"
+
+    def keys(self):
+        return [("in", self.name)]
+
+
+class Spec:
+    """vcc, m0, scc."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __str__(self):
+        return self.name
+
+    def keys(self):
+        return [("x", self.name)]
+
+
+VCC, M0 = Spec("vcc"), Spec("m0")
+
+
+def _keys(x):
+    return x.keys() if hasattr(x, "keys") and not isinstance(x, dict) else []
+
+
+def _txt(x):
+    if isinstance(x, int):
+        return hex(x) if (x < -16 or x > 64) else str(x)
+    return str(x)
+
+
+# ---------------------------------------------------------------------------
+# instructions
+# ---------------------------------------------------------------------------
+
+
+class Ins:
+    __slots__ = ("kind", "text", "defs", "uses", "ws", "mdst", "mc", "mab", "mem", "wvm", "wlgkm",
+                 "target", "cond", "trans", "perm", "dot", "m0use", "std", "cost", "frag")
+
+    def __init__(self, kind, text, defs=(), uses=(), **kw):
+        self.kind = kind
+        self.text = text
+        self.defs = [k for r in defs for k in _keys(r)]
+        self.uses = [k for r in uses for k in _keys(r)]
+        self.ws = kw.get("ws", 1)
+        self.mdst = kw.get("mdst")
+        self.mc = kw.get("mc")
+        self.mab = kw.get("mab", [])
+        self.mem = kw.get("mem")        # 'lgkm' or 'vm'
+        self.wvm = kw.get("wvm")
+        self.wlgkm = kw.get("wlgkm")
+        self.target = kw.get("target")
+        self.cond = kw.get("cond", False)
+        self.trans = kw.get("trans", False)
+        self.perm = kw.get("perm", False)
+        self.dot = kw.get("dot", False)
+        self.m0use = kw.get("m0use", False)
+        self.std = kw.get("std", [])
+        self.cost = kw.get("cost", 0)
+        self.frag = None
+
+
+def MFMA(d, a, b, c, op="v_mfma_f32_32x32x16_bf16"):
+    uses = [a, b] + ([c] if c is not None else [])
+    return Ins("mfma", f"{op} {d}, {a}, {b}, {c if c is not None else 0}", defs=[d], uses=uses,
+               mdst=tuple(d.keys()), mc=tuple(c.keys()) if c is not None else None,
+               mab=a.keys() + b.keys())
+
+
+def V(op, d, *s, trans=False, perm=False):
+    """VALU instruction; d may be a Reg, VCC or an SGPR pair (v_cmp)."""
+    ops = ", ".join(_txt(x) for x in ([d] if d is not None else []) + list(s))
+    defs = [d] if d is not None else []
+    uses = list(s)
+    if perm:
+        uses = uses + [d]
+        defs = defs + list(s)
+    return Ins("valu", f"{op} {ops}", defs=defs, uses=uses, trans=trans, perm=perm,
+               dot=op.startswith("v_dot2"), cost=12 if trans else 6)
+
+
+def ACCR(d, a):
+    return Ins("valu", f"v_accvgpr_read_b32 {d}, {a}", defs=[d], uses=[a], cost=6)
+
+
+def ACCW(a, s):
+    return Ins("valu", f"v_accvgpr_write_b32 {a}, {_txt(s)}", defs=[a], uses=[s], cost=6)
+
+
+def S(op, d, *s, scc_def=True):
+    ops = ", ".join(_txt(x) for x in ([d] if d is not None else []) + list(s))
+    return Ins("salu", f"{op} {ops}", defs=[d] if d is not None else [], uses=list(s), cost=2)
+
+
+def SLOAD(op, d, base, off):
+    return Ins("smem", f"{op} {d}, {base}, {_txt(off)}", defs=[d], uses=[base], mem="lgkm", cost=2)
+
+
+def DSR(op, d, addr, off=0):
+    t = f"{op} {d}, {addr}" + (f" offset:{off}" if off else "")
+    return Ins("lds", t, defs=[d], uses=[addr], mem="lgkm", cost=4)
+
+
+def DSW(op, addr, data, off=0):
+    t = f"{op} {addr}, {data}" + (f" offset:{off}" if off else "")
+    return Ins("lds", t, defs=[], uses=[addr, data], mem="lgkm", cost=4)
+
+
+def BLOAD(op, d, voff, rsrc, off=0):
+    t = f"{op} {d}, {voff}, {rsrc}, 0 offen" + (f" offset:{off}" if off else "")
+    return Ins("vmem", t, defs=[d], uses=[voff, rsrc], mem="vm", cost=4)
+
+
+def BLOAD_LDS(voff, rsrc):
+    return Ins("vmem", f"buffer_load_dwordx4 {voff}, {rsrc}, 0 offen lds", defs=[], uses=[voff, rsrc, M0],
+               mem="vm", m0use=True, cost=4)
+
+
+def BSTORE(op, data, voff, rsrc, off=0):
+    t = f"{op} {data}, {voff}, {rsrc}, 0 offen" + (f" offset:{off}" if off else "")
+    return Ins("vmem", t, defs=[], uses=[data, voff, rsrc], mem="vm", std=data.keys(), cost=4)
+
+
+def WAIT(vm=None, lgkm=None):
+    parts = []
+    if vm is not None:
+        parts.append(f"vmcnt({vm})")
+    if lgkm is not None:
+        parts.append(f"lgkmcnt({lgkm})")
+    return Ins("wait", "s_waitcnt " + " ".join(parts), wvm=vm, wlgkm=lgkm, cost=1)
+
+
+def NOP(n):
+    assert 0 <= n <= 7
+    return Ins("nop", f"s_nop {n}", ws=n + 1, cost=n + 1)
+
+
+def NOPS(n):
+    """n wait states of s_nop."""
+    out = []
+    while n > 0:
+        k = min(n, 8)
+        out.append(NOP(k - 1))
+        n -= k
+    return out
+
+
+def BAR():
+    return Ins("barrier", "s_barrier", cost=1)
+
+
+def LABEL(name):
+    return Ins("label", f"{name}:", ws=0)
+
+
+def BR(target):
+    return Ins("br", f"s_branch {target}", target=target, cost=1)
+
+
+def CBR(op, target):
+    return Ins("br", f"{op} {target}", target=target, cond=True, cost=1)
+
+
+# ---------------------------------------------------------------------------
+# hazard and counter checker
+# ---------------------------------------------------------------------------
+
+MFMA_WS = 20       # MFMA result -> any other read or write (16-pass figure + gfx950)
+MFMA_SRCC_WAR = 18  # MFMA reads srcC -> VALU overwrites it
+MFMA_AB_WAR = 1     # MFMA reads srcA/B at issue (only srcC has a listed WAR window)
+VALU_TO_MFMA = 3    # VALU write -> MFMA read (2 required)
+TRANS_FWD = 2       # transcendental result -> VALU read (1 required)
+DOT_FWD = 3         # v_dot2 result -> read by any instruction but a v_dot2 accumulating it
+                    # (measured: one instruction between reads the old value, two do not)
+PERM_WS = 4         # around v_permlane32_swap (conservative)
+VALU_SGPR_VMEM = 5  # VALU writes SGPR -> VMEM / SALU reads it
+VALU_SGPR_VALU = 2  # VALU writes SGPR or VCC -> VALU reads it (v_cndmask mask)
+M0_WS = 1           # SALU writes M0 -> LDS DMA
+STORE_DATA = 2      # wide store data -> VALU overwrite
+CAP = 32
+
+
+class CheckError(Exception):
+    pass
+
+
+def _is_vec(k):
+    return k[0] in ("v", "a")
+
+
+def check(prog, name):
+    """Dataflow over `prog` (list of Ins); raises CheckError on a violation."""
+    labels = {ins.text[:-1]: i for i, ins in enumerate(prog) if ins.kind == "label"}
+    n = len(prog)
+    succ = []
+    for i, ins in enumerate(prog):
+        s = []
+        if ins.kind == "br":
+            assert ins.target in labels, f"{name}: unknown label {ins.target}"
+            s.append(labels[ins.target])
+            if ins.cond and i + 1 < n:
+                s.append(i + 1)
+        elif i + 1 < n:
+            s.append(i + 1)
+        succ.append(s)
+
+    # state: (dist dict, lgkm tuple, vm tuple); dist: (cat, key) -> (d, tag)
+    instate = [None] * n
+    instate[0] = ({}, (), ())
+    work = [0]
+    errors = []
+
+    def merge(la, lb):
+        """In-flight lists of two paths, aligned at their most recent end:
+        entry j of the result holds the registers of entry j of either."""
+        if la == lb:
+            return la
+        n_ = max(len(la), len(lb))
+        out = []
+        for j in range(1, n_ + 1):
+            ea = la[-j] if j <= len(la) else frozenset()
+            eb = lb[-j] if j <= len(lb) else frozenset()
+            out.append(ea | eb)
+        return tuple(reversed(out))
+
+    def join(a, b, where):
+        if a is None:
+            return b
+        da, la, va = a
+        db, lb, vb = b
+        la, va = merge(la, lb), merge(va, vb)
+        d = dict(da)
+        for k, (dist, tag) in db.items():
+            if k in d:
+                d0, t0 = d[k]
+                d[k] = (min(d0, dist), t0 if t0 == tag else None)
+            else:
+                d[k] = (dist, tag)
+        return (d, la, va)
+
+    def err(i, msg):
+        errors.append(f"{name}: #{i} `{prog[i].text}`: {msg}")
+
+    def transfer(i, st):
+        ins = prog[i]
+        dist, lg, vm = st
+        g = dist.get
+
+        def dd(cat, k):
+            e = g((cat, k))
+            return e[0] if e else CAP
+
+        # --- counters: uses / defs of registers with loads in flight
+        pend_l = set().union(*lg) if lg else set()
+        pend_v = set().union(*vm) if vm else set()
+        for k in set(ins.uses) | set(ins.defs):
+            if k in pend_l:
+                err(i, f"{k} has an LDS operation in flight")
+            if k in pend_v:
+                err(i, f"{k} has a vector-memory load in flight")
+        # --- hazards
+        if ins.kind == "mfma":
+            for k in ins.uses:
+                if dd("dw", k) < DOT_FWD:
+                    err(i, f"reads {k} {dd('dw', k)} wait states after a v_dot2 wrote it")
+            for k in ins.mab:
+                if dd("mw", k) < MFMA_WS:
+                    err(i, f"srcA/B {k} written by an MFMA {dd('mw', k)} wait states before")
+                if dd("vw", k) < VALU_TO_MFMA:
+                    err(i, f"srcA/B {k} written by VALU {dd('vw', k)} wait states before")
+            for k in (ins.mc or ()):
+                e = g(("mw", k))
+                if e and e[0] < MFMA_WS and e[1] != ins.mdst:
+                    err(i, f"srcC {k} written by a different MFMA {e[0]} wait states before")
+                if dd("vw", k) < VALU_TO_MFMA:
+                    err(i, f"srcC {k} written by VALU {dd('vw', k)} wait states before")
+            for k in ins.mdst:
+                e = g(("mw", k))
+                if e and e[0] < MFMA_WS and e[1] != ins.mdst:
+                    err(i, f"dst {k} written by a different MFMA {e[0]} wait states before")
+                if dd("vw", k) < VALU_TO_MFMA:
+                    err(i, f"dst {k} written by VALU {dd('vw', k)} wait states before")
+        elif ins.kind in ("valu", "lds", "vmem"):
+            for k in ins.uses:
+                if _is_vec(k) and dd("mw", k) < MFMA_WS:
+                    err(i, f"reads {k} {dd('mw', k)} wait states after an MFMA wrote it")
+                if ins.kind == "valu" and not ins.trans and dd("tw", k) < TRANS_FWD:
+                    err(i, f"reads {k} {dd('tw', k)} wait states after a transcendental wrote it")
+                if dd("pw", k) < PERM_WS:
+                    err(i, f"reads {k} {dd('pw', k)} wait states after a permlane wrote it")
+                if not ins.dot and dd("dw", k) < DOT_FWD:
+                    err(i, f"reads {k} {dd('dw', k)} wait states after a v_dot2 wrote it")
+                if ins.perm and dd("vw", k) < PERM_WS:
+                    err(i, f"permlane reads {k} {dd('vw', k)} wait states after a VALU write")
+                if ins.kind in ("vmem", "lds") and k[0] == "s" and dd("vws", k) < VALU_SGPR_VMEM:
+                    err(i, f"memory op reads {k} written by VALU {dd('vws', k)} wait states before")
+                if ins.kind == "valu" and dd("vws", k) < VALU_SGPR_VALU:
+                    err(i, f"VALU reads {k} written by VALU {dd('vws', k)} wait states before")
+            for k in ins.defs:
+                if not _is_vec(k):
+                    continue
+                if dd("mw", k) < MFMA_WS:
+                    err(i, f"overwrites {k} {dd('mw', k)} wait states after an MFMA wrote it")
+                if dd("mrc", k) < MFMA_SRCC_WAR:
+                    err(i, f"overwrites {k} {dd('mrc', k)} wait states after an MFMA read it as srcC")
+                if dd("mrab", k) < MFMA_AB_WAR:
+                    err(i, f"overwrites {k} {dd('mrab', k)} wait states after an MFMA read it")
+                if dd("std", k) < STORE_DATA:
+                    err(i, f"overwrites {k} {dd('std', k)} wait states after a store read it")
+            if ins.m0use and dd("sm0", ("x", "m0")) < M0_WS:
+                err(i, "LDS DMA right after M0 was written")
+        elif ins.kind in ("salu", "smem"):
+            for k in ins.uses:
+                if k[0] == "s" and dd("vws", k) < VALU_SGPR_VMEM:
+                    err(i, f"scalar op reads {k} written by VALU {dd('vws', k)} wait states before")
+
+        # --- advance distances
+        w = ins.ws
+        nd = {}
+        for k, (d0, tag) in dist.items():
+            d1 = d0 + w
+            if d1 < CAP:
+                nd[k] = (d1, tag)
+        if ins.kind == "mfma":
+            for k in ins.mdst:
+                nd[("mw", k)] = (0, ins.mdst)
+            for k in (ins.mc or ()):
+                nd[("mrc", k)] = (0, None)
+            for k in ins.mab:
+                nd[("mrab", k)] = (0, None)
+        elif ins.kind == "valu":
+            for k in ins.defs:
+                nd[("vw", k)] = (0, None)
+                nd.pop(("mw", k), None)   # later reads see this write (its WAW was checked)
+                if ins.trans:
+                    nd[("tw", k)] = (0, None)
+                if ins.perm:
+                    nd[("pw", k)] = (0, None)
+                if ins.dot:
+                    nd[("dw", k)] = (0, None)
+                if k[0] == "s" or k == ("x", "vcc"):
+                    nd[("vws", k)] = (0, None)
+        elif ins.kind == "salu":
+            for k in ins.defs:
+                if k == ("x", "m0"):
+                    nd[("sm0", k)] = (0, None)
+        if ins.kind == "vmem" and ins.std:
+            for k in ins.std:
+                nd[("std", k)] = (0, None)
+        # --- counters
+        if ins.mem == "lgkm":
+            lg = lg + (frozenset(ins.defs),)
+        if ins.mem == "vm":
+            vm = vm + (frozenset(ins.defs),)
+        if ins.kind == "wait":
+            if ins.wlgkm is not None:
+                lg = lg[len(lg) - ins.wlgkm:] if ins.wlgkm < len(lg) else lg
+                if ins.wlgkm == 0:
+                    lg = ()
+            if ins.wvm is not None:
+                vm = vm[len(vm) - ins.wvm:] if ins.wvm < len(vm) else vm
+                if ins.wvm == 0:
+                    vm = ()
+        if len(lg) > 15:
+            # the counter holds 15: an older read could not be waited for exactly
+            if any(lg[:len(lg) - 15]):
+                err(i, "a read is more than 15 LDS operations deep (lgkmcnt saturates)")
+            lg = lg[len(lg) - 15:]
+        if len(vm) > 63:
+            vm = vm[-63:]
+        return (nd, lg, vm)
+
+    iters = 0
+    while work:
+        iters += 1
+        if iters > 200 * n:
+            raise CheckError(f"{name}: checker did not converge")
+        i = work.pop()
+        errs0 = len(errors)
+        out = transfer(i, instate[i])
+        if len(errors) > errs0:
+            raise CheckError("\n".join(errors))
+        for s in succ[i]:
+            new = join(instate[s], out, s)
+            if new != instate[s]:
+                instate[s] = new
+                work.append(s)
+    return True
+
+
+# ---------------------------------------------------------------------------
+# register map
+# ---------------------------------------------------------------------------
+
+
+def v(i, n=1):
+    return Reg("v", i, n)
+
+
+def a(i, n=1):
+    return Reg("a", i, n)
+
+
+def s(i, n=1):
+    return Reg("s", i, n)
+
+
+# VGPRs (v0..v239; v240..v255 hold the compiler-placed per-lane inputs)
+SACC = [[[v(64 * p + 32 * mb + 16 * nb, 16) for nb in range(2)] for mb in range(2)] for p in range(2)]
+PB = [[v(128 + 8 * kk + 4 * nb, 4) for nb in range(2)] for kk in range(4)]
+TMP = [v(160 + 8 * t, 8) for t in range(3)]
+# K / V^T fragments read from LDS: NSLOT slots, each read LOOK fragments (2 LOOK
+# MFMAs) ahead of its first use; slots 4-7 share v224-v239 with SCR, which the
+# steady walk does not use (the output, the first tile's max and the redo path
+# keep their temporaries elsewhere while fragments are in flight).
+NSLOT, LOOK = 8, 6
+FRAG = [v(184 + 4 * t, 4) for t in range(4)] + [v(224 + 4 * t, 4) for t in range(4)]
+MRUN = [v(200), v(201)]
+LRUN = [v(202), v(203)]
+MSUB = [v(204), v(205)]
+PSUM = [[v(206), v(207)], [v(208), v(209)]]
+NINF = v(210)
+KA = v(211)
+KX = v(212)
+VA = [[v(213 + 2 * ob + j) for j in range(2)] for ob in range(4)]   # v213..v220
+DREM = v(221)
+QOFF = [v(222), v(223)]
+SCR = v(224, 16)                                                    # v224..v239
+N_VGPR_OWN = 240
+
+# AGPRs
+OACC = [[a(16 * (2 * ob + nb), 16) for nb in range(2)] for ob in range(4)]
+QA = [[a(128 + 4 * (8 * nb + ks), 4) for ks in range(8)] for nb in range(2)]
+
+# per-lane inputs (placed by the compiler in v240..v255)
+IN_V = ["kofs", "vofs1", "vofs2", "loff0", "loff1", "loff2", "loff3", "qlane", "dl", "h8",
+        "wbase", "wx", "rdl", "stl", "lsel"]
+INV = {nm: Sym(nm) for nm in IN_V}
+
+# SGPRs: kernel arguments
+KARG = dict(QP=s(0, 2), KP=s(2, 2), VP=s(4, 2), OP=s(6, 2), LP=s(8, 2), SEQ=s(10), NQT=s(11),
+            NWORK=s(12), PAIRED=s(13), QSHIFT=s(14), SCALE=s(15), NBH=s(16), NFULL=s(17),
+            HALF=s(18), HQ=s(19), HKV=s(20), MNQT=s(21), SHNQT=s(22), MHALF=s(23), SHHALF=s(24),
+            MHQ=s(25), SHHQ=s(26), MRATIO=s(27), SHRATIO=s(28), XQ=s(29), XR=s(30))
+globals().update(KARG)
+DIVP = s(34, 2)        # 64-bit product of the magic divisions
+RQ = s(36, 4)
+RK = s(40, 4)
+RV = s(44, 4)
+RO = s(48, 4)
+RL = s(52, 4)
+KH = s(56, 2)
+VH = s(58, 2)
+ITEMV, WORK, BH0, QT0, BH1, QT1, BH, QT = (s(60 + j) for j in range(8))
+Q0, KVEND, NT, WT, QW0, KVB, ITER, WOFF = (s(68 + j) for j in range(8))
+T = [s(76 + j) for j in range(8)]
+CMPA = s(84, 2)
+CMPB = s(86, 2)
+ONES, BOUND, PASS, WAVE, GRID, LDSB = (s(88 + j) for j in range(6))
+# Slot bases of the walk's iterations: s31 (the kernel-argument block's pad)
+# and temporaries the query-tile setup uses only before the walk.
+SKRD = s(31)          # K read slot base of the iteration (K tile i + 1)
+SVRD = T[5]           # V slot base of tile i
+SVLD = T[6]           # V load destination (tile i + 2, this wave's quarter)
+SKLD = T[7]           # K load destination (tile i + 4, this wave's quarter)
+N_SGPR_OWN = 94       # s0..s93 (except s32, s33, which the compiler reserves)
+
+IN_S = ["ka", "wg", "ng", "wv", "lb"]
+INS_ = {nm: Sym(nm) for nm in IN_S}
+
+RSRC3 = 0x00020000     # buffer resource word 3: raw 32-bit dwords
+LDS_V = 65536          # V ring offset in LDS
+LDS_STG = 131072       # output staging offset in LDS
+SLOT = 16384           # bytes per K (or V) tile of 64 rows x 256 bytes
+BOUND_F = 0x57800000   # 2^48: the stale-max bound of a tile sum with bf16 P
+LN2 = 0x3F317218
+
+
+# ---------------------------------------------------------------------------
+# building blocks
+# ---------------------------------------------------------------------------
+
+
+def div_magic(dst, x, m, sh):
+    """dst = x / d for 0 <= x < 2^31 (m, sh from the host: magic division)."""
+    return [S("s_mul_i32", DIVP[0], x, m), S("s_mul_hi_u32", DIVP[1], x, m),
+            S("s_lshr_b64", DIVP, DIVP, sh), S("s_mov_b32", dst, DIVP[0])]
+
+
+def rsrc_at(r, head, off_s, size_s):
+    """Resource over bytes [off, size) of the head at `head` (64-bit SGPR
+    pair); off_s, size_s SGPRs (off may exceed size: empty resource)."""
+    return [S("s_add_u32", r[0], head[0], off_s), S("s_addc_u32", r[1], head[1], 0),
+            S("s_and_b32", r[1], r[1], 0xFFFF), S("s_sub_i32", r[2], size_s, off_s),
+            S("s_max_i32", r[2], r[2], 0), S("s_mov_b32", r[3], RSRC3)]
+
+
+def k_frag_reads(f_slot, ks, mb, first_of_ks):
+    """K fragment (ks, mb): one ds_read_b128 of the lane's key row krow + 32 mb,
+    logical 16-byte chunk 2 ks + h (the XOR 32 ks on the lane's base)."""
+    out = []
+    addr = KA if ks == 0 else KX
+    if first_of_ks and ks > 0:
+        out.append(V("v_xor_b32", KX, 32 * ks, KA))
+    out.append(DSR("ds_read_b128", FRAG[f_slot], addr, 8192 * mb))
+    return out
+
+
+def v_frag_reads(f_slot, kk, ob):
+    """V^T fragment (O^T block ob, P^T k-step kk): two ds_read_b64_tr_b16."""
+    return [DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(0, 2), VA[ob][0], 4096 * kk),
+            DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(2, 2), VA[ob][1], 4096 * kk)]
+
+
+class VOp:
+    __slots__ = ("ins", "deps", "nb_gap", "cost", "idx", "done", "emitted_at")
+
+    def __init__(self, ins, deps=(), nb_gap=-1):
+        self.ins = ins if isinstance(ins, list) else [ins]
+        self.deps = list(deps)     # (VOp, min index distance)
+        self.nb_gap = nb_gap       # not before this gap
+        self.cost = sum(x.cost for x in self.ins)
+        self.done = False
+        self.emitted_at = None
+
+
+class Softmax:
+    """The VALU program of one tile's softmax (ops in program order)."""
+
+    def __init__(self):
+        self.ops = []
+
+    def add(self, ins, deps=(), nb_gap=-1):
+        op = VOp(ins, deps, nb_gap)
+        self.ops.append(op)
+        return op
+
+
+def mask_kind(causal, mb, nb):
+    """How the masked tile treats S^T block (mb, nb): causal diagonal tile,
+    key block below the query block 'none', above it 'all', on it 'cmp';
+    the last tile of a non-causal walk (keys >= S) 'cmp'."""
+    if not causal:
+        return "cmp"
+    return {-1: "none", 0: "cmp", 1: "all"}[mb - nb]
+
+
+def mask_cmp(causal, mb, nb, r):
+    """v_cmp setting VCC for the masked logits of S^T block (mb, nb), register
+    r: causal, key > query within the diagonal tile (block on the diagonal);
+    else key >= S. The v_cndmask reading VCC must follow 2 wait states later."""
+    kc = 16 * (r // 8) + (r % 8)
+    if causal:
+        assert mb == nb
+        return V("v_cmp_gt_i32", VCC, kc, INV["dl"])
+    return V("v_cmp_ge_i32", VCC, 32 * mb + kc, DREM)
+
+
+def masked_select(causal, mb, nb, r, dst, src):
+    """dst = src, or -inf where masked (as a bundle)."""
+    kind = mask_kind(causal, mb, nb)
+    if kind == "none":
+        return [V("v_mov_b32", dst, src)] if dst.i != src.i else []
+    if kind == "all":
+        return [V("v_mov_b32", dst, NINF)]
+    return [mask_cmp(causal, mb, nb, r), NOP(VALU_SGPR_VALU - 1), V("v_cndmask_b32", dst, src, NINF, VCC)]
+
+
+def softmax_exp_program(sm, p, masked, causal, kk_release, first_sum_init=True, msub_deps=()):
+    """Exponentials, P and row sums of S^T[p] against MSUB: groups g = (kk, nb).
+    kk_release[kk]: gap from which P[kk] may be overwritten. The row sums add
+    the fp32 exponentials (v_add_f32, chains (nb, e % 2)): a v_dot2 of the
+    packed weights would occupy the matrix pipe (it costs an MFMA ~16
+    cycles each on gfx950)."""
+    last_read = {}    # (g, e): the last op reading group g's temp e
+    last_sum = {}
+    for g in range(8):
+        kk, nb = g // 2, g % 2
+        mb, hf = kk // 2, kk % 2
+        tb = TMP[g % 3]
+        src = SACC[p][mb][nb]
+        fmas, exps = [], []
+        for e in range(8):
+            deps = list(msub_deps)
+            if (g - 3, e) in last_read:
+                deps.append((last_read[(g - 3, e)], 1))
+            if masked and mask_kind(causal, mb, nb) == "all":
+                ins = [V("v_mov_b32", tb[e], NINF)]
+            else:
+                ins = [V("v_fma_f32", tb[e], src[8 * hf + e], SCALE, "-" + str(MSUB[nb]))]
+                ins[0].uses.append(("v", MSUB[nb].i))
+                if masked and mask_kind(causal, mb, nb) == "cmp":
+                    ins += masked_select(causal, mb, nb, 8 * hf + e, tb[e], tb[e])
+            fmas.append(sm.add(ins, deps))
+        for e in range(8):
+            exps.append(sm.add(V("v_exp_f32", tb[e], tb[e], trans=True), [(fmas[e], 1)]))
+        for q in range(4):
+            op = sm.add(V("v_cvt_pk_bf16_f32", PB[kk][nb][q], tb[2 * q], tb[2 * q + 1]),
+                        [(exps[2 * q], TRANS_FWD), (exps[2 * q + 1], TRANS_FWD)], nb_gap=kk_release[kk])
+            last_read[(g, 2 * q)] = last_read[(g, 2 * q + 1)] = op
+        for e in range(8):
+            acc = PSUM[nb][e % 2]
+            init = first_sum_init and kk == 0 and e < 2
+            deps = [(exps[e], TRANS_FWD), (last_read[(g, e)], 1)]
+            if (nb, e % 2) in last_sum:
+                deps.append((last_sum[(nb, e % 2)], 1))
+            op = sm.add(V("v_add_f32", acc, 0 if init else acc, tb[e]), deps)
+            last_sum[(nb, e % 2)] = op
+            last_read[(g, e)] = op
+    return sm
+
+
+STREAM = dict(per_gap=2, exp_last=False, pair_exps=False, fma_lead=1)
+
+
+def stream_softmax(p, kk_release, n_gaps=64, per_gap=None):
+    """The steady softmax of S^T[p] as a regular stream over the MFMA gaps:
+    element e (group g = e / 8: P^T k-step kk = g / 2, query block nb = g % 2;
+    register 8 (kk % 2) + e % 8 of S^T block (kk / 2, nb)) takes its FMA in
+    gap e - 1 and its exponential in gap e; the packs and row sums of element
+    pairs follow as soon as both exponentials are a gap old and the pair's
+    P^T registers are released by PV (kk_release), at most `per_gap` per gap,
+    and each element's fp32 row-sum add one gap after its exponential.
+    Returns {gap: [Ins]} with key "tail" for what follows the last MFMA."""
+    per_gap = STREAM["per_gap"] if per_gap is None else per_gap
+    out = {}
+    late = {}
+    put = lambda g, x: out.setdefault(g, []).append(x)
+    tmp = [v(160 + j) for j in range(24)]
+    for e in range(64):
+        g, j = e // 8, e % 8
+        kk, nb = g // 2, g % 2
+        src = SACC[p][kk // 2][nb][8 * (kk % 2) + j]
+        t = tmp[e % 24]
+        fma = V("v_fma_f32", t, src, SCALE, "-" + str(MSUB[nb]))
+        fma.uses.append(("v", MSUB[nb].i))
+        eg = e if not STREAM["pair_exps"] else (e // 2) * 2 + 1
+        put(eg - STREAM["fma_lead"], fma)
+        ex = V("v_exp_f32", t, t, trans=True)
+        if STREAM["exp_last"]:
+            late.setdefault(eg, []).append(ex)
+        else:
+            put(eg if eg < n_gaps else "tail", ex)
+    # packs in pair order, each as early as allowed; the fp32 row sums one
+    # gap after each exponential (chains (nb, e % 2))
+    load = {}
+    for i in range(32):
+        e0 = 2 * i
+        g = e0 // 8
+        kk, nb = g // 2, g % 2
+        q = (e0 % 8) // 2
+        gap = max(e0 + 2, kk_release[kk])
+        while gap < n_gaps and load.get(gap, 0) >= per_gap:
+            gap += 1
+        load[gap] = load.get(gap, 0) + 1
+        put(gap if gap < n_gaps else "tail",
+            V("v_cvt_pk_bf16_f32", PB[kk][nb][q], tmp[e0 % 24], tmp[(e0 + 1) % 24]))
+    for e in range(64):
+        g = e // 8
+        kk, nb = g // 2, g % 2
+        acc = PSUM[nb][e % 2]
+        init = kk == 0 and e % 8 < 2
+        put(e + 1 if e + 1 < n_gaps else "tail", V("v_add_f32", acc, 0 if init else acc, tmp[e % 24]))
+    for g_, lst in late.items():
+        for x in lst:
+            put(g_ if g_ < n_gaps else "tail", x)
+    # the last exponential is the tail's first op; its pack reads it a wait
+    # state later at the earliest
+    if "tail" in out:
+        tl = out["tail"]
+        k = next((j for j, x in enumerate(tl) if not x.text.startswith("v_exp")), None)
+        if k is not None:
+            tl.insert(k, NOP(TRANS_FWD - 1))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the MFMA-stream iteration scheduler
+# ---------------------------------------------------------------------------
+
+
+class Block:
+    def __init__(self):
+        self.out = []
+
+    def emit(self, x):
+        if isinstance(x, list):
+            for y in x:
+                self.out.append(y)
+        else:
+            self.out.append(x)
+
+
+def schedule_iteration(blk, mfmas, reads, pre_reads, side, sm_ops, budget=30, end_ops=(), fixed=None):
+    """Emit one iteration: `mfmas` a list of (Ins, frag index or None); `reads`
+    dict frag -> list of Ins, issued at gap 2(f - LOOK) (f >= LOOK) or before
+    the first MFMA (f < LOOK, unless in `pre_reads`, already in flight); `side` dict
+    gap -> list of Ins (gap -1: before the first MFMA); `sm_ops` the VALU
+    program, issued greedily under a per-gap cycle budget."""
+    nm = len(mfmas)
+    gap_reads = {}
+    for f, lst in reads.items():
+        if f in pre_reads:
+            continue
+        gap = 2 * (f - LOOK) if f >= LOOK else -1
+        gap_reads.setdefault(min(gap, nm - 1), []).extend(lst)
+    # LDS op bookkeeping for lgkmcnt: list of frag ids per emitted LDS op
+    lds_log = list(pre_reads_log_for(pre_reads, reads))
+    pending = list(sm_ops)
+    idx_of = {}
+
+    def emitted_index():
+        return len(blk.out)
+
+    def ready(op, gap):
+        if op.nb_gap > gap:
+            return False
+        for d, dist in op.deps:
+            if not d.done:
+                return False
+            if emitted_index() - d.emitted_at < dist:
+                return False
+        return True
+
+    def emit_op(op):
+        op.emitted_at = len(blk.out) + len(op.ins) - 1
+        for x in op.ins:
+            blk.out.append(x)
+        op.done = True
+
+    def fill(gap, limit):
+        spent = 0
+        while True:
+            found = None
+            for op in pending[:40]:
+                if ready(op, gap):
+                    found = op
+                    break
+            if found is None or spent + found.cost > limit and spent > 0:
+                break
+            pending.remove(found)
+            emit_op(found)
+            spent += found.cost
+        return spent
+
+    def do_gap(gap):
+        # side ops first: they include the address updates the gap's reads use
+        spent = 0
+        for x in side.get(gap, []):
+            blk.out.append(x)
+            spent += x.cost
+        for x in gap_reads.get(gap, []):
+            blk.out.append(x)
+            spent += x.cost
+            if x.mem == "lgkm":
+                lds_log.append(x.frag)
+        if fixed:
+            for x in fixed.get(gap, []):
+                blk.out.append(x)
+                spent += x.cost
+        fill(gap, max(budget - spent, 0))
+
+    do_gap(-1)
+    for mi, (ins, frag) in enumerate(mfmas):
+        if frag is not None and (mi == 0 or mfmas[mi - 1][1] != frag):
+            # wait for this fragment's reads: count LDS ops issued after its last one
+            last = max(j for j, f in enumerate(lds_log) if f == frag)
+            after = len(lds_log) - 1 - last
+            assert after <= 15
+            blk.out.append(WAIT(lgkm=after))
+        blk.out.append(ins)
+        do_gap(mi)
+    # leftover VALU after the MFMA stream: in order, with nops for the deps
+    gap = nm
+    while pending:
+        op = None
+        for cand in pending[:40]:
+            if ready(cand, gap + 1000):
+                op = cand
+                break
+        if op is None:
+            blk.out.append(NOP(0))
+            continue
+        pending.remove(op)
+        emit_op(op)
+    if fixed:
+        for x in fixed.get("tail", []):
+            blk.out.append(x)
+    for x in end_ops:
+        blk.out.append(x)
+
+
+# ---------------------------------------------------------------------------
+# slot scheduler: a single wave issues one instruction per 4-cycle slot, so an
+# MFMA every 32 cycles leaves 7 slots between two MFMAs (measured on gfx950:
+# 6 FMAs between MFMAs cost nothing, 8 cost 8 cycles, 10 cost 16; SALU the
+# same). Instructions are placed into those slots within their windows.
+# ---------------------------------------------------------------------------
+
+
+class Item:
+    """An instruction bundle placed into the gap after MFMA `gap` (gap -1:
+    before the first MFMA) with lo <= gap <= hi (hi None: any, or the tail);
+    deps: (item, d) -- at least d wait states (instructions) between the end
+    of item and this bundle (0: just after it)."""
+
+    __slots__ = ("ins", "lo", "hi", "deps", "seq", "at", "size")
+    _n = 0
+
+    def __init__(self, ins, lo=-1, hi=None, deps=()):
+        self.ins = ins if isinstance(ins, list) else [ins]
+        self.lo, self.hi = lo, hi
+        self.deps = list(deps)
+        Item._n += 1
+        self.seq = Item._n
+        self.at = None
+        self.size = sum(x.ws if x.kind == "nop" else 1 for x in self.ins)
+
+
+def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
+    """Emit `mfmas` [(Ins, frag)] with `items` in the gaps. LDS reads carry
+    their fragment in Ins.frag; before an MFMA whose fragment's reads are not
+    known complete, an s_waitcnt lgkmcnt covers it (and the next fragment, if
+    its reads are out). pre_log: fragments of the LDS ops already in flight."""
+    out = []
+    log = list(pre_log)     # fragment per LDS op, in issue order
+    done = 0                # ops [0, done) of log are known complete
+    pending = sorted(items, key=lambda it: it.seq)
+    # an item's deadline also bounds the items it depends on
+    changed = True
+    while changed:
+        changed = False
+        for it in pending:
+            if it.hi is None:
+                continue
+            for d, _ in it.deps:
+                if d.hi is None or d.hi > it.hi:
+                    d.hi = it.hi
+                    changed = True
+    nm = len(mfmas)
+
+    def ready(it, g):
+        if it.lo > g:
+            return False
+        for d, dist in it.deps:
+            if d.at is None or len(out) - d.at - 1 < dist:
+                return False
+        return True
+
+    def place(it):
+        for x in it.ins:
+            out.append(x)
+            if x.kind == "lds":
+                log.append(x.frag)
+        it.at = len(out) - 1
+        pending.remove(it)
+
+    def last_op(f):
+        idx = [j for j, fr in enumerate(log) if fr == f]
+        return idx[-1] if idx else None
+
+    for g in range(-1, nm):
+        used = 0
+        while True:
+            cands = [it for it in pending if ready(it, g)]
+            if not cands:
+                break
+            forced = [it for it in cands if it.hi is not None and it.hi <= g]
+            pick = min(forced or cands, key=lambda it: (it.hi if it.hi is not None else 10 ** 6, it.seq))
+            if not forced and used + pick.size > cap:
+                break
+            place(pick)
+            used += pick.size
+        late = [it for it in pending if it.hi is not None and it.hi <= g]
+        assert not late, f"gap {g}: items past their deadline: {[x.ins[0].text for x in late]}"
+        if g + 1 < nm:
+            ins, f = mfmas[g + 1]
+            if f is not None:
+                lf = last_op(f)
+                assert lf is not None, f"fragment {f} read before its MFMA {g + 1}"
+                if lf >= done:
+                    # cover the next fragment too if its reads are out: a wait
+                    # per two fragments
+                    ln = last_op(f + 1)
+                    upto = ln if ln is not None else lf
+                    n_after = min(len(log) - 1 - upto, 15)
+                    out.append(WAIT(lgkm=n_after))
+                    done = len(log) - n_after
+            out.append(ins)
+    # the tail: the rest in order of readiness, nops where a distance is not met
+    while pending:
+        cands = [it for it in pending if ready(it, 10 ** 6)]
+        if cands:
+            place(min(cands, key=lambda it: (it.hi if it.hi is not None else 10 ** 6, it.seq)))
+        else:
+            out.append(NOP(0))
+    out.extend(tail)
+    return hoist_memory(out)
+
+
+def _conflict(a, b):
+    da, ua, db, ub = set(a.defs), set(a.uses), set(b.defs), set(b.uses)
+    return bool(da & ub or ua & db or da & db)
+
+
+def hoist_memory(prog):
+    """Within each gap between two MFMAs, move LDS and vector-memory
+    instructions ahead of independent VALU / SALU work: issued behind VALU
+    work (a transcendental in particular) they hold up the next MFMA
+    (measured on gfx950: +2.3 cycles per MFMA for an LDS read at the end of
+    the gap, +3 for an LDS DMA, nothing at its start). Nothing moves across an
+    MFMA, a wait, a nop, a label or a branch."""
+    out = []
+    for x in prog:
+        if x.kind in ("lds", "vmem"):
+            j = len(out)
+            while j > 0 and out[j - 1].kind in ("valu", "salu") and not _conflict(out[j - 1], x):
+                j -= 1
+            out.insert(j, x)
+        else:
+            out.append(x)
+    return out
+
+
+def pre_reads_log_for(pre_reads, reads):
+    log = []
+    for f in sorted(pre_reads):
+        for x in reads[f]:
+            if x.mem == "lgkm":
+                log.append(f)
+    return log
+
+
+# ---------------------------------------------------------------------------
+# kernel body
+# ---------------------------------------------------------------------------
+
+
+class Gen:
+    def __init__(self, causal):
+        self.causal = causal
+        self.tag = "C" if causal else "F"
+        self.prog = []
+        self.nlab = 0
+
+    def L(self, name):
+        return f"L_pfw64{self.tag}_{name}"
+
+    def emit(self, x):
+        if isinstance(x, list):
+            self.prog.extend(x)
+        else:
+            self.prog.append(x)
+
+    # ------------------------------------------------------------ iteration parts
+    def iter_scalars(self):
+        """Slot bases and load resources of iteration ITER (tiles i+1 K read,
+        i V read, i+4 K load, i+2 V load)."""
+        t0, t1, t2, t3 = T[0], T[1], T[2], T[3]
+        out = [
+            S("s_add_i32", t0, ITER, 1), S("s_and_b32", t0, t0, 3), S("s_lshl_b32", t0, t0, 14),
+            S("s_add_u32", SKRD, t0, LDSB),
+            S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14),
+            S("s_add_u32", SVRD, t1, LDSB), S("s_add_u32", SVRD, SVRD, LDS_V),
+            S("s_add_u32", SKLD, t1, LDSB), S("s_add_u32", SKLD, SKLD, WOFF),
+            S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
+            S("s_add_u32", SVLD, t2, LDSB), S("s_add_u32", SVLD, SVLD, LDS_V + 0),
+            S("s_add_u32", SVLD, SVLD, WOFF),
+            S("s_add_i32", t3, ITER, 4), S("s_lshl_b32", t3, t3, 14),
+        ] + rsrc_at(RK, KH, t3, KVB) + [
+            S("s_add_i32", t3, ITER, 2), S("s_lshl_b32", t3, t3, 14),
+        ] + rsrc_at(RV, VH, t3, KVB)
+        return out
+
+    def load_ops(self):
+        """The 8 LDS-DMA loads of an iteration: K tile i+4, then V tile i+2
+        (each 4 x 1 KB, this wave's 16 rows), as 8 groups [m0 write, nop, load]."""
+        groups = []
+        for j in range(4):
+            groups.append([S("s_add_u32", M0, SKLD, 1024 * j), NOP(0), BLOAD_LDS(INV[f"loff{j}"], RK)])
+        for j in range(4):
+            groups.append([S("s_add_u32", M0, SVLD, 1024 * j), NOP(0), BLOAD_LDS(INV[f"loff{j}"], RV)])
+        return groups
+
+    def barrier(self, vm):
+        return [WAIT(vm=vm), BAR()]
+
+    def ka_update(self):
+        return [V("v_add_u32", KA, SKRD, INV["kofs"])]
+
+    def va_update(self):
+        out = [V("v_add_u32", VA[0][0], SVRD, INV["vofs1"]), V("v_add_u32", VA[0][1], SVRD, INV["vofs2"])]
+        for ob in range(1, 4):
+            out += [V("v_xor_b32", VA[ob][0], 64 * ob, VA[0][0]), V("v_xor_b32", VA[ob][1], 64 * ob, VA[0][1])]
+        return out
+
+    def mfma_lists(self, pv, qk_par):
+        """MFMA list [(Ins, frag)] and frag reads {frag: [Ins]} of an iteration
+        with PV (of the tile whose V addresses are in VA) and/or QK into
+        SACC[qk_par] (K addresses from KA)."""
+        mf, reads = [], {}
+        f = 0
+        if pv:
+            for kk in range(4):
+                for ob in range(4):
+                    slot = f % NSLOT
+                    reads[f] = v_frag_reads(slot, kk, ob)
+                    for nb in range(2):
+                        mf.append((MFMA(OACC[ob][nb], FRAG[slot], PB[kk][nb], OACC[ob][nb]), f))
+                    f += 1
+        if qk_par is not None:
+            for ks in range(8):
+                for mb in range(2):
+                    slot = f % NSLOT
+                    reads[f] = k_frag_reads(slot, ks, mb, mb == 0)
+                    for nb in range(2):
+                        dst = SACC[qk_par][mb][nb]
+                        mf.append((MFMA(dst, FRAG[slot], QA[nb][ks], None if ks == 0 else dst), f))
+                    f += 1
+        for fr, lst in reads.items():
+            for x in lst:
+                x.frag = fr
+        return mf, reads, f
+
+    # the V(i) fragments 0..2 read at the end of an iteration for the next PV
+    def v_prefetch(self, nf):
+        reads = {}
+        for j in range(LOOK):
+            lst = v_frag_reads((nf + j) % NSLOT, j // 4, j % 4)
+            for x in lst:
+                x.frag = nf + j
+            reads[nf + j] = lst
+        return reads
+
+    def mfma_iteration(self, name, pv, qk_par, sm, prefetch, side_extra=None, budget=30, end_ops=(), fixed=None):
+        mf, reads, nf = self.mfma_lists(pv, qk_par)
+        pre = set(range(LOOK)) if pv else set()
+        if prefetch:
+            reads.update(self.v_prefetch(nf))
+        side = {}
+        nm = len(mf)
+        # scalars at gap -1, loads spread over the stream
+        side[-1] = self.iter_scalars()
+        loads = self.load_ops()
+        for j, grp in enumerate(loads):
+            gap = (j * nm) // 8 + 1 if nm else -1
+            side.setdefault(min(gap, nm - 1) if nm else -1, []).extend(grp)
+        if side_extra:
+            for g, lst in side_extra.items():
+                side.setdefault(g, []).extend(lst)
+        blk = Block()
+        schedule_iteration(blk, mf, reads, pre, side, sm.ops if sm else [], budget=budget, end_ops=end_ops,
+                           fixed=fixed)
+        return blk.out
+
+    # ------------------------------------------------------------ softmax programs
+    def first_softmax(self, masked):
+        """Softmax of a wave's first tile (parity 0): the row max first."""
+        sm = Softmax()
+        p = 0
+        settle = []
+        for nb in range(2):
+            # temporaries in TMP[2]: its first exponentials wait for the max
+            acc = [TMP[2][nb * 4 + 0], TMP[2][nb * 4 + 1]]
+            ops = []
+            if not masked:
+                for mb in range(2):
+                    src = SACC[p][mb][nb]
+                    prev = sm.add(V("v_max3_f32", acc[mb], src[0], src[1], src[2]))
+                    r = 3
+                    while r < 16:
+                        hi = src[r + 1] if r + 1 < 16 else src[r]
+                        prev = sm.add(V("v_max3_f32", acc[mb], acc[mb], src[r], hi), [(prev, 1)])
+                        r += 2
+                    ops.append(prev)
+            else:
+                for mb in range(2):
+                    src = SACC[p][mb][nb]
+                    prev = sm.add(V("v_mov_b32", acc[mb], NINF))
+                    kind = mask_kind(self.causal, mb, nb)
+                    for r in range(16 if kind != "all" else 0):
+                        if kind == "none":
+                            prev = sm.add(V("v_max_f32", acc[mb], acc[mb], src[r]), [(prev, 1)])
+                            continue
+                        tmpr = TMP[0][(mb * 16 + r) % 8 + 0]
+                        op = sm.add(masked_select(self.causal, mb, nb, r, tmpr, src[r]), [(prev, 1)])
+                        prev = sm.add(V("v_max_f32", acc[mb], acc[mb], tmpr), [(op, 1)])
+                    ops.append(prev)
+            m = TMP[2][nb * 4 + 2]
+            x = TMP[2][nb * 4 + 3]
+            o1 = sm.add(V("v_max_f32", m, acc[0], acc[1]), [(ops[0], 1), (ops[1], 1)])
+            o2 = sm.add(V("v_mov_b32", x, m), [(o1, 1)])
+            o3 = sm.add([NOP(PERM_WS - 1), V("v_permlane32_swap_b32", m, x, perm=True)], [(o2, 1)])
+            o4 = sm.add([NOP(PERM_WS - 1), V("v_max_f32", m, m, x)], [(o3, 1)])
+            # MRUN = m == -inf ? -inf : m * c; MSUB = finite ? MRUN : 0
+            o5 = sm.add(V("v_mul_f32", MRUN[nb], SCALE, m), [(o4, 1)])
+            o6 = sm.add([V("v_cmp_neq_f32", VCC, NINF, m), NOP(1), V("v_cndmask_b32", MRUN[nb], NINF, MRUN[nb], VCC)],
+                        [(o5, 1)])
+            o7 = sm.add([V("v_cmp_neq_f32", VCC, NINF, MRUN[nb]), NOP(1),
+                         V("v_cndmask_b32", MSUB[nb], 0, MRUN[nb], VCC)], [(o6, 1)])
+            settle.append((o7, 1))
+        softmax_exp_program(sm, p, masked, self.causal, kk_release=[-1] * 4, msub_deps=settle)
+        return sm
+
+    def tail_first(self):
+        """Tile sums -> LRUN (first tile: l = sum)."""
+        return NOPS(DOT_FWD) + [V("v_add_f32", LRUN[0], PSUM[0][0], PSUM[0][1]),
+                                V("v_add_f32", LRUN[1], PSUM[1][0], PSUM[1][1])]
+
+    def tail_stale(self, redo_label, ret_label):
+        """Tile sums; redo when some lane's sum is above the bound or not
+        finite; else l += sum."""
+        return NOPS(DOT_FWD) + [
+                V("v_add_f32", PSUM[0][0], PSUM[0][0], PSUM[0][1]),
+                V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]),
+                V("v_cmp_nle_f32", CMPA, PSUM[0][0], BOUND),
+                V("v_cmp_nle_f32", CMPB, PSUM[1][0], BOUND),
+                NOP(4),
+                S("s_or_b64", CMPA, CMPA, CMPB),
+                CBR("s_cbranch_scc1", redo_label),
+                V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]),
+                V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
+                LABEL(ret_label)]
+
+    def redo_block(self, label, ret_label, p, masked):
+        """Rare path: a tile sum passed the bound. New max of S^T[p], O and l
+        rescaled, exponentials again (straight-line)."""
+        # temporaries in TMP and PB: the next tile's first V^T fragments are in
+        # flight into the fragment slots
+        R = TMP[1]
+        out = [LABEL(label)] + NOPS(MFMA_WS + 4)
+        for nb in range(2):
+            acc = [R[nb * 4 + 0], R[nb * 4 + 1]]
+            for mb in range(2):
+                src = SACC[p][mb][nb]
+                out.append(V("v_mov_b32", acc[mb], NINF))
+                kind = mask_kind(self.causal, mb, nb) if masked else "none"
+                for r in range(16 if kind != "all" else 0):
+                    if kind == "cmp":
+                        out += masked_select(self.causal, mb, nb, r, TMP[0][0], src[r])
+                        out.append(V("v_max_f32", acc[mb], acc[mb], TMP[0][0]))
+                    else:
+                        out.append(V("v_max_f32", acc[mb], acc[mb], src[r]))
+            m, x = R[nb * 4 + 2], R[nb * 4 + 3]
+            out += [V("v_max_f32", m, acc[0], acc[1]), V("v_mov_b32", x, m)] + NOPS(PERM_WS) + [
+                V("v_permlane32_swap_b32", m, x, perm=True)] + NOPS(PERM_WS) + [
+                V("v_max_f32", m, m, x),
+                V("v_mul_f32", acc[0], SCALE, m),
+                V("v_cmp_neq_f32", VCC, NINF, m), NOP(1),
+                V("v_cndmask_b32", acc[0], NINF, acc[0], VCC),                                  # tile max (scaled)
+                V("v_max_f32", m, MRUN[nb], acc[0]),                                            # m_new
+                V("v_sub_f32", x, MRUN[nb], m), V("v_exp_f32", x, x, trans=True), NOP(1),
+                V("v_cmp_neq_f32", VCC, NINF, m), NOP(1), V("v_cndmask_b32", x, "1.0", x, VCC)]
+            # alpha in x (R[nb*4+3]), m_new in m (R[nb*4+2])
+        # O *= alpha, 16 accumulators at a time through PB
+        for nb in range(2):
+            al = R[nb * 4 + 3]
+            for ob in range(4):
+                src = OACC[ob][nb]
+                tmp = [v(128 + 16 * (ob % 2) + r) for r in range(16)]
+                out += [ACCR(tmp[r], src[r]) for r in range(16)]
+                out += [V("v_mul_f32", tmp[r], al, tmp[r]) for r in range(16)]
+                out += [ACCW(src[r], tmp[r]) for r in range(16)]
+            out += [V("v_mul_f32", LRUN[nb], al, LRUN[nb]),
+                    V("v_mov_b32", MRUN[nb], R[nb * 4 + 2]),
+                    V("v_cmp_neq_f32", VCC, NINF, MRUN[nb]), NOP(1), V("v_cndmask_b32", MSUB[nb], 0, MRUN[nb], VCC)]
+        # exponentials again (program order, nops where a result is read early)
+        sm = Softmax()
+        softmax_exp_program(sm, p, masked, self.causal, kk_release=[-1] * 4)
+        emitted = []
+        for op in sm.ops:
+            for d, dist in op.deps:
+                have = len(emitted) - d.emitted_at
+                if have < dist:
+                    emitted += NOPS(dist - have)
+            op.emitted_at = len(emitted) + len(op.ins) - 1
+            emitted += op.ins
+        out += emitted + NOPS(DOT_FWD)
+        out += [V("v_add_f32", PSUM[0][0], PSUM[0][0], PSUM[0][1]),
+                V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]),
+                V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]),
+                V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
+                BR(ret_label)]
+        return out
+
+    def stale_softmax(self, p, masked, kk_release):
+        sm = Softmax()
+        softmax_exp_program(sm, p, masked, self.causal, kk_release)
+        return sm
+
+    # ------------------------------------------------------------ iteration variants
+    def it_fill(self):
+        """i = -1: QK(0) into SACC[0]; O zeroed under it."""
+        sm = Softmax()
+        for ob in range(4):
+            for nb in range(2):
+                for r in range(16):
+                    sm.add(ACCW(OACC[ob][nb][r], 0))
+        side = {-1: self.ka_update()}
+        return self.mfma_iteration("fill", False, 0, sm, False, side_extra=side, budget=40)
+
+    def it_first(self):
+        """i = 0 (walk of >= 2 tiles): softmax(0) with the row max, QK(1)."""
+        sm = self.first_softmax(False)
+        side = {-1: self.ka_update(), 2 * (16 - LOOK): self.va_update()}
+        return self.mfma_iteration("first", False, 1, sm, True, side_extra=side, budget=48,
+                                   end_ops=self.tail_first())
+
+    def it_first_last(self):
+        """i = 0 of a one-tile walk: masked softmax(0), no MFMAs."""
+        sm = self.first_softmax(True)
+        side = {-1: self.va_update()}
+        if not self.causal:
+            side[-1] += [V("v_sub_u32", DREM, KVEND, INV["h8"])]   # keys >= S of tile 0
+        return self.mfma_iteration("first_last", False, None, sm, True, side_extra=side, budget=10 ** 6,
+                                   end_ops=self.tail_first())
+
+    def it_steady(self, p):
+        """1 <= i <= wt-2: PV(i-1), QK(i+1) into SACC[1-p], softmax(i) of SACC[p]
+        and the loads of K tile i+4 and V tile i+2, placed by slot_schedule."""
+        mf, reads, nf = self.mfma_lists(True, 1 - p)
+        items = []
+
+        def add(ins, lo=-1, hi=None, deps=()):
+            it = Item(ins, lo, hi, deps)
+            items.append(it)
+            return it
+
+        def chain(ops, lo=-1, after=()):
+            prev, first = None, None
+            for x in ops:
+                it = add(x, lo, None, ([(prev, 0)] if prev else []) + [(a_, 0) for a_ in after])
+                first = first or it
+                prev = it
+            return prev
+        t0, t1, t2, t3, t4 = T[0], T[1], T[2], T[3], T[4]
+        # slot bases: K read tile i+1, V tile i, K load tile i+4 (slot of i),
+        # V load tile i+2; load resources of tiles i+4 (K) and i+2 (V)
+        skrd = chain([S("s_add_i32", t0, ITER, 1), S("s_and_b32", t0, t0, 3), S("s_lshl_b32", t0, t0, 14),
+                      S("s_add_u32", SKRD, t0, LDSB)])
+        t1d = chain([S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14)])
+        svrd = chain([S("s_add_u32", SVRD, t1, LDSB), S("s_add_u32", SVRD, SVRD, LDS_V)], after=[t1d])
+        skld = chain([S("s_add_u32", SKLD, t1, LDSB), S("s_add_u32", SKLD, SKLD, WOFF)], after=[t1d])
+        svld = chain([S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
+                      S("s_add_u32", SVLD, t2, LDSB), S("s_add_u32", SVLD, SVLD, LDS_V),
+                      S("s_add_u32", SVLD, SVLD, WOFF)])
+        rk = chain([S("s_add_i32", t3, ITER, 4), S("s_lshl_b32", t3, t3, 14)] + rsrc_at(RK, KH, t3, KVB))
+        rv = chain([S("s_add_i32", t4, ITER, 2), S("s_lshl_b32", t4, t4, 14)] + rsrc_at(RV, VH, t4, KVB))
+        # loads: one per 8 gaps, K then V (the barrier's vmcnt assumes this order)
+        prev = None
+        for j in range(8):
+            k = j < 4
+            deps = [(skld if k else svld, 0)] + ([(prev, 0)] if prev else [])
+            # the M0 write in an earlier gap than its load: the MFMA between
+            # gives the wait state, and the load can lead its own gap
+            m = add(S("s_add_u32", M0, SKLD if k else SVLD, 1024 * (j % 4)), 8 * j - 1, 8 * j, deps)
+            prev = add(BLOAD_LDS(INV[f"loff{j % 4}"], RK if k else RV), 1 + 8 * j, 61,
+                       [(m, M0_WS), (rk if k else rv, 0)])
+        ka = add(V("v_add_u32", KA, SKRD, INV["kofs"]), -1, 2 * (16 - LOOK) - 1, [(skrd, 0)])
+        # fragment reads: slot f % NSLOT is free after the MFMAs of fragment f - NSLOT
+        fitem = {}
+        xitem = None
+        for f in range(LOOK, nf):
+            # no earlier than LOOK fragments ahead (the LDS counter tracks 15 ops)
+            lo = max(2 * (f - NSLOT) + 1, 2 * (f - LOOK))
+            deps = []
+            lds = [x for x in reads[f] if x.kind == "lds"]
+            if f >= 16:                       # K fragment (ks, mb) = ((f-16)//2, (f-16)%2)
+                ks, mb = (f - 16) // 2, (f - 16) % 2
+                deps.append((ka, 0))
+                xor = [x for x in reads[f] if x.kind != "lds"]
+                if xor:                        # KX for this ks, after the last read of the old one
+                    xitem = add(xor, lo - 2, 2 * f - 6, [(ka, 0)] + ([(fitem[f - 1], 0)] if f - 1 >= 16 else []))
+                if ks > 0:
+                    deps.append((xitem, 0))
+            fitem[f] = add(lds, lo, 2 * f - 5, deps)
+        # V(i) addresses after the last PV(i-1) read, before the prefetch
+        va0 = [add(V("v_add_u32", VA[0][j], SVRD, INV[f"vofs{j + 1}"]), 0, 44, [(fitem[15], 0), (svrd, 0)])
+               for j in range(2)]
+        vas = list(va0)
+        for ob in range(1, 4):
+            for j in range(2):
+                vas.append(add(V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]), 0, 46, [(va0[j], 0), (fitem[15], 0)]))
+        # prefetch of V(i) fragments 0..LOOK-1 into the next iteration's slots
+        pre_next = self.v_prefetch(nf)
+        for f, lst in sorted(pre_next.items()):
+            add(lst, max(2 * (f - NSLOT) + 1, 2 * (f - LOOK)), None, [(x, 0) for x in vas])
+        # softmax of tile i: element e (group e / 8 = (kk, nb)), fp32 row sums
+        rel = [8 * kk + 7 for kk in range(4)]
+        tmp = [v(160 + j) for j in range(24)]
+        fma, exp, adds, cvt = {}, {}, {}, {}
+        for e in range(64):
+            g = e // 8
+            kk, nb = g // 2, g % 2
+            srcr = SACC[p][kk // 2][nb][8 * (kk % 2) + e % 8]
+            t = tmp[e % 24]
+            x = V("v_fma_f32", t, srcr, SCALE, "-" + str(MSUB[nb]))
+            x.uses.append(("v", MSUB[nb].i))
+            deps = []
+            if e >= 24:
+                deps += [(adds[e - 24], 0), (cvt[(e - 24) // 2], 0)]
+            fma[e] = add(x, max(0, e - 3), e + 1, deps)
+            exp[e] = add(V("v_exp_f32", t, t, trans=True), e, e + 2, [(fma[e], 0)])
+            if e % 2 == 1:
+                i = e // 2
+                cvt[i] = add(V("v_cvt_pk_bf16_f32", PB[kk][nb][(e % 8) // 2], tmp[(e - 1) % 24], t),
+                             max(e + 1, rel[kk]), max(e + 1, rel[kk]) + 6,
+                             [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
+            acc = PSUM[nb][e % 2]
+            init = kk == 0 and e % 8 < 2
+            deps = [(exp[e], TRANS_FWD)]
+            if not init:
+                prev_same = max(j for j in adds if (j // 8) % 2 == nb and j % 2 == e % 2)
+                deps.append((adds[prev_same], 0))
+            adds[e] = add(V("v_add_f32", acc, 0 if init else acc, t), e + 1, e + 4, deps)
+        # tile sums (nb = 0 is complete before the stream ends)
+        last0 = [adds[e] for e in range(64) if (e // 8) % 2 == 0]
+        last1 = [adds[e] for e in range(64) if (e // 8) % 2 == 1]
+        s0 = add(V("v_add_f32", PSUM[0][0], PSUM[0][0], PSUM[0][1]), 0, None, [(a_, 0) for a_ in last0])
+        c0 = add(V("v_cmp_nle_f32", CMPA, PSUM[0][0], BOUND), 0, None, [(s0, 0)])
+        s1 = add(V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]), 0, None, [(a_, 0) for a_ in last1])
+        c1 = add(V("v_cmp_nle_f32", CMPB, PSUM[1][0], BOUND), 0, None, [(s1, 0)])
+        tail = [NOP(VALU_SGPR_VMEM - 1), S("s_or_b64", CMPA, CMPA, CMPB),
+                CBR("s_cbranch_scc1", self.L(f"redo_s{p}")),
+                V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]),
+                V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
+                LABEL(self.L(f"ret_s{p}"))]
+        pre_log = [f for f in range(LOOK) for _ in range(2)]
+        return slot_schedule(mf, items, pre_log, cap=7, tail=tail)
+
+    def it_last(self, p):
+        """i = wt-1 >= 1: PV(i-1), masked softmax(i) of SACC[p]."""
+        rel = [8 * kk + 8 for kk in range(4)]
+        sm = self.stale_softmax(p, True, rel)
+        # V(i) addresses between the last PV(i-1) fragment read (gap
+        # 2 (15 - LOOK)) and the first prefetch read (gap 2 (16 - LOOK), after
+        # the gap's side ops)
+        side = {2 * (16 - LOOK): self.va_update()}
+        if not self.causal:
+            side[-1] = [S("s_lshl_b32", T[4], ITER, 6), S("s_sub_i32", T[4], KVEND, T[4]),
+                        V("v_sub_u32", DREM, T[4], INV["h8"])]
+        return self.mfma_iteration(f"last{p}", True, None, sm, True, side_extra=side, budget=40,
+                                   end_ops=self.tail_stale(self.L(f"redo_l{p}"), self.L(f"ret_l{p}")))
+
+    def it_drain(self):
+        """i = wt: PV(wt-1)."""
+        return self.mfma_iteration("drain", True, None, None, False, end_ops=[WAIT(lgkm=0)])
+
+    def it_idle(self):
+        out = self.iter_scalars()
+        for grp in self.load_ops():
+            out += grp
+        return out
+
+    # ------------------------------------------------------------ output
+    def output(self):
+        out = []
+        INVL = [SCR[0], SCR[1]]
+        LT = [SCR[2], SCR[3]]
+        X = SCR[4]
+        out += NOPS(MFMA_WS + 4)
+        for nb in range(2):
+            out += [V("v_mov_b32", X, LRUN[nb])] + NOPS(PERM_WS) + [
+                V("v_permlane32_swap_b32", LRUN[nb], X, perm=True)] + NOPS(PERM_WS) + [
+                V("v_add_f32", LT[nb], LRUN[nb], X),
+                V("v_rcp_f32", INVL[nb], LT[nb], trans=True), NOP(1),
+                V("v_cmp_lt_f32", VCC, 0, LT[nb]), NOP(1), V("v_cndmask_b32", INVL[nb], 0, INVL[nb], VCC)]
+            # LSE = (m + log2 l) ln 2, -inf for an empty row; lanes h = 1 store out of range
+            lg = SCR[5]
+            out += [V("v_log_f32", lg, LT[nb], trans=True), NOP(1),
+                    V("v_add_f32", lg, MRUN[nb], lg), V("v_mul_f32", lg, LN2, lg),
+                    V("v_cndmask_b32", lg, NINF, lg, VCC),
+                    S("s_lshl_b32", T[0], QW0, 2), S("s_add_u32", T[0], T[0], 128 * nb),
+                    V("v_add_u32", SCR[6], T[0], INV["lsel"]),
+                    BSTORE("buffer_store_dword", lg, SCR[6], RL)]
+            out += NOPS(STORE_DATA)
+        # staging write addresses, chunk c: base + 128 l32 + 8 h + (16 c ^ 16 (l32 & 7))
+        stg = T[1]
+        out += [S("s_lshl_b32", stg, WAVE, 13), S("s_add_u32", stg, stg, LDSB), S("s_add_u32", stg, stg, LDS_STG)]
+        WA = [TMP[2][c] for c in range(8)]
+        for c in range(8):
+            out += [V("v_xor_b32", WA[c], 16 * c, INV["wx"]), V("v_add3_u32", WA[c], WA[c], INV["wbase"], stg)]
+        RDA = SCR[7]
+        out += [V("v_add_u32", RDA, stg, INV["rdl"])]
+        # global row offsets: (qw0 + 8k) * 256 + lane part; pass p adds 128 bytes
+        out += [S("s_lshl_b32", T[2], QW0, 8)]
+        VO = [TMP[1][k] for k in range(8)]
+        for k in range(8):
+            out += [S("s_add_u32", T[3], T[2], 2048 * k) if k else S("s_mov_b32", T[3], T[2]),
+                    V("v_add_u32", VO[k], T[3], INV["stl"])]
+        for ps in range(2):
+            dst = [v(128 + 4 * k, 4) for k in range(8)] if ps == 0 else \
+                  [TMP[0].sl(0, 4), TMP[0].sl(4, 4), FRAG[0], FRAG[1], FRAG[2], FRAG[3], SCR.sl(8, 4), SCR.sl(12, 4)]
+            for j in range(2):
+                ob = 2 * ps + j
+                for nb in range(2):
+                    for aa in range(4):
+                        t = [SCR[8 + e] for e in range(4)] if ps == 0 else [v(128 + e + 8 * (aa % 2)) for e in range(4)]
+                        o = OACC[ob][nb]
+                        out += [ACCR(t[e], o[4 * aa + e]) for e in range(4)]
+                        out += [V("v_mul_f32", t[e], INVL[nb], t[e]) for e in range(4)]
+                        out += [V("v_cvt_pk_bf16_f32", t[0], t[0], t[1]), V("v_cvt_pk_bf16_f32", t[1], t[2], t[3])]
+                        c = 4 * j + aa
+                        out += [DSW("ds_write_b64", WA[c], Reg(t[0].f, t[0].i, 2), 4096 * nb)]
+            out += [WAIT(lgkm=0)]
+            for k in range(8):
+                out.append(DSR("ds_read_b128", dst[k], RDA, 1024 * k))
+            out += [WAIT(lgkm=0)]
+            for k in range(8):
+                out.append(BSTORE("buffer_store_dwordx4", dst[k], VO[k], RO, 128 * ps))
+            out += NOPS(STORE_DATA)
+        return out
+
+    # ------------------------------------------------------------ query tile
+    def qtile(self):
+        L = self.L
+        out = []
+        t = T
+        # kv head of bh: (bh / Hq) * Hkv + (bh % Hq) / (Hq / Hkv)
+        out += div_magic(t[0], BH, MHQ, SHHQ)
+        out += [S("s_mul_i32", t[1], t[0], HQ), S("s_sub_u32", t[1], BH, t[1])]
+        out += div_magic(t[2], t[1], MRATIO, SHRATIO)
+        out += [S("s_mul_i32", t[0], t[0], HKV), S("s_add_u32", t[0], t[0], t[2])]
+        out += [S("s_lshl_b32", t[3], SEQ, 8)]                     # bytes per head (S * 256)
+        out += [S("s_mul_i32", t[4], t[0], t[3]), S("s_mul_hi_u32", t[5], t[0], t[3]),
+                S("s_add_u32", KH[0], KP[0], t[4]), S("s_addc_u32", KH[1], KP[1], t[5]),
+                S("s_add_u32", VH[0], VP[0], t[4]), S("s_addc_u32", VH[1], VP[1], t[5])]
+        out += [S("s_mul_i32", t[4], BH, t[3]), S("s_mul_hi_u32", t[5], BH, t[3]),
+                S("s_add_u32", RQ[0], QP[0], t[4]), S("s_addc_u32", RQ[1], QP[1], t[5]),
+                S("s_and_b32", RQ[1], RQ[1], 0xFFFF), S("s_mov_b32", RQ[2], t[3]), S("s_mov_b32", RQ[3], RSRC3),
+                S("s_add_u32", RO[0], OP[0], t[4]), S("s_addc_u32", RO[1], OP[1], t[5]),
+                S("s_and_b32", RO[1], RO[1], 0xFFFF), S("s_mov_b32", RO[2], t[3]), S("s_mov_b32", RO[3], RSRC3)]
+        out += [S("s_lshl_b32", t[6], SEQ, 2), S("s_mul_i32", t[4], BH, t[6]), S("s_mul_hi_u32", t[5], BH, t[6]),
+                S("s_add_u32", RL[0], LP[0], t[4]), S("s_addc_u32", RL[1], LP[1], t[5]),
+                S("s_and_b32", RL[1], RL[1], 0xFFFF),
+                S("s_or_b32", t[7], LP[0], LP[1]), S("s_cmp_eq_u32", t[7], 0),
+                S("s_cselect_b32", RL[2], 0, t[6]), S("s_mov_b32", RL[3], RSRC3)]
+        # q0, kv_end, tiles, this wave's first row and walk length
+        out += [S("s_lshl_b32", Q0, QT, 8), S("s_sub_i32", Q0, Q0, QSHIFT)]
+        if self.causal:
+            out += [S("s_add_i32", KVEND, Q0, 256), S("s_min_i32", KVEND, KVEND, SEQ)]
+        else:
+            out += [S("s_mov_b32", KVEND, SEQ)]
+        out += [S("s_add_i32", NT, KVEND, 63), S("s_ashr_i32", NT, NT, 6), S("s_lshl_b32", KVB, KVEND, 8),
+                S("s_lshl_b32", t[0], WAVE, 6), S("s_add_i32", QW0, Q0, t[0])]
+        if self.causal:
+            out += [S("s_ashr_i32", t[0], QW0, 6), S("s_add_i32", t[0], t[0], 1), S("s_min_i32", t[0], t[0], NT),
+                    S("s_cmp_ge_i32", QW0, 0), S("s_cselect_b32", WT, t[0], 0)]
+        else:
+            out += [S("s_cmp_ge_i32", QW0, 0), S("s_cselect_b32", WT, NT, 0)]
+        # Q offsets of the lane's two rows
+        out += [S("s_lshl_b32", t[0], QW0, 8), V("v_add_u32", QOFF[0], t[0], INV["qlane"]),
+                V("v_add_u32", QOFF[1], 0x2000, QOFF[0])]
+        # prologue loads: K(0), Q, K(1), K(2), V(0)
+        def kload(tile):
+            o = [S("s_mov_b32", t[3], tile * SLOT)] + rsrc_at(RK, KH, t[3], KVB)
+            base = tile * SLOT
+            for j in range(4):
+                o += [S("s_add_u32", M0, LDSB, base + 1024 * j), S("s_add_u32", M0, M0, WOFF), NOP(0),
+                      BLOAD_LDS(INV[f"loff{j}"], RK)]
+            return o
+        out += kload(0)
+        out += NOPS(2)
+        for nb in range(2):
+            for ks in range(8):
+                out.append(BLOAD("buffer_load_dwordx4", QA[nb][ks], QOFF[nb], RQ, 32 * ks))
+        out += kload(1) + kload(2)
+        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RV, VH, t[3], KVB)
+        for j in range(4):
+            out += [S("s_add_u32", M0, LDSB, LDS_V + 1024 * j), S("s_add_u32", M0, M0, WOFF), NOP(0),
+                    BLOAD_LDS(INV[f"loff{j}"], RV)]
+        # ---- the walk
+        out += [S("s_mov_b32", ITER, -1)] + self.barrier(12)
+        out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("idle_m1"))]
+        out += self.it_fill()
+        out += [BR(L("it0")), LABEL(L("idle_m1"))] + self.it_idle()
+        out += [LABEL(L("it0")), S("s_mov_b32", ITER, 0)] + self.barrier(8)
+        out += [S("s_cmp_ge_i32", WT, 2), CBR("s_cbranch_scc1", L("first")),
+                S("s_cmp_eq_u32", WT, 1), CBR("s_cbranch_scc1", L("first_last"))]
+        out += self.it_idle() + [BR(L("it1"))]
+        out += [LABEL(L("first"))] + self.it_first() + [BR(L("it1"))]
+        out += [LABEL(L("first_last"))] + self.it_first_last() + [BR(L("it1"))]
+        out += [LABEL(L("it1")), S("s_mov_b32", ITER, 1)]
+        out += [LABEL(L("steady_chk")), S("s_sub_i32", t[0], WT, 2), S("s_cmp_le_i32", ITER, t[0]),
+                CBR("s_cbranch_scc0", L("after_steady")), S("s_bitcmp1_b32", ITER, 0),
+                CBR("s_cbranch_scc1", L("steady1"))]
+        for p in (0, 1):
+            out += [LABEL(L(f"steady{p}"))] + self.barrier(8) + self.it_steady(p)
+            out += [S("s_add_i32", ITER, ITER, 1), BR(L("steady_chk"))]
+        out += [LABEL(L("after_steady")), S("s_sub_i32", t[0], WT, 1), S("s_cmp_eq_u32", ITER, t[0]),
+                CBR("s_cbranch_scc0", L("drain_chk")), S("s_bitcmp1_b32", ITER, 0),
+                CBR("s_cbranch_scc1", L("last1"))]
+        for p in (0, 1):
+            out += [LABEL(L(f"last{p}"))] + self.barrier(8) + self.it_last(p)
+            out += [S("s_add_i32", ITER, ITER, 1), BR(L("drain_chk"))]
+        out += [LABEL(L("drain_chk")), S("s_cmp_eq_u32", ITER, WT), CBR("s_cbranch_scc0", L("idle_chk"))]
+        out += self.barrier(8) + self.it_drain() + [S("s_add_i32", ITER, ITER, 1)]
+        out += [LABEL(L("idle_chk")), S("s_cmp_le_i32", ITER, NT), CBR("s_cbranch_scc0", L("walk_end"))]
+        out += self.barrier(8) + self.it_idle() + [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
+        out += [LABEL(L("walk_end"))] + [WAIT(vm=0, lgkm=0), BAR()]
+        out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("out_done"))]
+        out += self.output()
+        out += [LABEL(L("out_done"))]
+        return out
+
+    def redo_blocks(self):
+        out = []
+        for p in (0, 1):
+            out += self.redo_block(self.L(f"redo_s{p}"), self.L(f"ret_s{p}"), p, False)
+            out += self.redo_block(self.L(f"redo_l{p}"), self.L(f"ret_l{p}"), p, True)
+        return out
+
+    def kernel(self):
+        L = self.L
+        out = [SLOAD("s_load_dwordx16", s(0, 16), INS_["ka"], 0), SLOAD("s_load_dwordx16", s(16, 16), INS_["ka"], 64),
+               S("s_mov_b32", ITEMV, INS_["wg"]), S("s_mov_b32", GRID, INS_["ng"]), S("s_mov_b32", WAVE, INS_["wv"]),
+               S("s_mov_b32", LDSB, INS_["lb"]), S("s_mov_b32", ONES, 0x3F803F80), S("s_mov_b32", BOUND, BOUND_F),
+               S("s_lshl_b32", WOFF, INS_["wv"], 12),
+               V("v_mov_b32", NINF, 0xFF800000),
+               WAIT(lgkm=0)]
+        t = T
+        out += [LABEL(L("item")), S("s_cmp_ge_u32", ITEMV, NWORK), CBR("s_cbranch_scc1", L("end"))]
+        # work = xcd_remap(v)
+        out += [S("s_and_b32", t[0], ITEMV, 7), S("s_lshr_b32", t[1], ITEMV, 3), S("s_add_u32", t[2], XQ, 1),
+                S("s_mul_i32", t[3], t[0], t[2]), S("s_sub_u32", t[4], t[0], XR), S("s_mul_i32", t[4], t[4], XQ),
+                S("s_mul_i32", t[5], XR, t[2]), S("s_add_u32", t[4], t[4], t[5]), S("s_cmp_lt_u32", t[0], XR),
+                S("s_cselect_b32", t[3], t[3], t[4]), S("s_add_u32", WORK, t[3], t[1])]
+        # decode the work item (prefill_work)
+        out += [S("s_cmp_eq_u32", PAIRED, 0), CBR("s_cbranch_scc1", L("unpaired")),
+                S("s_cmp_lt_u32", WORK, NFULL), CBR("s_cbranch_scc0", L("pair_tail"))]
+        out += div_magic(t[0], WORK, MHALF, SHHALF)
+        out += [S("s_mul_i32", t[1], t[0], HALF), S("s_sub_u32", t[1], WORK, t[1]),
+                S("s_mov_b32", BH0, t[0]), S("s_mov_b32", BH1, t[0]), S("s_sub_u32", QT0, NQT, 1),
+                S("s_sub_u32", QT0, QT0, t[1]), S("s_mov_b32", QT1, t[1]), BR(L("decoded"))]
+        out += [LABEL(L("pair_tail")), S("s_sub_u32", t[0], WORK, NFULL), S("s_lshl_b32", BH0, t[0], 1),
+                S("s_mov_b32", QT0, HALF), S("s_add_u32", BH1, BH0, 1), S("s_mov_b32", QT1, HALF),
+                S("s_cmp_lt_u32", BH1, NBH), CBR("s_cbranch_scc1", L("decoded")), S("s_mov_b32", QT1, -1),
+                BR(L("decoded"))]
+        out += [LABEL(L("unpaired"))] + div_magic(t[0], WORK, MNQT, SHNQT)
+        out += [S("s_mul_i32", t[1], t[0], NQT), S("s_sub_u32", t[1], WORK, t[1]), S("s_mov_b32", BH0, t[0]),
+                S("s_sub_u32", QT0, NQT, 1), S("s_sub_u32", QT0, QT0, t[1]), S("s_mov_b32", QT1, -1)]
+        out += [LABEL(L("decoded")), S("s_mov_b32", PASS, 0)]
+        out += [LABEL(L("qtile")), S("s_cmp_eq_u32", PASS, 0), S("s_cselect_b32", BH, BH0, BH1),
+                S("s_cselect_b32", QT, QT0, QT1)]
+        out += self.qtile()
+        out += [S("s_cmp_eq_u32", PASS, 0), CBR("s_cbranch_scc0", L("next")), S("s_cmp_lt_i32", QT1, 0),
+                CBR("s_cbranch_scc1", L("next")), S("s_mov_b32", PASS, 1), BR(L("qtile"))]
+        out += [LABEL(L("next")), S("s_add_u32", ITEMV, ITEMV, GRID), BR(L("item"))]
+        out += self.redo_blocks()
+        out += [LABEL(L("end")), WAIT(vm=0, lgkm=0)]
+        self.prog = out
+        return out
+
+
+def to_macro(name, prog):
+    lines = []
+    for ins in prog:
+        t = ins.text
+        if ins.kind != "label":
+            t = "  " + t
+        t = t.replace("%[", "\x00").replace("%", "%%").replace("\x00", "%[")
+        lines.append(f'  "{t}\\n"')
+    return f"#define {name} \\\n" + " \\\n".join(lines) + "\n"
+
+
+def clobbers():
+    regs = [f'"v{i}"' for i in range(N_VGPR_OWN)] + [f'"a{i}"' for i in range(256)]
+    regs += [f'"s{i}"' for i in range(N_SGPR_OWN) if i not in (32, 33)]
+    regs += ['"vcc"', '"scc"', '"memory"']
+    return ", ".join(regs)
+
+
+def stats(prog):
+    from collections import Counter
+    c = Counter(i.kind for i in prog)
+    return dict(c)
+
+
+def main(argv):
+    out_path = argv[1] if len(argv) > 1 else None
+    text = ["// Generated by gen_prefill_w64.py: the 64-row prefill kernel bodies. Do not edit.",
+            "#pragma once", ""]
+    for causal in (True, False):
+        g = Gen(causal)
+        prog = g.kernel()
+        check(prog, g.tag)
+        text.append(to_macro("CA_PFW64_BODY_" + ("CAUSAL" if causal else "FULL"), prog))
+        print(f"variant {g.tag}: {len(prog)} lines {stats(prog)}", file=sys.stderr)
+    text.append("#define CA_PFW64_CLOBBERS " + clobbers())
+    text.append(f"#define CA_PFW64_IN_V {len(IN_V)}")
+    src = "\n".join(text) + "\n"
+    if out_path:
+        with open(out_path, "w") as f:
+            f.write(src)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv))

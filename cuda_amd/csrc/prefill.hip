@@ -1011,6 +1011,8 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
   }
   if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, lse, B, Hq, Hkv, S, D, scale, causal, stream);
   if (dtype == kDtypeBF16) {
+    if (prefill_w64_supported(D, S, scale, rq.cos != nullptr))
+      return launch_prefill_w64(q, k, v, o, lse, B, Hq, Hkv, S, scale, causal, stream);
     CA_PREFILL_DMA(BF16, 64)
     CA_PREFILL_DMA(BF16, 128)
   } else if (dtype == kDtypeF16) {
