@@ -178,9 +178,11 @@ def BLOAD(op, d, voff, rsrc, off=0):
     return Ins("vmem", t, defs=[d], uses=[voff, rsrc], mem="vm", cost=4)
 
 
-def BLOAD_LDS(voff, rsrc):
-    return Ins("vmem", f"buffer_load_dwordx4 {voff}, {rsrc}, 0 offen lds", defs=[], uses=[voff, rsrc, M0],
-               mem="vm", m0use=True, cost=4)
+def BLOAD_LDS(voff, rsrc, off=0):
+    """16 bytes per lane into LDS at M0 + off + 16 lane; the instruction
+    offset adds to the global address as well."""
+    t = f"buffer_load_dwordx4 {voff}, {rsrc}, 0 offen" + (f" offset:{off}" if off else "") + " lds"
+    return Ins("vmem", t, defs=[], uses=[voff, rsrc, M0], mem="vm", m0use=True, cost=4)
 
 
 def BSTORE(op, data, voff, rsrc, off=0):
@@ -245,6 +247,10 @@ VALU_SGPR_VALU = 2  # VALU writes SGPR or VCC -> VALU reads it (v_cndmask mask)
 M0_WS = 1           # SALU writes M0 -> LDS DMA
 STORE_DATA = 2      # wide store data -> VALU overwrite
 CAP = 32
+# v_mfma_f32_32x32x16_bf16 takes 8 passes: an MFMA issues at least 8 wait
+# states (32 cycles; measured 32.1 cycles apart back to back) after the one
+# before it, so whatever preceded an MFMA is 8 wait states older by the next.
+MFMA_ISSUE = 8
 
 
 class CheckError(Exception):
@@ -271,7 +277,8 @@ def check(prog, name):
             s.append(i + 1)
         succ.append(s)
 
-    # state: (dist dict, lgkm tuple, vm tuple); dist: (cat, key) -> (d, tag)
+    # state: (dist dict, lgkm tuple, vm tuple); dist: (cat, key) -> (d, tag, dm),
+    # dm: d at the last MFMA issue on the path (None: the entry is younger)
     instate = [None] * n
     instate[0] = ({}, (), ())
     work = [0]
@@ -297,12 +304,12 @@ def check(prog, name):
         db, lb, vb = b
         la, va = merge(la, lb), merge(va, vb)
         d = dict(da)
-        for k, (dist, tag) in db.items():
+        for k, (dist, tag, dm) in db.items():
             if k in d:
-                d0, t0 = d[k]
-                d[k] = (min(d0, dist), t0 if t0 == tag else None)
+                d0, t0, m0 = d[k]
+                d[k] = (min(d0, dist), t0 if t0 == tag else None, None if m0 is None or dm is None else min(m0, dm))
             else:
-                d[k] = (dist, tag)
+                d[k] = (dist, tag, dm)
         return (d, la, va)
 
     def err(i, msg):
@@ -384,36 +391,41 @@ def check(prog, name):
         # --- advance distances
         w = ins.ws
         nd = {}
-        for k, (d0, tag) in dist.items():
+        mf = ins.kind == "mfma"
+        for k, (d0, tag, dm) in dist.items():
             d1 = d0 + w
+            if mf:
+                if dm is not None:
+                    d1 = max(d1, dm + MFMA_ISSUE)
+                dm = d1
             if d1 < CAP:
-                nd[k] = (d1, tag)
-        if ins.kind == "mfma":
+                nd[k] = (d1, tag, dm)
+        if mf:
             for k in ins.mdst:
-                nd[("mw", k)] = (0, ins.mdst)
+                nd[("mw", k)] = (0, ins.mdst, 0)
             for k in (ins.mc or ()):
-                nd[("mrc", k)] = (0, None)
+                nd[("mrc", k)] = (0, None, 0)
             for k in ins.mab:
-                nd[("mrab", k)] = (0, None)
+                nd[("mrab", k)] = (0, None, 0)
         elif ins.kind == "valu":
             for k in ins.defs:
-                nd[("vw", k)] = (0, None)
+                nd[("vw", k)] = (0, None, None)
                 nd.pop(("mw", k), None)   # later reads see this write (its WAW was checked)
                 if ins.trans:
-                    nd[("tw", k)] = (0, None)
+                    nd[("tw", k)] = (0, None, None)
                 if ins.perm:
-                    nd[("pw", k)] = (0, None)
+                    nd[("pw", k)] = (0, None, None)
                 if ins.dot:
-                    nd[("dw", k)] = (0, None)
+                    nd[("dw", k)] = (0, None, None)
                 if k[0] == "s" or k == ("x", "vcc"):
-                    nd[("vws", k)] = (0, None)
+                    nd[("vws", k)] = (0, None, None)
         elif ins.kind == "salu":
             for k in ins.defs:
                 if k == ("x", "m0"):
-                    nd[("sm0", k)] = (0, None)
+                    nd[("sm0", k)] = (0, None, None)
         if ins.kind == "vmem" and ins.std:
             for k in ins.std:
-                nd[("std", k)] = (0, None)
+                nd[("std", k)] = (0, None, None)
         # --- counters
         if ins.mem == "lgkm":
             lg = lg + (frozenset(ins.defs),)
@@ -481,6 +493,7 @@ TMP = [v(160 + 8 * t, 8) for t in range(3)]
 # steady walk does not use (the output, the first tile's max and the redo path
 # keep their temporaries elsewhere while fragments are in flight).
 NSLOT, LOOK = 8, 6
+STEADY_SPAN = 55   # the steady softmax spreads its 64 elements over gaps 0..STEADY_SPAN
 FRAG = [v(184 + 4 * t, 4) for t in range(4)] + [v(224 + 4 * t, 4) for t in range(4)]
 MRUN = [v(200), v(201)]
 LRUN = [v(202), v(203)]
@@ -524,12 +537,12 @@ T = [s(76 + j) for j in range(8)]
 CMPA = s(84, 2)
 CMPB = s(86, 2)
 ONES, BOUND, PASS, WAVE, GRID, LDSB = (s(88 + j) for j in range(6))
-# Slot bases of the walk's iterations: s31 (the kernel-argument block's pad)
-# and temporaries the query-tile setup uses only before the walk.
-SKRD = s(31)          # K read slot base of the iteration (K tile i + 1)
-SVRD = T[5]           # V slot base of tile i
-SVLD = T[6]           # V load destination (tile i + 2, this wave's quarter)
-SKLD = T[7]           # K load destination (tile i + 4, this wave's quarter)
+# s31 (the kernel-argument block's pad) and temporaries the query-tile setup
+# uses only before the walk. WOFF = LDS base + 4 KB x wave: this wave's quarter
+# of a ring slot.
+LIM = s(31)           # the steady walk runs while ITER < LIM = WT - 1
+SVLD = T[6]           # idle iterations: V load destination (tile i + 2)
+SKLD = T[7]           # idle iterations: K load destination (tile i + 4)
 N_SGPR_OWN = 94       # s0..s93 (except s32, s33, which the compiler reserves)
 
 IN_S = ["ka", "wg", "ng", "wv", "lb"]
@@ -562,21 +575,30 @@ def rsrc_at(r, head, off_s, size_s):
             S("s_max_i32", r[2], r[2], 0), S("s_mov_b32", r[3], RSRC3)]
 
 
-def k_frag_reads(f_slot, ks, mb, first_of_ks):
-    """K fragment (ks, mb): one ds_read_b128 of the lane's key row krow + 32 mb,
-    logical 16-byte chunk 2 ks + h (the XOR 32 ks on the lane's base)."""
+def k_frag_reads(f_slot, ks, mb, first_of_ks, kslot):
+    """K fragment (ks, mb) of the tile in ring slot kslot: one ds_read_b128 of
+    the lane's key row krow + 32 mb, logical 16-byte chunk 2 ks + h (the XOR
+    32 ks on the lane's base)."""
     out = []
     addr = KA if ks == 0 else KX
     if first_of_ks and ks > 0:
         out.append(V("v_xor_b32", KX, 32 * ks, KA))
-    out.append(DSR("ds_read_b128", FRAG[f_slot], addr, 8192 * mb))
+    out.append(DSR("ds_read_b128", FRAG[f_slot], addr, SLOT * kslot + 8192 * mb))
     return out
 
 
-def v_frag_reads(f_slot, kk, ob):
-    """V^T fragment (O^T block ob, P^T k-step kk): two ds_read_b64_tr_b16."""
-    return [DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(0, 2), VA[ob][0], 4096 * kk),
-            DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(2, 2), VA[ob][1], 4096 * kk)]
+def v_frag_reads(f_slot, kk, ob, vslot):
+    """V^T fragment (O^T block ob, P^T k-step kk) of the tile in ring slot
+    vslot: two ds_read_b64_tr_b16."""
+    return [DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(0, 2), VA[ob][0], SLOT * vslot + 4096 * kk),
+            DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(2, 2), VA[ob][1], SLOT * vslot + 4096 * kk)]
+
+
+def rsrc_step(r):
+    """Resource r moved on by one tile: base + SLOT, size - SLOT (at least 0).
+    The carry pair is one bundle, so no SCC writer lands between."""
+    return [[S("s_add_u32", r[0], r[0], SLOT), S("s_addc_u32", r[1], r[1], 0)],
+            [S("s_sub_i32", r[2], r[2], SLOT)], [S("s_max_i32", r[2], r[2], 0)]]
 
 
 class VOp:
@@ -928,16 +950,22 @@ def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
 
     for g in range(-1, nm):
         used = 0
-        while True:
-            cands = [it for it in pending if ready(it, g)]
-            if not cands:
-                break
-            forced = [it for it in cands if it.hi is not None and it.hi <= g]
-            pick = min(forced or cands, key=lambda it: (it.hi if it.hi is not None else 10 ** 6, it.seq))
-            if not forced and used + pick.size > cap:
-                break
-            place(pick)
-            used += pick.size
+        # LDS and vector-memory bundles lead the gap: issued behind VALU work
+        # (a transcendental in particular) they hold up the next MFMA
+        # (measured on gfx950: +2.3 cycles per MFMA for an LDS read at the end
+        # of the gap, +3 for an LDS DMA, nothing at its start)
+        for mem_only in (True, False):
+            while True:
+                cands = [it for it in pending if ready(it, g) and
+                         (not mem_only or it.ins[0].kind in ("lds", "vmem"))]
+                if not cands:
+                    break
+                forced = [it for it in cands if it.hi is not None and it.hi <= g]
+                pick = min(forced or cands, key=lambda it: (it.hi if it.hi is not None else 10 ** 6, it.seq))
+                if not forced and used + pick.size > cap:
+                    break
+                place(pick)
+                used += pick.size
         late = [it for it in pending if it.hi is not None and it.hi <= g]
         assert not late, f"gap {g}: items past their deadline: {[x.ins[0].text for x in late]}"
         if g + 1 < nm:
@@ -962,31 +990,12 @@ def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
         else:
             out.append(NOP(0))
     out.extend(tail)
-    return hoist_memory(out)
+    return out
 
 
 def _conflict(a, b):
     da, ua, db, ub = set(a.defs), set(a.uses), set(b.defs), set(b.uses)
     return bool(da & ub or ua & db or da & db)
-
-
-def hoist_memory(prog):
-    """Within each gap between two MFMAs, move LDS and vector-memory
-    instructions ahead of independent VALU / SALU work: issued behind VALU
-    work (a transcendental in particular) they hold up the next MFMA
-    (measured on gfx950: +2.3 cycles per MFMA for an LDS read at the end of
-    the gap, +3 for an LDS DMA, nothing at its start). Nothing moves across an
-    MFMA, a wait, a nop, a label or a branch."""
-    out = []
-    for x in prog:
-        if x.kind in ("lds", "vmem"):
-            j = len(out)
-            while j > 0 and out[j - 1].kind in ("valu", "salu") and not _conflict(out[j - 1], x):
-                j -= 1
-            out.insert(j, x)
-        else:
-            out.append(x)
-    return out
 
 
 def pre_reads_log_for(pre_reads, reads):
@@ -1020,58 +1029,45 @@ class Gen:
             self.prog.append(x)
 
     # ------------------------------------------------------------ iteration parts
-    def iter_scalars(self):
-        """Slot bases and load resources of iteration ITER (tiles i+1 K read,
-        i V read, i+4 K load, i+2 V load)."""
-        t0, t1, t2, t3 = T[0], T[1], T[2], T[3]
-        out = [
-            S("s_add_i32", t0, ITER, 1), S("s_and_b32", t0, t0, 3), S("s_lshl_b32", t0, t0, 14),
-            S("s_add_u32", SKRD, t0, LDSB),
-            S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14),
-            S("s_add_u32", SVRD, t1, LDSB), S("s_add_u32", SVRD, SVRD, LDS_V),
-            S("s_add_u32", SKLD, t1, LDSB), S("s_add_u32", SKLD, SKLD, WOFF),
-            S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
-            S("s_add_u32", SVLD, t2, LDSB), S("s_add_u32", SVLD, SVLD, LDS_V + 0),
-            S("s_add_u32", SVLD, SVLD, WOFF),
-            S("s_add_i32", t3, ITER, 4), S("s_lshl_b32", t3, t3, 14),
-        ] + rsrc_at(RK, KH, t3, KVB) + [
-            S("s_add_i32", t3, ITER, 2), S("s_lshl_b32", t3, t3, 14),
-        ] + rsrc_at(RV, VH, t3, KVB)
-        return out
+    # Ring slots. Iteration i (u = i mod 4) reads K tile i + 1 (QK), V tile
+    # i - 1 (PV) and V tile i (the next PV's first fragments), and loads K
+    # tile i + 4 and V tile i + 2; tile t lives in slot t mod 4 of its ring.
+    # Every iteration but the idle one has its u fixed where it is generated,
+    # so the slots are instruction offsets on addresses fixed for the kernel.
+    @staticmethod
+    def slots(u):
+        return dict(krd=(u + 1) % 4, vpv=(u + 3) % 4, vpre=u, kld=u, vld=(u + 2) % 4)
 
-    def load_ops(self):
-        """The 8 LDS-DMA loads of an iteration: K tile i+4, then V tile i+2
-        (each 4 x 1 KB, this wave's 16 rows), as 8 groups [m0 write, nop, load]."""
+    def load_groups(self, u):
+        """The 8 LDS-DMA loads of iteration i (u = i mod 4): K tile i+4, then V
+        tile i+2, this wave's 16 rows of each as 4 x 1 KB. M0 is set once per
+        tile (the instruction offset steps the LDS and global addresses by
+        1 KB together); RK and RV move on to tiles i+5 and i+3 after their last
+        load. 8 groups, one load each."""
+        sl = self.slots(u)
         groups = []
-        for j in range(4):
-            groups.append([S("s_add_u32", M0, SKLD, 1024 * j), NOP(0), BLOAD_LDS(INV[f"loff{j}"], RK)])
-        for j in range(4):
-            groups.append([S("s_add_u32", M0, SVLD, 1024 * j), NOP(0), BLOAD_LDS(INV[f"loff{j}"], RV)])
+        for r, base in ((RK, SLOT * sl["kld"]), (RV, LDS_V + SLOT * sl["vld"])):
+            for j in range(4):
+                pre = [S("s_add_u32", M0, WOFF, base), NOP(0)] if j == 0 else []
+                groups.append(pre + [BLOAD_LDS(INV[f"loff{j}"], r, 1024 * j)])
+        groups[4] += [x for b in rsrc_step(RK) for x in b]
+        groups[7] += [x for b in rsrc_step(RV) for x in b]
         return groups
 
     def barrier(self, vm):
         return [WAIT(vm=vm), BAR()]
 
-    def ka_update(self):
-        return [V("v_add_u32", KA, SKRD, INV["kofs"])]
-
-    def va_update(self):
-        out = [V("v_add_u32", VA[0][0], SVRD, INV["vofs1"]), V("v_add_u32", VA[0][1], SVRD, INV["vofs2"])]
-        for ob in range(1, 4):
-            out += [V("v_xor_b32", VA[ob][0], 64 * ob, VA[0][0]), V("v_xor_b32", VA[ob][1], 64 * ob, VA[0][1])]
-        return out
-
-    def mfma_lists(self, pv, qk_par):
-        """MFMA list [(Ins, frag)] and frag reads {frag: [Ins]} of an iteration
-        with PV (of the tile whose V addresses are in VA) and/or QK into
-        SACC[qk_par] (K addresses from KA)."""
+    def mfma_lists(self, pv, qk_par, u):
+        """MFMA list [(Ins, frag)] and frag reads {frag: [Ins]} of iteration
+        i = u (mod 4) with PV(i - 1) and/or QK(i + 1) into SACC[qk_par]."""
+        sl = self.slots(u)
         mf, reads = [], {}
         f = 0
         if pv:
             for kk in range(4):
                 for ob in range(4):
                     slot = f % NSLOT
-                    reads[f] = v_frag_reads(slot, kk, ob)
+                    reads[f] = v_frag_reads(slot, kk, ob, sl["vpv"])
                     for nb in range(2):
                         mf.append((MFMA(OACC[ob][nb], FRAG[slot], PB[kk][nb], OACC[ob][nb]), f))
                     f += 1
@@ -1079,7 +1075,7 @@ class Gen:
             for ks in range(8):
                 for mb in range(2):
                     slot = f % NSLOT
-                    reads[f] = k_frag_reads(slot, ks, mb, mb == 0)
+                    reads[f] = k_frag_reads(slot, ks, mb, mb == 0, sl["krd"])
                     for nb in range(2):
                         dst = SACC[qk_par][mb][nb]
                         mf.append((MFMA(dst, FRAG[slot], QA[nb][ks], None if ks == 0 else dst), f))
@@ -1089,26 +1085,25 @@ class Gen:
                 x.frag = fr
         return mf, reads, f
 
-    # the V(i) fragments 0..2 read at the end of an iteration for the next PV
-    def v_prefetch(self, nf):
+    # the V(i) fragments 0..LOOK-1 read at the end of an iteration for the next PV
+    def v_prefetch(self, nf, u):
         reads = {}
         for j in range(LOOK):
-            lst = v_frag_reads((nf + j) % NSLOT, j // 4, j % 4)
+            lst = v_frag_reads((nf + j) % NSLOT, j // 4, j % 4, self.slots(u)["vpre"])
             for x in lst:
                 x.frag = nf + j
             reads[nf + j] = lst
         return reads
 
-    def mfma_iteration(self, name, pv, qk_par, sm, prefetch, side_extra=None, budget=30, end_ops=(), fixed=None):
-        mf, reads, nf = self.mfma_lists(pv, qk_par)
+    def mfma_iteration(self, name, u, pv, qk_par, sm, prefetch, side_extra=None, budget=30, end_ops=(), fixed=None):
+        mf, reads, nf = self.mfma_lists(pv, qk_par, u)
         pre = set(range(LOOK)) if pv else set()
         if prefetch:
-            reads.update(self.v_prefetch(nf))
+            reads.update(self.v_prefetch(nf, u))
         side = {}
         nm = len(mf)
-        # scalars at gap -1, loads spread over the stream
-        side[-1] = self.iter_scalars()
-        loads = self.load_ops()
+        # loads spread over the stream
+        loads = self.load_groups(u)
         for j, grp in enumerate(loads):
             gap = (j * nm) // 8 + 1 if nm else -1
             side.setdefault(min(gap, nm - 1) if nm else -1, []).extend(grp)
@@ -1189,9 +1184,10 @@ class Gen:
                 V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
                 LABEL(ret_label)]
 
-    def redo_block(self, label, ret_label, p, masked):
+    def redo_block(self, label, ret_kind, p, masked):
         """Rare path: a tile sum passed the bound. New max of S^T[p], O and l
-        rescaled, exponentials again (straight-line)."""
+        rescaled, exponentials again (straight-line); back to the copy of the
+        iteration (u = ITER mod 4, u = p or p + 2) it came from."""
         # temporaries in TMP and PB: the next tile's first V^T fragments are in
         # flight into the fragment slots
         R = TMP[1]
@@ -1247,7 +1243,8 @@ class Gen:
                 V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]),
                 V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]),
                 V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
-                BR(ret_label)]
+                S("s_and_b32", T[0], ITER, 3), S("s_cmp_eq_u32", T[0], p),
+                CBR("s_cbranch_scc1", self.L(f"{ret_kind}{p}")), BR(self.L(f"{ret_kind}{p + 2}"))]
         return out
 
     def stale_softmax(self, p, masked, kk_release):
@@ -1263,29 +1260,29 @@ class Gen:
             for nb in range(2):
                 for r in range(16):
                     sm.add(ACCW(OACC[ob][nb][r], 0))
-        side = {-1: self.ka_update()}
-        return self.mfma_iteration("fill", False, 0, sm, False, side_extra=side, budget=40)
+        return self.mfma_iteration("fill", 3, False, 0, sm, False, budget=40)
 
     def it_first(self):
         """i = 0 (walk of >= 2 tiles): softmax(0) with the row max, QK(1)."""
         sm = self.first_softmax(False)
-        side = {-1: self.ka_update(), 2 * (16 - LOOK): self.va_update()}
-        return self.mfma_iteration("first", False, 1, sm, True, side_extra=side, budget=48,
-                                   end_ops=self.tail_first())
+        return self.mfma_iteration("first", 0, False, 1, sm, True, budget=48, end_ops=self.tail_first())
 
     def it_first_last(self):
         """i = 0 of a one-tile walk: masked softmax(0), no MFMAs."""
         sm = self.first_softmax(True)
-        side = {-1: self.va_update()}
+        side = {}
         if not self.causal:
-            side[-1] += [V("v_sub_u32", DREM, KVEND, INV["h8"])]   # keys >= S of tile 0
-        return self.mfma_iteration("first_last", False, None, sm, True, side_extra=side, budget=10 ** 6,
+            side[-1] = [V("v_sub_u32", DREM, KVEND, INV["h8"])]   # keys >= S of tile 0
+        return self.mfma_iteration("first_last", 0, False, None, sm, True, side_extra=side, budget=10 ** 6,
                                    end_ops=self.tail_first())
 
-    def it_steady(self, p):
-        """1 <= i <= wt-2: PV(i-1), QK(i+1) into SACC[1-p], softmax(i) of SACC[p]
-        and the loads of K tile i+4 and V tile i+2, placed by slot_schedule."""
-        mf, reads, nf = self.mfma_lists(True, 1 - p)
+    def it_steady(self, u):
+        """1 <= i <= wt-2 (u = i mod 4): PV(i-1), QK(i+1) into SACC[1-p],
+        softmax(i) of SACC[p] (p = u % 2) and the loads of K tile i+4 and V
+        tile i+2, placed by slot_schedule."""
+        p = u % 2
+        sl = self.slots(u)
+        mf, reads, nf = self.mfma_lists(True, 1 - p, u)
         items = []
 
         def add(ins, lo=-1, hi=None, deps=()):
@@ -1293,37 +1290,34 @@ class Gen:
             items.append(it)
             return it
 
-        def chain(ops, lo=-1, after=()):
-            prev, first = None, None
-            for x in ops:
-                it = add(x, lo, None, ([(prev, 0)] if prev else []) + [(a_, 0) for a_ in after])
-                first = first or it
-                prev = it
-            return prev
-        t0, t1, t2, t3, t4 = T[0], T[1], T[2], T[3], T[4]
-        # slot bases: K read tile i+1, V tile i, K load tile i+4 (slot of i),
-        # V load tile i+2; load resources of tiles i+4 (K) and i+2 (V)
-        skrd = chain([S("s_add_i32", t0, ITER, 1), S("s_and_b32", t0, t0, 3), S("s_lshl_b32", t0, t0, 14),
-                      S("s_add_u32", SKRD, t0, LDSB)])
-        t1d = chain([S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14)])
-        svrd = chain([S("s_add_u32", SVRD, t1, LDSB), S("s_add_u32", SVRD, SVRD, LDS_V)], after=[t1d])
-        skld = chain([S("s_add_u32", SKLD, t1, LDSB), S("s_add_u32", SKLD, SKLD, WOFF)], after=[t1d])
-        svld = chain([S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
-                      S("s_add_u32", SVLD, t2, LDSB), S("s_add_u32", SVLD, SVLD, LDS_V),
-                      S("s_add_u32", SVLD, SVLD, WOFF)])
-        rk = chain([S("s_add_i32", t3, ITER, 4), S("s_lshl_b32", t3, t3, 14)] + rsrc_at(RK, KH, t3, KVB))
-        rv = chain([S("s_add_i32", t4, ITER, 2), S("s_lshl_b32", t4, t4, 14)] + rsrc_at(RV, VH, t4, KVB))
-        # loads: one per 8 gaps, K then V (the barrier's vmcnt assumes this order)
-        prev = None
+        # The iteration's barrier, behind its first MFMA (which reads a V(i-1)
+        # fragment read in the previous iteration): it orders every wave's
+        # reads of iteration i-1 before this iteration's loads into the slots
+        # they read, and (after vmcnt(8): the loads of i-2 and older have
+        # landed) the V(i) prefetch after the tile's arrival. The reads of
+        # this iteration before the prefetch are of tiles that landed by the
+        # previous barrier (K(i+1) and V(i-1) were loaded in iteration i-3).
+        bar = add([WAIT(vm=8), BAR()], 0, 0)
+        # loads: one per 8 gaps, K then V (the barrier's vmcnt assumes this
+        # order); M0 once per tile, written in an earlier gap than its first
+        # load (the MFMA between gives the wait state, and the load can lead
+        # its gap) and after the last load that reads the old value
+        prev = bar
+        last = {}
         for j in range(8):
-            k = j < 4
-            deps = [(skld if k else svld, 0)] + ([(prev, 0)] if prev else [])
-            # the M0 write in an earlier gap than its load: the MFMA between
-            # gives the wait state, and the load can lead its own gap
-            m = add(S("s_add_u32", M0, SKLD if k else SVLD, 1024 * (j % 4)), 8 * j - 1, 8 * j, deps)
-            prev = add(BLOAD_LDS(INV[f"loff{j % 4}"], RK if k else RV), 1 + 8 * j, 61,
-                       [(m, M0_WS), (rk if k else rv, 0)])
-        ka = add(V("v_add_u32", KA, SKRD, INV["kofs"]), -1, 2 * (16 - LOOK) - 1, [(skrd, 0)])
+            r = RK if j < 4 else RV
+            deps = [(prev, 0)] if prev else []
+            if j % 4 == 0:
+                base = SLOT * sl["kld"] if j < 4 else LDS_V + SLOT * sl["vld"]
+                m = add(S("s_add_u32", M0, WOFF, base), 8 * j - 1, 8 * j, deps)
+                deps = deps + [(m, M0_WS)]
+            prev = add(BLOAD_LDS(INV[f"loff{j % 4}"], r, 1024 * (j % 4)), 1 + 8 * j, 61, deps)
+            last[r.i] = prev
+        # the resources move on to tiles i+5 (K) and i+3 (V) after their last load
+        for r in (RK, RV):
+            dep = last[r.i]
+            for b in rsrc_step(r):
+                dep = add(b, -1, None, [(dep, 0)])
         # fragment reads: slot f % NSLOT is free after the MFMAs of fragment f - NSLOT
         fitem = {}
         xitem = None
@@ -1334,29 +1328,24 @@ class Gen:
             lds = [x for x in reads[f] if x.kind == "lds"]
             if f >= 16:                       # K fragment (ks, mb) = ((f-16)//2, (f-16)%2)
                 ks, mb = (f - 16) // 2, (f - 16) % 2
-                deps.append((ka, 0))
                 xor = [x for x in reads[f] if x.kind != "lds"]
                 if xor:                        # KX for this ks, after the last read of the old one
-                    xitem = add(xor, lo - 2, 2 * f - 6, [(ka, 0)] + ([(fitem[f - 1], 0)] if f - 1 >= 16 else []))
+                    xitem = add(xor, lo - 2, 2 * f - 6, [(fitem[f - 1], 0)] if f - 1 >= 16 else [])
                 if ks > 0:
                     deps.append((xitem, 0))
             fitem[f] = add(lds, lo, 2 * f - 5, deps)
-        # V(i) addresses after the last PV(i-1) read, before the prefetch
-        va0 = [add(V("v_add_u32", VA[0][j], SVRD, INV[f"vofs{j + 1}"]), 0, 44, [(fitem[15], 0), (svrd, 0)])
-               for j in range(2)]
-        vas = list(va0)
-        for ob in range(1, 4):
-            for j in range(2):
-                vas.append(add(V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]), 0, 46, [(va0[j], 0), (fitem[15], 0)]))
         # prefetch of V(i) fragments 0..LOOK-1 into the next iteration's slots
-        pre_next = self.v_prefetch(nf)
+        pre_next = self.v_prefetch(nf, u)
         for f, lst in sorted(pre_next.items()):
-            add(lst, max(2 * (f - NSLOT) + 1, 2 * (f - LOOK)), None, [(x, 0) for x in vas])
+            add(lst, max(2 * (f - NSLOT) + 1, 2 * (f - LOOK)), None, [(bar, 0)])
         # softmax of tile i: element e (group e / 8 = (kk, nb)), fp32 row sums
         rel = [8 * kk + 7 for kk in range(4)]
         tmp = [v(160 + j) for j in range(24)]
         fma, exp, adds, cvt = {}, {}, {}, {}
         for e in range(64):
+            # element e around gap pos: the 64 elements over gaps 0..SPAN, so
+            # the tile sums and the redo check fit before the last MFMA
+            pos = (e * STEADY_SPAN) // 63
             g = e // 8
             kk, nb = g // 2, g % 2
             srcr = SACC[p][kk // 2][nb][8 * (kk % 2) + e % 8]
@@ -1366,20 +1355,20 @@ class Gen:
             deps = []
             if e >= 24:
                 deps += [(adds[e - 24], 0), (cvt[(e - 24) // 2], 0)]
-            fma[e] = add(x, max(0, e - 3), e + 1, deps)
-            exp[e] = add(V("v_exp_f32", t, t, trans=True), e, e + 2, [(fma[e], 0)])
+            fma[e] = add(x, max(0, pos - 3), pos + 1, deps)
+            exp[e] = add(V("v_exp_f32", t, t, trans=True), pos, pos + 2, [(fma[e], 0)])
             if e % 2 == 1:
                 i = e // 2
+                lo = max(pos + 1, rel[kk])
                 cvt[i] = add(V("v_cvt_pk_bf16_f32", PB[kk][nb][(e % 8) // 2], tmp[(e - 1) % 24], t),
-                             max(e + 1, rel[kk]), max(e + 1, rel[kk]) + 6,
-                             [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
+                             lo, min(lo + 6, 62), [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
             acc = PSUM[nb][e % 2]
             init = kk == 0 and e % 8 < 2
             deps = [(exp[e], TRANS_FWD)]
             if not init:
                 prev_same = max(j for j in adds if (j // 8) % 2 == nb and j % 2 == e % 2)
                 deps.append((adds[prev_same], 0))
-            adds[e] = add(V("v_add_f32", acc, 0 if init else acc, t), e + 1, e + 4, deps)
+            adds[e] = add(V("v_add_f32", acc, 0 if init else acc, t), pos + 1, pos + 4, deps)
         # tile sums (nb = 0 is complete before the stream ends)
         last0 = [adds[e] for e in range(64) if (e // 8) % 2 == 0]
         last1 = [adds[e] for e in range(64) if (e // 8) % 2 == 1]
@@ -1387,36 +1376,45 @@ class Gen:
         c0 = add(V("v_cmp_nle_f32", CMPA, PSUM[0][0], BOUND), 0, None, [(s0, 0)])
         s1 = add(V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]), 0, None, [(a_, 0) for a_ in last1])
         c1 = add(V("v_cmp_nle_f32", CMPB, PSUM[1][0], BOUND), 0, None, [(s1, 0)])
-        tail = [NOP(VALU_SGPR_VMEM - 1), S("s_or_b64", CMPA, CMPA, CMPB),
-                CBR("s_cbranch_scc1", self.L(f"redo_s{p}")),
-                V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]),
-                V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
-                LABEL(self.L(f"ret_s{p}"))]
+        # the redo check before the last MFMA (QK(i+1) does not read the
+        # sums; PV(i-1) is complete, so the redo path may rescale O); the redo
+        # path adds its own sums to l and comes back to the label
+        add([S("s_or_b64", CMPA, CMPA, CMPB), CBR("s_cbranch_scc1", self.L(f"redo_s{p}")),
+             V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]), V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
+             LABEL(self.L(f"ret_s{u}"))], 0, len(mf) - 2, [(c0, VALU_SGPR_VMEM), (c1, VALU_SGPR_VMEM)])
         pre_log = [f for f in range(LOOK) for _ in range(2)]
-        return slot_schedule(mf, items, pre_log, cap=7, tail=tail)
+        return slot_schedule(mf, items, pre_log, cap=7)
 
-    def it_last(self, p):
-        """i = wt-1 >= 1: PV(i-1), masked softmax(i) of SACC[p]."""
+    def it_last(self, u):
+        """i = wt-1 >= 1 (u = i mod 4): PV(i-1), masked softmax(i) of SACC[u % 2]."""
+        p = u % 2
         rel = [8 * kk + 8 for kk in range(4)]
         sm = self.stale_softmax(p, True, rel)
-        # V(i) addresses between the last PV(i-1) fragment read (gap
-        # 2 (15 - LOOK)) and the first prefetch read (gap 2 (16 - LOOK), after
-        # the gap's side ops)
-        side = {2 * (16 - LOOK): self.va_update()}
+        side = {}
         if not self.causal:
             side[-1] = [S("s_lshl_b32", T[4], ITER, 6), S("s_sub_i32", T[4], KVEND, T[4]),
                         V("v_sub_u32", DREM, T[4], INV["h8"])]
-        return self.mfma_iteration(f"last{p}", True, None, sm, True, side_extra=side, budget=40,
-                                   end_ops=self.tail_stale(self.L(f"redo_l{p}"), self.L(f"ret_l{p}")))
+        return self.mfma_iteration(f"last{u}", u, True, None, sm, True, side_extra=side, budget=40,
+                                   end_ops=self.tail_stale(self.L(f"redo_l{p}"), self.L(f"ret_l{u}")))
 
-    def it_drain(self):
-        """i = wt: PV(wt-1)."""
-        return self.mfma_iteration("drain", True, None, None, False, end_ops=[WAIT(lgkm=0)])
+    def it_drain(self, u):
+        """i = wt (u = i mod 4): PV(wt-1)."""
+        return self.mfma_iteration(f"drain{u}", u, True, None, None, False, end_ops=[WAIT(lgkm=0)])
 
     def it_idle(self):
-        out = self.iter_scalars()
-        for grp in self.load_ops():
-            out += grp
+        """An iteration with no tile of this wave's walk: its share of the loads
+        only, slots and resources from ITER."""
+        t1, t2, t3 = T[1], T[2], T[3]
+        out = [S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14), S("s_add_u32", SKLD, t1, WOFF),
+               S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
+               S("s_add_u32", SVLD, t2, WOFF), S("s_add_u32", SVLD, SVLD, LDS_V),
+               S("s_add_i32", t3, ITER, 4), S("s_lshl_b32", t3, t3, 14)] + rsrc_at(RK, KH, t3, KVB) + [
+               S("s_add_i32", t3, ITER, 2), S("s_lshl_b32", t3, t3, 14)] + rsrc_at(RV, VH, t3, KVB)
+        for r, base in ((RK, SKLD), (RV, SVLD)):
+            for j in range(4):
+                out += ([S("s_mov_b32", M0, base), NOP(0)] if j == 0 else []) + [BLOAD_LDS(INV[f"loff{j}"], r, 1024 * j)]
+        for r in (RK, RV):
+            out += [x for b in rsrc_step(r) for x in b]
         return out
 
     # ------------------------------------------------------------ output
@@ -1518,24 +1516,21 @@ class Gen:
         # Q offsets of the lane's two rows
         out += [S("s_lshl_b32", t[0], QW0, 8), V("v_add_u32", QOFF[0], t[0], INV["qlane"]),
                 V("v_add_u32", QOFF[1], 0x2000, QOFF[0])]
-        # prologue loads: K(0), Q, K(1), K(2), V(0)
-        def kload(tile):
-            o = [S("s_mov_b32", t[3], tile * SLOT)] + rsrc_at(RK, KH, t[3], KVB)
-            base = tile * SLOT
-            for j in range(4):
-                o += [S("s_add_u32", M0, LDSB, base + 1024 * j), S("s_add_u32", M0, M0, WOFF), NOP(0),
-                      BLOAD_LDS(INV[f"loff{j}"], RK)]
-            return o
-        out += kload(0)
+        # prologue loads: K(0), Q, K(1), K(2), V(0); then the resources of the
+        # first iteration's loads (K tile 3, V tile 1)
+        def load(r, dst):
+            o = [S("s_add_u32", M0, WOFF, dst), NOP(0)]
+            return o + [BLOAD_LDS(INV[f"loff{j}"], r, 1024 * j) for j in range(4)]
+        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RK, KH, t[3], KVB) + load(RK, 0)
         out += NOPS(2)
         for nb in range(2):
             for ks in range(8):
                 out.append(BLOAD("buffer_load_dwordx4", QA[nb][ks], QOFF[nb], RQ, 32 * ks))
-        out += kload(1) + kload(2)
-        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RV, VH, t[3], KVB)
-        for j in range(4):
-            out += [S("s_add_u32", M0, LDSB, LDS_V + 1024 * j), S("s_add_u32", M0, M0, WOFF), NOP(0),
-                    BLOAD_LDS(INV[f"loff{j}"], RV)]
+        for tile in (1, 2):
+            out += [x for b in rsrc_step(RK) for x in b] + load(RK, tile * SLOT)
+        out += [x for b in rsrc_step(RK) for x in b]
+        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RV, VH, t[3], KVB) + load(RV, LDS_V)
+        out += [x for b in rsrc_step(RV) for x in b]
         # ---- the walk
         out += [S("s_mov_b32", ITER, -1)] + self.barrier(12)
         out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("idle_m1"))]
@@ -1547,21 +1542,26 @@ class Gen:
         out += self.it_idle() + [BR(L("it1"))]
         out += [LABEL(L("first"))] + self.it_first() + [BR(L("it1"))]
         out += [LABEL(L("first_last"))] + self.it_first_last() + [BR(L("it1"))]
-        out += [LABEL(L("it1")), S("s_mov_b32", ITER, 1)]
-        out += [LABEL(L("steady_chk")), S("s_sub_i32", t[0], WT, 2), S("s_cmp_le_i32", ITER, t[0]),
-                CBR("s_cbranch_scc0", L("after_steady")), S("s_bitcmp1_b32", ITER, 0),
-                CBR("s_cbranch_scc1", L("steady1"))]
-        for p in (0, 1):
-            out += [LABEL(L(f"steady{p}"))] + self.barrier(8) + self.it_steady(p)
-            out += [S("s_add_i32", ITER, ITER, 1), BR(L("steady_chk"))]
-        out += [LABEL(L("after_steady")), S("s_sub_i32", t[0], WT, 1), S("s_cmp_eq_u32", ITER, t[0]),
-                CBR("s_cbranch_scc0", L("drain_chk")), S("s_bitcmp1_b32", ITER, 0),
-                CBR("s_cbranch_scc1", L("last1"))]
-        for p in (0, 1):
-            out += [LABEL(L(f"last{p}"))] + self.barrier(8) + self.it_last(p)
-            out += [S("s_add_i32", ITER, ITER, 1), BR(L("drain_chk"))]
-        out += [LABEL(L("drain_chk")), S("s_cmp_eq_u32", ITER, WT), CBR("s_cbranch_scc0", L("idle_chk"))]
-        out += self.barrier(8) + self.it_drain() + [S("s_add_i32", ITER, ITER, 1)]
+        # i = 1: steady while i < wt - 1, then last (i = wt - 1), drain (i = wt);
+        # a copy per i mod 4 of each, chained in walk order
+        out += [LABEL(L("it1")), S("s_mov_b32", ITER, 1), S("s_sub_i32", LIM, WT, 1),
+                S("s_cmp_lt_i32", ITER, LIM), CBR("s_cbranch_scc1", L("steady1")),
+                S("s_cmp_eq_u32", ITER, LIM), CBR("s_cbranch_scc1", L("last1")),
+                S("s_cmp_eq_u32", ITER, WT), CBR("s_cbranch_scc1", L("drain1")),
+                BR(L("idle_chk"))]
+        for u in (1, 2, 3, 0):
+            out += [LABEL(L(f"steady{u}"))] + self.it_steady(u)
+            out += [S("s_add_i32", ITER, ITER, 1), S("s_cmp_lt_i32", ITER, LIM)]
+            if u == 0:
+                out += [CBR("s_cbranch_scc1", L("steady1")), BR(L("last1"))]
+            else:
+                out += [CBR("s_cbranch_scc0", L(f"last{(u + 1) % 4}"))]
+        for u in range(4):
+            out += [LABEL(L(f"last{u}"))] + self.barrier(8) + self.it_last(u)
+            out += [S("s_add_i32", ITER, ITER, 1), BR(L(f"drain{(u + 1) % 4}"))]
+        for u in range(4):
+            out += [LABEL(L(f"drain{u}"))] + self.barrier(8) + self.it_drain(u)
+            out += [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("idle_chk")), S("s_cmp_le_i32", ITER, NT), CBR("s_cbranch_scc0", L("walk_end"))]
         out += self.barrier(8) + self.it_idle() + [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("walk_end"))] + [WAIT(vm=0, lgkm=0), BAR()]
@@ -1573,8 +1573,8 @@ class Gen:
     def redo_blocks(self):
         out = []
         for p in (0, 1):
-            out += self.redo_block(self.L(f"redo_s{p}"), self.L(f"ret_s{p}"), p, False)
-            out += self.redo_block(self.L(f"redo_l{p}"), self.L(f"ret_l{p}"), p, True)
+            out += self.redo_block(self.L(f"redo_s{p}"), "ret_s", p, False)
+            out += self.redo_block(self.L(f"redo_l{p}"), "ret_l", p, True)
         return out
 
     def kernel(self):
@@ -1582,8 +1582,15 @@ class Gen:
         out = [SLOAD("s_load_dwordx16", s(0, 16), INS_["ka"], 0), SLOAD("s_load_dwordx16", s(16, 16), INS_["ka"], 64),
                S("s_mov_b32", ITEMV, INS_["wg"]), S("s_mov_b32", GRID, INS_["ng"]), S("s_mov_b32", WAVE, INS_["wv"]),
                S("s_mov_b32", LDSB, INS_["lb"]), S("s_mov_b32", ONES, 0x3F803F80), S("s_mov_b32", BOUND, BOUND_F),
-               S("s_lshl_b32", WOFF, INS_["wv"], 12),
+               S("s_lshl_b32", WOFF, INS_["wv"], 12), S("s_add_u32", WOFF, WOFF, INS_["lb"]),
                V("v_mov_b32", NINF, 0xFF800000),
+               # LDS read bases, fixed for the kernel (the ring slot is the
+               # instruction offset; the base is 1 KB aligned, so the XORs on
+               # bits 5-7 commute with it)
+               V("v_add_u32", KA, INS_["lb"], INV["kofs"]),
+               V("v_add_u32", VA[0][0], INS_["lb"], INV["vofs1"]), V("v_add_u32", VA[0][1], INS_["lb"], INV["vofs2"]),
+               V("v_add_u32", VA[0][0], LDS_V, VA[0][0]), V("v_add_u32", VA[0][1], LDS_V, VA[0][1])] + [
+               V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]) for ob in range(1, 4) for j in range(2)] + [
                WAIT(lgkm=0)]
         t = T
         out += [LABEL(L("item")), S("s_cmp_ge_u32", ITEMV, NWORK), CBR("s_cbranch_scc1", L("end"))]
@@ -1619,6 +1626,33 @@ class Gen:
         return out
 
 
+_SCC_KEEP = ("s_mov", "s_cselect", "s_mul_i32", "s_mul_hi", "s_nop", "s_waitcnt", "s_barrier", "s_branch",
+             "s_cbranch", "s_load", "s_memtime", "s_movk")
+
+
+def check_scc(prog, name):
+    """Each SCC reader's nearest SCC writer before it in program order is its
+    producer: s_addc_u32 r[i] after s_add_u32 r[i-1]; a select or conditional
+    branch after a compare (s_cmp, s_bitcmp) or s_or_b64 / s_and_b64."""
+    writer = None
+    for k, x in enumerate(prog):
+        if x.kind != "salu" and not (x.kind == "br" and x.cond):
+            continue
+        op = x.text.split()[0]
+        reads = op in ("s_addc_u32", "s_subb_u32") or op.startswith(("s_cselect", "s_cbranch_scc"))
+        if reads:
+            assert writer is not None, f"{name}: {x.text} with no SCC writer before it"
+            wop, wtxt = writer.text.split()[0], writer.text
+            if op in ("s_addc_u32", "s_subb_u32"):
+                lo = x.defs[0][1] - 1
+                ok = wop == {"s_addc_u32": "s_add_u32", "s_subb_u32": "s_sub_u32"}[op] and writer.defs[0] == ("s", lo)
+            else:
+                ok = wop.startswith(("s_cmp", "s_bitcmp")) or wop in ("s_or_b64", "s_and_b64")
+            assert ok, f"{name}: {x.text!r} reads SCC of {wtxt!r} (instruction {k})"
+        if not op.startswith(_SCC_KEEP) and x.kind == "salu":
+            writer = x
+
+
 def to_macro(name, prog):
     lines = []
     for ins in prog:
@@ -1651,6 +1685,7 @@ def main(argv):
         g = Gen(causal)
         prog = g.kernel()
         check(prog, g.tag)
+        check_scc(prog, g.tag)
         text.append(to_macro("CA_PFW64_BODY_" + ("CAUSAL" if causal else "FULL"), prog))
         print(f"variant {g.tag}: {len(prog)} lines {stats(prog)}", file=sys.stderr)
     text.append("#define CA_PFW64_CLOBBERS " + clobbers())

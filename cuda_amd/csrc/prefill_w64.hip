@@ -16,7 +16,8 @@
 // HBM -> LDS by buffer loads into two rings of 4 tiles (K tile t is read by
 // QK in iteration t - 1, V tile t by PV in iteration t + 1, so the rings
 // release their slots at different times), every wave loading a quarter of
-// each tile.
+// each tile. The walk's code has a copy per iteration index mod 4, so every
+// ring slot is an instruction offset on LDS addresses fixed for the kernel.
 //
 // Per wave, iteration i of the walk issues 64 v_mfma_f32_32x32x16_bf16:
 //   PV(i - 1): O^T[128 d x 64 q] += V^T P^T   (A = V^T via ds_read_b64_tr_b16,
@@ -89,12 +90,14 @@ __global__ __launch_bounds__(kW64Threads, 1) void prefill_w64_kernel(PfW64Args a
   const int vofs1 = tr_row * 256 + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
   const int vofs2 = (tr_row + 4) * 256 + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
   // HBM -> LDS: load j of this wave covers tile rows 16 wave + 4 j + lane / 16;
-  // the lane fetches the chunk that belongs at position lane % 16
+  // the lane fetches the chunk that belongs at position lane % 16. The load's
+  // instruction offset (1 KB j) adds to both addresses, so loff[j] leaves out
+  // the 4 j rows.
   int loff[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = 16 * wave + 4 * j + (lane >> 4);
-    loff[j] = row * 256 + 16 * ((lane & 15) ^ swz(row));
+    loff[j] = row * 256 + 16 * ((lane & 15) ^ swz(row)) - 1024 * j;
   }
   const int qlane = l32 * 256 + 16 * h;          // Q row l32, bytes 16 h of each 32
   const int dl = l32 - 8 * h;                    // causal mask: key > query
