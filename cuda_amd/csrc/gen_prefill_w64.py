@@ -494,6 +494,8 @@ TMP = [v(160 + 8 * t, 8) for t in range(3)]
 # keep their temporaries elsewhere while fragments are in flight).
 NSLOT, LOOK = 8, 6
 STEADY_SPAN = 55   # the steady softmax spreads its 64 elements over gaps 0..STEADY_SPAN
+LDS_SLOTS = 1      # issue slots the slot scheduler charges for an LDS read
+GAP_CAP = 7        # issue slots per MFMA gap
 FRAG = [v(184 + 4 * t, 4) for t in range(4)] + [v(224 + 4 * t, 4) for t in range(4)]
 MRUN = [v(200), v(201)]
 LRUN = [v(202), v(203)]
@@ -532,11 +534,15 @@ RL = s(52, 4)
 KH = s(56, 2)
 VH = s(58, 2)
 ITEMV, WORK, BH0, QT0, BH1, QT1, BH, QT = (s(60 + j) for j in range(8))
+NXT = WORK            # after the decode: the next tile's flags
 Q0, KVEND, NT, WT, QW0, KVB, ITER, WOFF = (s(68 + j) for j in range(8))
 T = [s(76 + j) for j in range(8)]
 CMPA = s(84, 2)
 CMPB = s(86, 2)
-ONES, BOUND, PASS, WAVE, GRID, LDSB = (s(88 + j) for j in range(6))
+OQW, BOUND, PASS, WAVE, GRID, LDSB = (s(88 + j) for j in range(6))
+# the finished tile's O resource while the next tile is set up: the redo
+# check's registers, idle between walks
+ORO = s(84, 4)
 # s31 (the kernel-argument block's pad) and temporaries the query-tile setup
 # uses only before the walk. WOFF = LDS base + 4 KB x wave: this wave's quarter
 # of a ring slot.
@@ -592,6 +598,12 @@ def v_frag_reads(f_slot, kk, ob, vslot):
     vslot: two ds_read_b64_tr_b16."""
     return [DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(0, 2), VA[ob][0], SLOT * vslot + 4096 * kk),
             DSR("ds_read_b64_tr_b16", FRAG[f_slot].sl(2, 2), VA[ob][1], SLOT * vslot + 4096 * kk)]
+
+
+def rsrc_base(r, head, size_s):
+    """Resource over bytes [0, size) of the head at `head` (64-bit SGPR pair)."""
+    return [S("s_mov_b32", r[0], head[0]), S("s_and_b32", r[1], head[1], 0xFFFF), S("s_max_i32", r[2], size_s, 0),
+            S("s_mov_b32", r[3], RSRC3)]
 
 
 def rsrc_step(r):
@@ -903,7 +915,7 @@ class Item:
         Item._n += 1
         self.seq = Item._n
         self.at = None
-        self.size = sum(x.ws if x.kind == "nop" else 1 for x in self.ins)
+        self.size = sum(x.ws if x.kind == "nop" else LDS_SLOTS if x.kind == "lds" else 1 for x in self.ins)
 
 
 def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
@@ -1273,6 +1285,7 @@ class Gen:
         side = {}
         if not self.causal:
             side[-1] = [V("v_sub_u32", DREM, KVEND, INV["h8"])]   # keys >= S of tile 0
+        side.setdefault(-1, []).extend(x for b in self.q_loads() for x in b)
         return self.mfma_iteration("first_last", 0, False, None, sm, True, side_extra=side, budget=10 ** 6,
                                    end_ops=self.tail_first())
 
@@ -1383,7 +1396,7 @@ class Gen:
              V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]), V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
              LABEL(self.L(f"ret_s{u}"))], 0, len(mf) - 2, [(c0, VALU_SGPR_VMEM), (c1, VALU_SGPR_VMEM)])
         pre_log = [f for f in range(LOOK) for _ in range(2)]
-        return slot_schedule(mf, items, pre_log, cap=7)
+        return slot_schedule(mf, items, pre_log, cap=GAP_CAP)
 
     def it_last(self, u):
         """i = wt-1 >= 1 (u = i mod 4): PV(i-1), masked softmax(i) of SACC[u % 2]."""
@@ -1394,6 +1407,10 @@ class Gen:
         if not self.causal:
             side[-1] = [S("s_lshl_b32", T[4], ITER, 6), S("s_sub_i32", T[4], KVEND, T[4]),
                         V("v_sub_u32", DREM, T[4], INV["h8"])]
+        # the next tile's Q, into QA (the last QK was in the previous
+        # iteration): one load every other gap
+        for j, b in enumerate(self.q_loads()):
+            side.setdefault(2 * j, []).extend(b)
         return self.mfma_iteration(f"last{u}", u, True, None, sm, True, side_extra=side, budget=40,
                                    end_ops=self.tail_stale(self.L(f"redo_l{p}"), self.L(f"ret_l{u}")))
 
@@ -1418,9 +1435,15 @@ class Gen:
         return out
 
     # ------------------------------------------------------------ output
-    def output(self):
+    # the output registers of a finished tile: the next tile's setup reuses
+    # RO and QW0 while this tile's O is still being written out
+    INVL = [SCR[0], SCR[1]]
+
+    def output_lse(self):
+        """1 / l of the wave's rows into INVL, the LSE stores; then RO and QW0
+        copied to ORO, OQW for output_o."""
         out = []
-        INVL = [SCR[0], SCR[1]]
+        INVL = self.INVL
         LT = [SCR[2], SCR[3]]
         X = SCR[4]
         out += NOPS(MFMA_WS + 4)
@@ -1439,6 +1462,19 @@ class Gen:
                     V("v_add_u32", SCR[6], T[0], INV["lsel"]),
                     BSTORE("buffer_store_dword", lg, SCR[6], RL)]
             out += NOPS(STORE_DATA)
+        out += [S("s_mov_b32", OQW, QW0)] + [S("s_mov_b32", ORO[j], RO[j]) for j in range(4)]
+        return out
+
+    def output_o(self, bundles=()):
+        """O / l through the wave's LDS staging area to global memory
+        (16 buffer_store_dwordx4), from ORO, OQW and INVL; `bundles` (the next
+        tile's prologue loads) go one per 4-row block. Returns the program and
+        the number of vector-memory operations after the last of the first
+        N_EARLY bundles."""
+        out = []
+        bundles = list(bundles)
+        early_end = None
+        INVL = self.INVL
         # staging write addresses, chunk c: base + 128 l32 + 8 h + (16 c ^ 16 (l32 & 7))
         stg = T[1]
         out += [S("s_lshl_b32", stg, WAVE, 13), S("s_add_u32", stg, stg, LDSB), S("s_add_u32", stg, stg, LDS_STG)]
@@ -1448,7 +1484,7 @@ class Gen:
         RDA = SCR[7]
         out += [V("v_add_u32", RDA, stg, INV["rdl"])]
         # global row offsets: (qw0 + 8k) * 256 + lane part; pass p adds 128 bytes
-        out += [S("s_lshl_b32", T[2], QW0, 8)]
+        out += [S("s_lshl_b32", T[2], OQW, 8)]
         VO = [TMP[1][k] for k in range(8)]
         for k in range(8):
             out += [S("s_add_u32", T[3], T[2], 2048 * k) if k else S("s_mov_b32", T[3], T[2]),
@@ -1460,6 +1496,11 @@ class Gen:
                 ob = 2 * ps + j
                 for nb in range(2):
                     for aa in range(4):
+                        blk = 16 * ps + 8 * j + 4 * nb + aa
+                        if blk < len(bundles):
+                            out += bundles[blk]
+                            if blk == self.N_EARLY - 1:
+                                early_end = len(out)
                         t = [SCR[8 + e] for e in range(4)] if ps == 0 else [v(128 + e + 8 * (aa % 2)) for e in range(4)]
                         o = OACC[ob][nb]
                         out += [ACCR(t[e], o[4 * aa + e]) for e in range(4)]
@@ -1472,12 +1513,16 @@ class Gen:
                 out.append(DSR("ds_read_b128", dst[k], RDA, 1024 * k))
             out += [WAIT(lgkm=0)]
             for k in range(8):
-                out.append(BSTORE("buffer_store_dwordx4", dst[k], VO[k], RO, 128 * ps))
+                out.append(BSTORE("buffer_store_dwordx4", dst[k], VO[k], ORO, 128 * ps))
             out += NOPS(STORE_DATA)
-        return out
+        assert len(bundles) <= 32
+        n_after = None if early_end is None else sum(1 for x in out[early_end:] if x.kind == "vmem")
+        return out, n_after
 
     # ------------------------------------------------------------ query tile
-    def qtile(self):
+    def setup_loads(self):
+        """Registers of the query tile (BH, QT) and its prologue loads: K(0),
+        Q, K(1), K(2), V(0) (32 vector-memory operations)."""
         L = self.L
         out = []
         t = T
@@ -1516,23 +1561,68 @@ class Gen:
         # Q offsets of the lane's two rows
         out += [S("s_lshl_b32", t[0], QW0, 8), V("v_add_u32", QOFF[0], t[0], INV["qlane"]),
                 V("v_add_u32", QOFF[1], 0x2000, QOFF[0])]
-        # prologue loads: K(0), Q, K(1), K(2), V(0); then the resources of the
-        # first iteration's loads (K tile 3, V tile 1)
-        def load(r, dst):
-            o = [S("s_add_u32", M0, WOFF, dst), NOP(0)]
-            return o + [BLOAD_LDS(INV[f"loff{j}"], r, 1024 * j) for j in range(4)]
-        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RK, KH, t[3], KVB) + load(RK, 0)
-        out += NOPS(2)
-        for nb in range(2):
-            for ks in range(8):
-                out.append(BLOAD("buffer_load_dwordx4", QA[nb][ks], QOFF[nb], RQ, 32 * ks))
-        for tile in (1, 2):
-            out += [x for b in rsrc_step(RK) for x in b] + load(RK, tile * SLOT)
-        out += [x for b in rsrc_step(RK) for x in b]
-        out += [S("s_mov_b32", t[3], 0)] + rsrc_at(RV, VH, t[3], KVB) + load(RV, LDS_V)
-        out += [x for b in rsrc_step(RV) for x in b]
-        # ---- the walk
-        out += [S("s_mov_b32", ITER, -1)] + self.barrier(12)
+        return out
+
+    # the prologue loads of K(0) and Q are the first N_EARLY bundles
+    N_EARLY = 20
+
+    def prologue_loads(self, with_q=True):
+        """The query tile's prologue loads as bundles, each ending in one
+        load: K(0), Q (unless the previous walk loaded it), K(1), K(2), V(0);
+        the last leaves RK, RV at the first iteration's tiles (K 3, V 1)."""
+        def flat(bl):
+            return [x for b in bl for x in b]
+
+        def tile(r, dst, pre):
+            return [(pre + [S("s_add_u32", M0, WOFF, dst), NOP(0)] if j == 0 else []) +
+                    [BLOAD_LDS(INV[f"loff{j}"], r, 1024 * j)] for j in range(4)]
+        b = tile(RK, 0, rsrc_base(RK, KH, KVB))
+        if with_q:
+            b += self.q_loads()
+            assert len(b) == self.N_EARLY
+        for tl in (1, 2):
+            b += tile(RK, tl * SLOT, flat(rsrc_step(RK)))
+        b += tile(RV, LDS_V, flat(rsrc_step(RK)) + rsrc_base(RV, VH, KVB))
+        b[-1] += flat(rsrc_step(RV))
+        return b
+
+    def q_loads(self):
+        """The 16 loads of this wave's 64 Q rows into QA (from RQ, QOFF)."""
+        return [[BLOAD("buffer_load_dwordx4", QA[nb][ks], QOFF[nb], RQ, 32 * ks)] for nb in range(2) for ks in range(8)]
+
+    def q_address(self):
+        """RQ and QOFF of query tile (BH, QT) for this wave's rows."""
+        t = T
+        return [S("s_lshl_b32", t[3], SEQ, 8), S("s_mul_i32", t[4], BH, t[3]), S("s_mul_hi_u32", t[5], BH, t[3]),
+                S("s_add_u32", RQ[0], QP[0], t[4]), S("s_addc_u32", RQ[1], QP[1], t[5]),
+                S("s_and_b32", RQ[1], RQ[1], 0xFFFF), S("s_mov_b32", RQ[2], t[3]), S("s_mov_b32", RQ[3], RSRC3),
+                S("s_lshl_b32", t[0], QT, 8), S("s_sub_i32", t[0], t[0], QSHIFT), S("s_lshl_b32", t[1], WAVE, 6),
+                S("s_add_i32", t[0], t[0], t[1]), S("s_lshl_b32", t[0], t[0], 8),
+                V("v_add_u32", QOFF[0], t[0], INV["qlane"]), V("v_add_u32", QOFF[1], 0x2000, QOFF[0])]
+
+    def next_tile(self):
+        """At the start of a walk (its prologue loads issued): the next query
+        tile into (BH, QT) -- pass 1 of this work item, or pass 0 of the next
+        one, decoded here -- and its Q address into RQ, QOFF, so the walk's
+        last iteration can load its Q. NXT: bit 0 a next tile exists, bit 1
+        it is pass 1. Without one, RQ is empty."""
+        L = lambda n: self.L(f"nt_{n}")
+        out = [S("s_cmp_eq_u32", PASS, 0), CBR("s_cbranch_scc0", L("item")), S("s_cmp_lt_i32", QT1, 0),
+               CBR("s_cbranch_scc1", L("item")), S("s_mov_b32", BH, BH1), S("s_mov_b32", QT, QT1),
+               S("s_mov_b32", NXT, 3), BR(L("q"))]
+        out += [LABEL(L("item")), S("s_add_u32", ITEMV, ITEMV, GRID), S("s_cmp_ge_u32", ITEMV, NWORK),
+                CBR("s_cbranch_scc1", L("none"))]
+        out += self.decode("d1") + [S("s_mov_b32", BH, BH0), S("s_mov_b32", QT, QT0), S("s_mov_b32", NXT, 1),
+                                    BR(L("q"))]
+        out += [LABEL(L("none")), S("s_mov_b32", NXT, 0), S("s_mov_b32", RQ[2], 0), BR(L("done"))]
+        out += [LABEL(L("q"))] + self.q_address() + [LABEL(L("done"))]
+        return out
+
+    def walk(self):
+        """The key walk of the query tile, from iteration -1 (the prologue's
+        K(0) and Q have landed, and the barrier after them has passed)."""
+        L = self.L
+        out = [S("s_mov_b32", ITER, -1)]
         out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("idle_m1"))]
         out += self.it_fill()
         out += [BR(L("it0")), LABEL(L("idle_m1"))] + self.it_idle()
@@ -1541,7 +1631,8 @@ class Gen:
                 S("s_cmp_eq_u32", WT, 1), CBR("s_cbranch_scc1", L("first_last"))]
         out += self.it_idle() + [BR(L("it1"))]
         out += [LABEL(L("first"))] + self.it_first() + [BR(L("it1"))]
-        out += [LABEL(L("first_last"))] + self.it_first_last() + [BR(L("it1"))]
+        # a one-tile walk (wt = 1) goes on to its drain at i = 1
+        out += [LABEL(L("first_last"))] + self.it_first_last() + [S("s_mov_b32", ITER, 1), BR(L("drain1"))]
         # i = 1: steady while i < wt - 1, then last (i = wt - 1), drain (i = wt);
         # a copy per i mod 4 of each, chained in walk order
         out += [LABEL(L("it1")), S("s_mov_b32", ITER, 1), S("s_sub_i32", LIM, WT, 1),
@@ -1560,46 +1651,23 @@ class Gen:
             out += [LABEL(L(f"last{u}"))] + self.barrier(8) + self.it_last(u)
             out += [S("s_add_i32", ITER, ITER, 1), BR(L(f"drain{(u + 1) % 4}"))]
         for u in range(4):
-            out += [LABEL(L(f"drain{u}"))] + self.barrier(8) + self.it_drain(u)
+            # the last iteration's 8 ring loads and 16 Q loads may be in flight
+            out += [LABEL(L(f"drain{u}"))] + self.barrier(8 + 16) + self.it_drain(u)
             out += [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("idle_chk")), S("s_cmp_le_i32", ITER, NT), CBR("s_cbranch_scc0", L("walk_end"))]
         out += self.barrier(8) + self.it_idle() + [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("walk_end"))] + [WAIT(vm=0, lgkm=0), BAR()]
-        out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("out_done"))]
-        out += self.output()
-        out += [LABEL(L("out_done"))]
         return out
 
-    def redo_blocks(self):
-        out = []
-        for p in (0, 1):
-            out += self.redo_block(self.L(f"redo_s{p}"), "ret_s", p, False)
-            out += self.redo_block(self.L(f"redo_l{p}"), "ret_l", p, True)
-        return out
-
-    def kernel(self):
-        L = self.L
-        out = [SLOAD("s_load_dwordx16", s(0, 16), INS_["ka"], 0), SLOAD("s_load_dwordx16", s(16, 16), INS_["ka"], 64),
-               S("s_mov_b32", ITEMV, INS_["wg"]), S("s_mov_b32", GRID, INS_["ng"]), S("s_mov_b32", WAVE, INS_["wv"]),
-               S("s_mov_b32", LDSB, INS_["lb"]), S("s_mov_b32", ONES, 0x3F803F80), S("s_mov_b32", BOUND, BOUND_F),
-               S("s_lshl_b32", WOFF, INS_["wv"], 12), S("s_add_u32", WOFF, WOFF, INS_["lb"]),
-               V("v_mov_b32", NINF, 0xFF800000),
-               # LDS read bases, fixed for the kernel (the ring slot is the
-               # instruction offset; the base is 1 KB aligned, so the XORs on
-               # bits 5-7 commute with it)
-               V("v_add_u32", KA, INS_["lb"], INV["kofs"]),
-               V("v_add_u32", VA[0][0], INS_["lb"], INV["vofs1"]), V("v_add_u32", VA[0][1], INS_["lb"], INV["vofs2"]),
-               V("v_add_u32", VA[0][0], LDS_V, VA[0][0]), V("v_add_u32", VA[0][1], LDS_V, VA[0][1])] + [
-               V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]) for ob in range(1, 4) for j in range(2)] + [
-               WAIT(lgkm=0)]
+    def decode(self, tag):
+        """Work item ITEMV -> (BH0, QT0) and (BH1, QT1) (QT1 = -1: no second
+        tile): work = xcd_remap(ITEMV), then prefill_work's pairing."""
+        L = lambda n: self.L(f"{n}_{tag}")
         t = T
-        out += [LABEL(L("item")), S("s_cmp_ge_u32", ITEMV, NWORK), CBR("s_cbranch_scc1", L("end"))]
-        # work = xcd_remap(v)
-        out += [S("s_and_b32", t[0], ITEMV, 7), S("s_lshr_b32", t[1], ITEMV, 3), S("s_add_u32", t[2], XQ, 1),
-                S("s_mul_i32", t[3], t[0], t[2]), S("s_sub_u32", t[4], t[0], XR), S("s_mul_i32", t[4], t[4], XQ),
-                S("s_mul_i32", t[5], XR, t[2]), S("s_add_u32", t[4], t[4], t[5]), S("s_cmp_lt_u32", t[0], XR),
-                S("s_cselect_b32", t[3], t[3], t[4]), S("s_add_u32", WORK, t[3], t[1])]
-        # decode the work item (prefill_work)
+        out = [S("s_and_b32", t[0], ITEMV, 7), S("s_lshr_b32", t[1], ITEMV, 3), S("s_add_u32", t[2], XQ, 1),
+               S("s_mul_i32", t[3], t[0], t[2]), S("s_sub_u32", t[4], t[0], XR), S("s_mul_i32", t[4], t[4], XQ),
+               S("s_mul_i32", t[5], XR, t[2]), S("s_add_u32", t[4], t[4], t[5]), S("s_cmp_lt_u32", t[0], XR),
+               S("s_cselect_b32", t[3], t[3], t[4]), S("s_add_u32", WORK, t[3], t[1])]
         out += [S("s_cmp_eq_u32", PAIRED, 0), CBR("s_cbranch_scc1", L("unpaired")),
                 S("s_cmp_lt_u32", WORK, NFULL), CBR("s_cbranch_scc0", L("pair_tail"))]
         out += div_magic(t[0], WORK, MHALF, SHHALF)
@@ -1613,13 +1681,58 @@ class Gen:
         out += [LABEL(L("unpaired"))] + div_magic(t[0], WORK, MNQT, SHNQT)
         out += [S("s_mul_i32", t[1], t[0], NQT), S("s_sub_u32", t[1], WORK, t[1]), S("s_mov_b32", BH0, t[0]),
                 S("s_sub_u32", QT0, NQT, 1), S("s_sub_u32", QT0, QT0, t[1]), S("s_mov_b32", QT1, -1)]
-        out += [LABEL(L("decoded")), S("s_mov_b32", PASS, 0)]
-        out += [LABEL(L("qtile")), S("s_cmp_eq_u32", PASS, 0), S("s_cselect_b32", BH, BH0, BH1),
-                S("s_cselect_b32", QT, QT0, QT1)]
-        out += self.qtile()
-        out += [S("s_cmp_eq_u32", PASS, 0), CBR("s_cbranch_scc0", L("next")), S("s_cmp_lt_i32", QT1, 0),
-                CBR("s_cbranch_scc1", L("next")), S("s_mov_b32", PASS, 1), BR(L("qtile"))]
-        out += [LABEL(L("next")), S("s_add_u32", ITEMV, ITEMV, GRID), BR(L("item"))]
+        out += [LABEL(L("decoded"))]
+        return out
+
+    def select(self):
+        """(BH, QT) of pass PASS of the work item."""
+        return [S("s_cmp_eq_u32", PASS, 0), S("s_cselect_b32", BH, BH0, BH1), S("s_cselect_b32", QT, QT0, QT1)]
+
+    def redo_blocks(self):
+        out = []
+        for p in (0, 1):
+            out += self.redo_block(self.L(f"redo_s{p}"), "ret_s", p, False)
+            out += self.redo_block(self.L(f"redo_l{p}"), "ret_l", p, True)
+        return out
+
+    def kernel(self):
+        L = self.L
+        out = [SLOAD("s_load_dwordx16", s(0, 16), INS_["ka"], 0), SLOAD("s_load_dwordx16", s(16, 16), INS_["ka"], 64),
+               S("s_mov_b32", ITEMV, INS_["wg"]), S("s_mov_b32", GRID, INS_["ng"]), S("s_mov_b32", WAVE, INS_["wv"]),
+               S("s_mov_b32", LDSB, INS_["lb"]), S("s_mov_b32", BOUND, BOUND_F),
+               S("s_lshl_b32", WOFF, INS_["wv"], 12), S("s_add_u32", WOFF, WOFF, INS_["lb"]),
+               V("v_mov_b32", NINF, 0xFF800000),
+               # LDS read bases, fixed for the kernel (the ring slot is the
+               # instruction offset; the base is 1 KB aligned, so the XORs on
+               # bits 5-7 commute with it)
+               V("v_add_u32", KA, INS_["lb"], INV["kofs"]),
+               V("v_add_u32", VA[0][0], INS_["lb"], INV["vofs1"]), V("v_add_u32", VA[0][1], INS_["lb"], INV["vofs2"]),
+               V("v_add_u32", VA[0][0], LDS_V, VA[0][0]), V("v_add_u32", VA[0][1], LDS_V, VA[0][1])] + [
+               V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]) for ob in range(1, 4) for j in range(2)] + [
+               WAIT(lgkm=0)]
+        t = T
+        # A tile's walk, then its LSE; the next tile's setup and prologue
+        # loads go out before this tile's O is written, so the loads land
+        # while the output runs.
+        out += [S("s_cmp_ge_u32", ITEMV, NWORK), CBR("s_cbranch_scc1", L("end"))]
+        loads = [x for b in self.prologue_loads() for x in b]
+        out += self.decode("d0") + [S("s_mov_b32", PASS, 0)] + self.select() + self.setup_loads() + loads
+        out += self.barrier(12) + [BR(L("walk"))]
+        out += [LABEL(L("walk"))] + self.next_tile() + self.walk()
+        out += [S("s_mov_b32", OQW, -1), S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("lse_done"))]
+        out += self.output_lse() + [LABEL(L("lse_done"))]
+        # the next tile (BH, QT) was chosen at the walk's start
+        out += [S("s_bitcmp1_b32", NXT, 0), CBR("s_cbranch_scc0", L("final")), S("s_lshr_b32", PASS, NXT, 1)]
+        out += self.setup_loads()
+        out += [S("s_cmp_lt_i32", OQW, 0), CBR("s_cbranch_scc1", L("no_out"))]
+        # this wave had rows, so its last iteration loaded the next Q: K(0),
+        # K(1), K(2), V(0), then the output's 16 stores; the barrier waits for
+        # K(0) (the 12 loads and 16 stores after it may be in flight)
+        out += [x for b in self.prologue_loads(False) for x in b] + self.output_o()[0]
+        out += self.barrier(12 + 16) + [BR(L("walk"))]
+        out += [LABEL(L("no_out"))] + loads + self.barrier(12) + [BR(L("walk"))]
+        out += [LABEL(L("final")), S("s_cmp_lt_i32", OQW, 0), CBR("s_cbranch_scc1", L("end"))]
+        out += self.output_o()[0] + [BR(L("end"))]
         out += self.redo_blocks()
         out += [LABEL(L("end")), WAIT(vm=0, lgkm=0)]
         self.prog = out
