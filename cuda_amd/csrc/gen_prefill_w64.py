@@ -495,6 +495,10 @@ TMP = [v(160 + 8 * t, 8) for t in range(3)]
 NSLOT, LOOK = 8, 6
 STEADY_SPAN = 55   # the steady softmax spreads its 64 elements over gaps 0..STEADY_SPAN
 LDS_SLOTS = 1      # issue slots the slot scheduler charges for an LDS read
+# slot caps of the other iterations slot_schedule places (measured per tile
+# of C2: fill 1500 cycles at 5, last 2611 and drain at 10; the first tile's
+# iteration is faster under the greedy schedule, 2315 against 2386)
+OTHER_CAP = {"fill": 5, "last": 10, "drain": 10}
 GAP_CAP = 5        # issue slots per MFMA gap (5 measured best: 2220 cycles per steady iteration, 7 gave 2307)
 FRAG = [v(184 + 4 * t, 4) for t in range(4)] + [v(224 + 4 * t, 4) for t in range(4)]
 MRUN = [v(200), v(201)]
@@ -711,75 +715,6 @@ def softmax_exp_program(sm, p, masked, causal, kk_release, first_sum_init=True, 
     return sm
 
 
-STREAM = dict(per_gap=2, exp_last=False, pair_exps=False, fma_lead=1)
-
-
-def stream_softmax(p, kk_release, n_gaps=64, per_gap=None):
-    """The steady softmax of S^T[p] as a regular stream over the MFMA gaps:
-    element e (group g = e / 8: P^T k-step kk = g / 2, query block nb = g % 2;
-    register 8 (kk % 2) + e % 8 of S^T block (kk / 2, nb)) takes its FMA in
-    gap e - 1 and its exponential in gap e; the packs and row sums of element
-    pairs follow as soon as both exponentials are a gap old and the pair's
-    P^T registers are released by PV (kk_release), at most `per_gap` per gap,
-    and each element's fp32 row-sum add one gap after its exponential.
-    Returns {gap: [Ins]} with key "tail" for what follows the last MFMA."""
-    per_gap = STREAM["per_gap"] if per_gap is None else per_gap
-    out = {}
-    late = {}
-    put = lambda g, x: out.setdefault(g, []).append(x)
-    tmp = [v(160 + j) for j in range(24)]
-    for e in range(64):
-        g, j = e // 8, e % 8
-        kk, nb = g // 2, g % 2
-        src = SACC[p][kk // 2][nb][8 * (kk % 2) + j]
-        t = tmp[e % 24]
-        fma = V("v_fma_f32", t, src, SCALE, "-" + str(MSUB[nb]))
-        fma.uses.append(("v", MSUB[nb].i))
-        eg = e if not STREAM["pair_exps"] else (e // 2) * 2 + 1
-        put(eg - STREAM["fma_lead"], fma)
-        ex = V("v_exp_f32", t, t, trans=True)
-        if STREAM["exp_last"]:
-            late.setdefault(eg, []).append(ex)
-        else:
-            put(eg if eg < n_gaps else "tail", ex)
-    # packs in pair order, each as early as allowed; the fp32 row sums one
-    # gap after each exponential (chains (nb, e % 2))
-    load = {}
-    for i in range(32):
-        e0 = 2 * i
-        g = e0 // 8
-        kk, nb = g // 2, g % 2
-        q = (e0 % 8) // 2
-        gap = max(e0 + 2, kk_release[kk])
-        while gap < n_gaps and load.get(gap, 0) >= per_gap:
-            gap += 1
-        load[gap] = load.get(gap, 0) + 1
-        put(gap if gap < n_gaps else "tail",
-            V("v_cvt_pk_bf16_f32", PB[kk][nb][q], tmp[e0 % 24], tmp[(e0 + 1) % 24]))
-    for e in range(64):
-        g = e // 8
-        kk, nb = g // 2, g % 2
-        acc = PSUM[nb][e % 2]
-        init = kk == 0 and e % 8 < 2
-        put(e + 1 if e + 1 < n_gaps else "tail", V("v_add_f32", acc, 0 if init else acc, tmp[e % 24]))
-    for g_, lst in late.items():
-        for x in lst:
-            put(g_ if g_ < n_gaps else "tail", x)
-    # the last exponential is the tail's first op; its pack reads it a wait
-    # state later at the earliest
-    if "tail" in out:
-        tl = out["tail"]
-        k = next((j for j, x in enumerate(tl) if not x.text.startswith("v_exp")), None)
-        if k is not None:
-            tl.insert(k, NOP(TRANS_FWD - 1))
-    return out
-
-
-# ---------------------------------------------------------------------------
-# the MFMA-stream iteration scheduler
-# ---------------------------------------------------------------------------
-
-
 class Block:
     def __init__(self):
         self.out = []
@@ -889,6 +824,7 @@ def schedule_iteration(blk, mfmas, reads, pre_reads, side, sm_ops, budget=30, en
             blk.out.append(x)
     for x in end_ops:
         blk.out.append(x)
+    check_item_order(None, blk.out, ref=[x for op in sm_ops for x in op.ins])
 
 
 # ---------------------------------------------------------------------------
@@ -1002,7 +938,39 @@ def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
         else:
             out.append(NOP(0))
     out.extend(tail)
+    check_item_order(items, out)
     return out
+
+
+def check_item_order(items, out, ref=None):
+    """The scheduled order keeps the items' dataflow: every register a
+    placed instruction reads comes from the same writer as in the items'
+    creation order (or the reference order `ref`), and each register's last
+    writer is the same. (Items that touch a register without a dependency
+    between them would race.)"""
+    if ref is None:
+        ref = [x for it in sorted(items, key=lambda it: it.seq) for x in it.ins]
+    ids = {id(x) for x in ref}
+    assert len(ids) == len(ref), "an instruction placed twice"
+
+    def flow(seq):
+        last, reads = {}, {}
+        for x in seq:
+            if id(x) not in ids:
+                continue
+            for k in x.uses:
+                reads[(id(x), k)] = last.get(k)
+            for k in x.defs:
+                last[k] = id(x)
+        return reads, last
+    r0, l0 = flow(ref)
+    r1, l1 = flow(out)
+    bad = [k for k in r0 if r0[k] != r1.get(k)] + [k for k in l0 if l0[k] != l1.get(k)]
+    if bad:
+        txt = {id(x): x.text for x in ref}
+        k = bad[0]
+        where = txt.get(k[0], k) if isinstance(k, tuple) else k
+        raise CheckError(f"schedule changes the dataflow of {len(bad)} reads, first: {where} {k}")
 
 
 def _conflict(a, b):
@@ -1156,7 +1124,10 @@ class Gen:
                         if kind == "none":
                             prev = sm.add(V("v_max_f32", acc[mb], acc[mb], src[r]), [(prev, 1)])
                             continue
-                        tmpr = TMP[0][(mb * 16 + r) % 8 + 0]
+                        # one temporary per (nb, mb) chain: the chains are
+                        # independent and may interleave; within a chain the
+                        # select waits for the previous max
+                        tmpr = TMP[0][2 * nb + mb]
                         op = sm.add(masked_select(self.causal, mb, nb, r, tmpr, src[r]), [(prev, 1)])
                         prev = sm.add(V("v_max_f32", acc[mb], acc[mb], tmpr), [(op, 1)])
                     ops.append(prev)
@@ -1264,6 +1235,71 @@ class Gen:
         softmax_exp_program(sm, p, masked, self.causal, kk_release)
         return sm
 
+    def slot_iter(self, kind, u, pv, qk_par, sm, prefetch, side=None, end_ops=()):
+        """An iteration i = u (mod 4) other than the steady one, placed by
+        slot_schedule: PV(i-1) if pv, QK(i+1) into SACC[qk_par] if qk_par is
+        not None, the VALU program sm (its ops in program order, a VOp
+        distance d kept as d instructions between), the V(i) prefetch, the 8
+        loads and the resource steps; side: {gap: [Ins]} placed in order from
+        that gap on; end_ops after the stream."""
+        mf, reads, nf = self.mfma_lists(pv, qk_par, u)
+        nm = len(mf)
+        items = []
+
+        def add(ins, lo=-1, hi=None, deps=()):
+            it = Item(ins, lo, hi, deps)
+            items.append(it)
+            return it
+        sl = self.slots(u)
+        prev, last = None, {}
+        for j in range(8):
+            r = RK if j < 4 else RV
+            at = (j * nm) // 8
+            deps = [(prev, 0)] if prev else []
+            if j % 4 == 0:
+                base = SLOT * sl["kld"] if j < 4 else LDS_V + SLOT * sl["vld"]
+                m = add(S("s_add_u32", M0, WOFF, base), at - 1 if nm else -1, at if nm else None, deps)
+                deps = deps + [(m, M0_WS)]
+            prev = add(BLOAD_LDS(INV[f"loff{j % 4}"], r, 1024 * (j % 4)), at + 1 if nm else -1, None, deps)
+            last[r.i] = prev
+        for r in (RK, RV):
+            dep = last[r.i]
+            for b in rsrc_step(r):
+                dep = add(b, -1, None, [(dep, 0)])
+        fitem, xitem = {}, None
+        for f in range(nf):
+            if pv and f < LOOK:
+                continue                       # read by the iteration before
+            lo = max(2 * (f - NSLOT) + 1, 2 * (f - LOOK), -1)
+            hi = max(2 * f - 5, -1) if nm else None
+            deps = []
+            lds = [x for x in reads[f] if x.kind == "lds"]
+            xor = [x for x in reads[f] if x.kind != "lds"]
+            if xor:                            # KX for this ks, after the last read of the old one
+                xitem = add(xor, max(lo - 2, -1), max(2 * f - 6, -1) if nm else None,
+                            [(fitem[f - 1], 0)] if f - 1 in fitem else [])
+            if ("v", KX.i) in lds[0].uses:
+                deps.append((xitem, 0))
+            fitem[f] = add(lds, lo, hi, deps)
+        if prefetch:
+            for f, lst in sorted(self.v_prefetch(nf, u).items()):
+                add(lst, max(2 * (f - NSLOT) + 1, 2 * (f - LOOK), -1) if nm else -1, None)
+        # side ops (gap -1's before the VALU program, which may read them)
+        first_side = None
+        for g, lst in sorted((side or {}).items()):
+            dep = None
+            for x in lst:
+                dep = add(x, g if nm else -1, None, [(dep, 0)] if dep else [])
+            if g == -1:
+                first_side = dep
+        if sm is not None:
+            conv = {}
+            for op in sm.ops:
+                deps = [(conv[id(d)], dist) for d, dist in op.deps] + ([(first_side, 0)] if first_side else [])
+                conv[id(op)] = add(op.ins, op.nb_gap if nm else -1, None, deps)
+        pre_log = [f for f in range(LOOK) for _ in range(2)] if pv else []
+        return slot_schedule(mf, items, pre_log, cap=OTHER_CAP[kind], tail=list(end_ops))
+
     # ------------------------------------------------------------ iteration variants
     def it_fill(self):
         """i = -1: QK(0) into SACC[0]; O zeroed under it."""
@@ -1272,7 +1308,7 @@ class Gen:
             for nb in range(2):
                 for r in range(16):
                     sm.add(ACCW(OACC[ob][nb][r], 0))
-        return self.mfma_iteration("fill", 3, False, 0, sm, False, budget=40)
+        return self.slot_iter("fill", 3, False, 0, sm, False)
 
     def it_first(self):
         """i = 0 (walk of >= 2 tiles): softmax(0) with the row max, QK(1)."""
@@ -1411,12 +1447,12 @@ class Gen:
         # iteration): one load every other gap
         for j, b in enumerate(self.q_loads()):
             side.setdefault(2 * j, []).extend(b)
-        return self.mfma_iteration(f"last{u}", u, True, None, sm, True, side_extra=side, budget=40,
+        return self.slot_iter("last", u, True, None, sm, True, side=side,
                                    end_ops=self.tail_stale(self.L(f"redo_l{p}"), self.L(f"ret_l{u}")))
 
     def it_drain(self, u):
         """i = wt (u = i mod 4): PV(wt-1)."""
-        return self.mfma_iteration(f"drain{u}", u, True, None, None, False, end_ops=[WAIT(lgkm=0)])
+        return self.slot_iter("drain", u, True, None, None, False, end_ops=[WAIT(lgkm=0)])
 
     def it_idle(self):
         """An iteration with no tile of this wave's walk: its share of the loads
