@@ -81,9 +81,11 @@ def test_backward_custom_scale(dev):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize("hq,hkv,s", [(4, 4, 100), (8, 2, 777), (4, 4, 4096)])
+@pytest.mark.parametrize("hq,hkv,s", [(4, 4, 1), (4, 4, 50), (4, 4, 100), (8, 2, 777), (4, 4, 4096)])
 @pytest.mark.parametrize("is_causal", [False, True])
 def test_forward_lse(dev, dtype, head_dim, hq, hkv, s, is_causal):
+    """Also one-tile walks (s <= 64), whose row max is taken in the same
+    iteration as the exponentials."""
     q, k, v = qkv(1, hq, s, head_dim, dtype, dev, hkv=hkv)
     out, lse = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=is_causal)
     torch.cuda.synchronize()
