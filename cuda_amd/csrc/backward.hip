@@ -37,10 +37,6 @@
 namespace ca {
 namespace {
 
-#ifndef CA_BWD_PRIO
-#define CA_BWD_PRIO 0
-#endif
-
 __device__ __forceinline__ int rho32(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
 // Per query row of B * Hq * S: the pair (LSE * log2(e), D) with D = sum_d
@@ -295,7 +291,6 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
     const uint32_t ka = hb + rofs, va = ka + kTileB;
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
     u32x4 kr[2], vr[2];
     kr[0] = lds_read_b128<0>(ka);
     vr[0] = lds_read_b128<0>(va);
@@ -314,7 +309,6 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
       s = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb]), qv[ks], s);
       dp = Tr::mfma32(__builtin_bit_cast(vec8, vr[cb]), gv[ks], dp);
     }
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
     // dS^T / scale = P (dP - D) as the B operand of dQ^T += K^T dS^T
     vec8 pb[2];
     auto softmax = [&](auto mask_tag) CA_INLINE {
@@ -343,7 +337,6 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
     if (mask) softmax(std::true_type{});
     else softmax(std::false_type{});
     // dQ^T[d x q] += K^T[d x keys] dS^T[keys x q]
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ob = 0; ob < kNOB; ++ob) {
       const vec8 a0 = Gm::template tr_operand<Tr, 0>(hb, tofs, ob);
@@ -355,7 +348,6 @@ __device__ CA_INLINE void bwd_dq_dma_tile(const uint16_t* __restrict__ Q,
       acc[ob] = Tr::mfma32(x0, pb[0], acc[ob]);
       acc[ob] = Tr::mfma32(x1, pb[1], acc[ob]);
     }
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
 #pragma unroll
@@ -502,7 +494,6 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
 #pragma unroll
     for (int r = 0; r < 16; ++r) { s[r] = 0.f; dp[r] = 0.f; }
     const uint32_t qa = sb + rofs, ga = qa + kTileB;
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
     u32x4 qr[2], gr[2], vr[2];
     qr[0] = lds_read_b128<0>(qa);
     gr[0] = lds_read_b128<0>(ga);
@@ -524,7 +515,6 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
       s = Tr::mfma32(__builtin_bit_cast(vec8, qr[cb]), kv[ks], s);
       dp = Tr::mfma32(__builtin_bit_cast(vec8, gr[cb]), __builtin_bit_cast(vec8, vr[cb]), dp);
     }
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
     // P and dS / scale = P (dP - D) as B operands, k-step kk = 16 queries
     vec8 pp[2], pd[2];
     auto softmax = [&](auto mask_tag) CA_INLINE {
@@ -568,7 +558,6 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
     if (mask) softmax(std::true_type{});
     else softmax(std::false_type{});
     // dV^T[d x keys] += dO^T P and dK^T[d x keys] += Q^T dS
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ob = 0; ob < kNOB; ++ob) {
       const vec8 g0 = Gm::template tr_operand<Tr, 0>(sb + kTileB, tofs, ob);
@@ -586,7 +575,6 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
       dv[ob] = Tr::mfma32(a1, pp[1], dv[ob]);
       dk[ob] = Tr::mfma32(b1, pd[1], dk[ob]);
     }
-    if (CA_BWD_PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
 #pragma unroll

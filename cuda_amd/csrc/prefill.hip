@@ -127,9 +127,6 @@ constexpr int pf_group(int d) { return d == 64 ? 4 : kPfGroup; }
 // Ping-pong walk: tile t + kPpAhead is loaded with tile t (its slot held
 // tile t - 2, released by the barrier of tile t).
 constexpr int kPpAhead = 2;
-#ifndef CA_PF_DOT2
-#define CA_PF_DOT2 0
-#endif
 // 24 wait states: longer than any MFMA-result -> VALU and VALU -> MFMA-operand
 // hazard of gfx950, so MFMAs issued before it have written their results.
 __device__ __forceinline__ void acc_gap() { CA_DEVICE_ASM("s_nop 7\n\ts_nop 7\n\ts_nop 7"); }
@@ -389,7 +386,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
     // pairs 0 and 1 start the two chains (an add of 0.f is not folded away)
-    if constexpr (MX || CA_PF_DOT2)
+    if constexpr (MX)
       psum[j & 1] = Tr::sum2(pk, p < 2 ? 0.f : psum[j & 1]);
     else
       psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
