@@ -42,6 +42,7 @@ SIGNATURES = {
     "ca_mx_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "ca_decode_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "ca_check_block_tables": (_I, [_P, _P, _I, _I, _I, _I, _P]),
+    "ca_check_mx_scales": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "ca_last_error": (ctypes.c_char_p, []),
     "ca_version": (ctypes.c_char_p, []),
 }

@@ -452,8 +452,10 @@ def fused_microscaled_attention(q_fp8, q_scale, k_fp8, k_scale, v_fp8, v_scale,
     q/k/v: e4m3 codes (uint8 / int8 / float8_e4m3fn) [B, H, S, 128];
     scales: one per 32 elements along D, [B, H, S, 4]: e8m0 bytes (uint8 /
     float8_e8m0fnu) or floating tensors holding powers of two (the
-    reference's float form; passed to the C ABI as float32, which rejects
-    anything else). Mixed forms are brought to e8m0 bytes here. Output
+    reference's float form; passed to the C ABI as float32, which takes
+    anything else as NaN; with CUDA_LLM_CHECK_MX_SCALES=1 in the environment
+    they are checked first, synchronously, and RuntimeError is raised).
+    Mixed forms are brought to e8m0 bytes here, which checks them. Output
     [B, H, S, 128] bf16/fp16.
     """
     for t in (q_fp8, k_fp8, v_fp8, q_scale, k_scale, v_scale):
@@ -471,6 +473,10 @@ def fused_microscaled_attention(q_fp8, q_scale, k_fp8, k_scale, v_fp8, v_scale,
     if all(t.is_floating_point() and t.dtype != torch.float8_e8m0fnu for t in scales):
         kind = _lib.CA_SCALE_F32
         qs, ks, vs = (_aligned(t.to(torch.float32).contiguous()) for t in scales)
+        if os.environ.get("CUDA_LLM_CHECK_MX_SCALES", "0") not in ("", "0"):
+            # ca_check_mx_scales (synchronous): by default a scale that is not
+            # a power of two is taken as NaN and the call stays asynchronous
+            _lib.call("ca_check_mx_scales", _ptr(qs), _ptr(ks), _ptr(vs), b, h, s, d, _stream())
     else:
         kind = _lib.CA_SCALE_E8M0
         qs, ks, vs = (mx_scales_to_e8m0(t).contiguous() for t in scales)

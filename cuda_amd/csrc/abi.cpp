@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <climits>
 #include <initializer_list>
+#include <new>
 #include <vector>
 
 #include "../../include/cuda_llm_abi.h"
@@ -312,19 +313,16 @@ ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
                 "%s: these sizes need %zu bytes of split partials, more than the %zu bytes of "
                 "the library's scratch (use ca_fp8_paged_attention with a workspace)",
                 what, need, ca::kNoAllocScratchBytes);
-  void* scratch = nullptr;
-  if (need > 0) {
-    const hipError_t e = ca::noalloc_scratch(&scratch);
-    if (e != hipSuccess)
-      return fail(CA_LAUNCH_FAILED, "%s: scratch lookup failed: %s", what, hipGetErrorString(e));
-  }
-  return from_hip(ca::launch_paged_decode((int)dtype, 1, query, key_cache, value_cache, k_scale,
-                                          v_scale, per_block_scales != 0, block_tables,
-                                          context_lens, out, num_seqs, num_q_heads,
-                                          num_kv_heads, head_dim, max_blocks_per_seq,
-                                          num_blocks > 0 ? num_blocks : 1, softmax_scale,
-                                          scratch, need, (hipStream_t)stream),
-                  what);
+  auto launch = [&](void* scratch) {
+    return ca::launch_paged_decode((int)dtype, 1, query, key_cache, value_cache, k_scale, v_scale,
+                                   per_block_scales != 0, block_tables, context_lens, out, num_seqs,
+                                   num_q_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                   num_blocks > 0 ? num_blocks : 1, softmax_scale, scratch, need,
+                                   (hipStream_t)stream);
+  };
+  // one split needs no partials; otherwise the scratch, serialised per device
+  if (need == 0) return from_hip(launch(nullptr), what);
+  return from_hip(ca::with_noalloc_scratch((hipStream_t)stream, launch), what);
 }
 
 size_t ca_mx_workspace_bytes(ca_scale_kind scale_kind, int batch, int num_heads, int seq_len,
@@ -367,14 +365,28 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, c
   if (workspace_bytes < need || !workspace)
     return fail(CA_INVALID_ARGUMENT, "%s: workspace of %zu bytes required, %zu given", what, need,
                 workspace_bytes);
-  bool bad_scales = false;
-  st = from_hip(
+  return from_hip(
       ca::launch_mxfp8((int)out_dtype, (int)scale_kind, q, q_scale, k, k_scale, v, v_scale, out,
                        batch, num_heads, seq_len, head_dim, softmax_scale, is_causal != 0, workspace,
-                       workspace_bytes, &bad_scales, (hipStream_t)stream),
+                       workspace_bytes, (hipStream_t)stream),
       what);
+}
+
+ca_status ca_check_mx_scales(const float* q_scale, const float* k_scale, const float* v_scale,
+                             int batch, int num_heads, int seq_len, int head_dim, void* stream) {
+  const char* what = "check_mx_scales";
+  if (batch < 0 || num_heads < 0 || seq_len < 0 || head_dim <= 0 || head_dim % 32)
+    return fail(CA_INVALID_ARGUMENT, "%s: negative size or head_dim not a multiple of 32", what);
+  const long long n = (long long)batch * num_heads * seq_len * (head_dim / 32);
+  if (n == 0) return CA_OK;
+  if (!q_scale || !k_scale || !v_scale) return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
+  if ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale) |
+       reinterpret_cast<uintptr_t>(v_scale)) & 3u)
+    return fail(CA_INVALID_ARGUMENT, "%s: float scales must be 4-byte aligned", what);
+  bool bad = false;
+  ca_status st = from_hip(ca::check_mx_scales(q_scale, k_scale, v_scale, n, &bad, (hipStream_t)stream), what);
   if (st != CA_OK) return st;
-  if (bad_scales)
+  if (bad)
     return fail(CA_INVALID_ARGUMENT,
                 "%s: float MX scales must be powers of two in [2^-127, 2^127] (the e8m0 values)",
                 what);
@@ -431,23 +443,48 @@ ca_status ca_check_block_tables(const int32_t* block_tables, const int32_t* cont
     return fail(CA_INVALID_ARGUMENT, "%s: null pointer", what);
   // the tables may still be being written on `stream`
   hipError_t e = hipStreamSynchronize((hipStream_t)stream);
-  std::vector<int32_t> lens((size_t)num_seqs), tab((size_t)num_seqs * max_blocks_per_seq);
-  if (e == hipSuccess)
-    e = hipMemcpy(lens.data(), context_lens, lens.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
-  if (e == hipSuccess && !tab.empty())
-    e = hipMemcpy(tab.data(), block_tables, tab.size() * sizeof(int32_t), hipMemcpyDeviceToHost);
-  if (e != hipSuccess)
-    return fail(CA_LAUNCH_FAILED, "%s: copy failed: %s", what, hipGetErrorString(e));
-  for (int n = 0; n < num_seqs; ++n) {
-    const long long len = lens[n] < 0 ? 0 : lens[n];
-    const long long used = std::min<long long>((len + page_size - 1) / page_size, max_blocks_per_seq);
-    for (long long j = 0; j < used; ++j) {
-      const int32_t id = tab[(size_t)n * max_blocks_per_seq + j];
-      if (id < 0 || id >= num_blocks)
-        return fail(CA_INVALID_ARGUMENT,
-                    "%s: block_tables[%d][%lld] = %d is outside the pool [0, %d) (context length %lld)",
-                    what, n, j, (int)id, num_blocks, len);
+  if (e != hipSuccess) return fail(CA_LAUNCH_FAILED, "%s: %s", what, hipGetErrorString(e));
+  // host memory stays bounded: lengths and table entries go through buffers
+  // of at most kChunk entries, runs of whole rows at a time (a row longer
+  // than kChunk in pieces)
+  constexpr size_t kChunk = size_t(1) << 20;
+  const size_t W = (size_t)max_blocks_per_seq;
+  const int rows = (int)std::min<size_t>({(size_t)num_seqs, kChunk, W ? std::max<size_t>(1, kChunk / W) : kChunk});
+  try {
+    std::vector<int32_t> lens((size_t)rows), buf(std::min(W * rows, kChunk));
+    for (int n0 = 0; n0 < num_seqs; n0 += rows) {
+      const int nr = std::min(rows, num_seqs - n0);
+      e = hipMemcpy(lens.data(), context_lens + n0, (size_t)nr * sizeof(int32_t), hipMemcpyDeviceToHost);
+      const bool whole = W * nr <= kChunk;   // the run's rows in one copy
+      if (e == hipSuccess && whole && W)
+        e = hipMemcpy(buf.data(), block_tables + (size_t)n0 * W, W * nr * sizeof(int32_t), hipMemcpyDeviceToHost);
+      if (e != hipSuccess) return fail(CA_LAUNCH_FAILED, "%s: copy failed: %s", what, hipGetErrorString(e));
+      for (int i = 0; i < nr; ++i) {
+        const int n = n0 + i;
+        const long long len = lens[(size_t)i] < 0 ? 0 : lens[(size_t)i];
+        const long long used = std::min<long long>((len + page_size - 1) / page_size, max_blocks_per_seq);
+        for (long long j0 = 0; j0 < used; j0 += (long long)buf.size()) {
+          const long long m = std::min<long long>((long long)buf.size(), used - j0);
+          const int32_t* row = buf.data() + (whole ? (size_t)i * W : 0);
+          if (!whole) {
+            e = hipMemcpy(buf.data(), block_tables + (size_t)n * W + j0, (size_t)m * sizeof(int32_t),
+                          hipMemcpyDeviceToHost);
+            if (e != hipSuccess)
+              return fail(CA_LAUNCH_FAILED, "%s: copy failed: %s", what, hipGetErrorString(e));
+          }
+          for (long long j = 0; j < m; ++j) {
+            const int32_t id = row[whole ? j0 + j : j];
+            if (id < 0 || id >= num_blocks)
+              return fail(CA_INVALID_ARGUMENT,
+                          "%s: block_tables[%d][%lld] = %d is outside the pool [0, %d) (context length %lld)",
+                          what, n, j0 + j, (int)id, num_blocks, len);
+          }
+          if (whole) break;   // the whole row is in buf
+        }
+      }
     }
+  } catch (const std::bad_alloc&) {
+    return fail(CA_LAUNCH_FAILED, "%s: out of host memory", what);
   }
   return CA_OK;
 }

@@ -30,6 +30,7 @@
 // A sequence that fits one split writes its output directly; otherwise each
 // wave writes (o / l, log2-sum-exp) to the workspace and decode_merge_kernel
 // combines the splits.
+#include <functional>
 #include <mutex>
 
 #include "common.h"
@@ -1088,34 +1089,60 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
 // Scratch for the allocation-free FP8 paged decode entry point: the split-K
 // partials live in this file-scope device array instead of a caller
 // workspace. Each device holds its own copy (at its own address) from the
-// library's load until the process ends; every call on a device shares it,
-// so calls that overlap on one device race. Its contents need no clearing:
-// the merge reads only the partials its own launch wrote.
+// library's load until the process ends. Its contents need no clearing: the
+// merge reads only the partials its own launch wrote. Calls on one device are
+// serialised on it: each call's stream waits for the previous call's launches
+// when that call used another stream (an event per device, recorded after
+// every launch); under stream capture that ordering is the caller's, as for
+// any graph.
 // ---------------------------------------------------------------------------
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
+struct ScratchState {
+  void* ptr = nullptr;          // device address of `scratch` on this device
+  hipEvent_t done = nullptr;    // recorded after the last call's launches
+  hipStream_t last = nullptr;   // that call's stream
+  bool recorded = false;
+};
 std::mutex g_scratch_mu;
-void* g_scratch_dev[64];  // device -> device address of `scratch` there
+ScratchState g_scratch[64];
 }  // namespace
 
-hipError_t noalloc_scratch(void** ptr) {
+hipError_t with_noalloc_scratch(hipStream_t stream, const std::function<hipError_t(void*)>& run) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_dev[dev]) {
-    // host code names `scratch` only here: its device address comes from the
-    // runtime, once per device, with that device current
+  ScratchState& st = g_scratch[dev];
+  if (!st.ptr) {
+    // set-up, once per device with it current: host code names `scratch`
+    // only here (its device address comes from the runtime), and the
+    // serialising event is created
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
-    g_scratch_dev[dev] = p;
+    e = hipEventCreateWithFlags(&st.done, hipEventDisableTiming);
+    if (e != hipSuccess) return e;
+    st.ptr = p;
   }
-  *ptr = g_scratch_dev[dev];
-  return hipSuccess;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cs);
+  if (e != hipSuccess) return e;
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  if (!capturing && st.recorded && st.last != stream) {
+    e = hipStreamWaitEvent(stream, st.done, 0);
+    if (e != hipSuccess) return e;
+  }
+  e = run(st.ptr);
+  if (e == hipSuccess && !capturing) {
+    e = hipEventRecord(st.done, stream);
+    st.last = stream;
+    st.recorded = e == hipSuccess;
+  }
+  return e;
 }
 
 size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int D,

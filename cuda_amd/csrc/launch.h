@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <functional>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -113,7 +115,9 @@ size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int
 // device array of kNoAllocScratchBytes per device; *ptr receives its address
 // on the current device (looked up once per device).
 constexpr size_t kNoAllocScratchBytes = 16u << 20;
-hipError_t noalloc_scratch(void** ptr);
+// Runs `run` with the device address of this device's allocation-free
+// scratch, serialised against the previous call on the device (see decode.hip).
+hipError_t with_noalloc_scratch(hipStream_t stream, const std::function<hipError_t(void*)>& run);
 
 // Contiguous-cache decode (q_len = 1 over k/v [B, Hkv, S, D]).
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,
@@ -141,14 +145,18 @@ hipError_t launch_stream_read(const void* p, size_t bytes, void* sink, hipStream
 // MXFP8 attention (mxfp8.hip): e4m3 q/k/v [B, H, S, D] with scales [B, H, S,
 // D/32], e8m0 bytes (scale_kind 0) or float32 powers of two (scale_kind 1);
 // ws holds mx_workspace_bytes (V dequantised to bf16; with float scales the
-// converted q/k scale bytes and a flag). A float scale that is not a power of
-// two in [2^-127, 2^127] sets *bad_scales (the launch then waits for that
-// check) and no attention kernel runs.
+// converted q/k scale bytes). Asynchronous in both forms: a float scale that
+// is not a power of two in [2^-127, 2^127] becomes the e8m0 NaN, so the
+// outputs it reaches are not meaningful; check_mx_scales reports such scales.
 size_t mx_workspace_bytes(int scale_kind, int B, int H, int S, int D);
 hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const void* qs,
                         const uint8_t* k, const void* ks, const uint8_t* v, const void* vs, void* o,
                         int B, int H, int S, int D, float scale, bool causal, void* ws,
-                        size_t ws_bytes, bool* bad_scales, hipStream_t stream);
+                        size_t ws_bytes, hipStream_t stream);
+// Synchronous: waits for `stream`, then sets *bad if any of the n entries of
+// the three float scale arrays is not a power of two in [2^-127, 2^127].
+hipError_t check_mx_scales(const float* qs, const float* ks, const float* vs, long long n, bool* bad,
+                           hipStream_t stream);
 // The MX prefill kernel (prefill.hip): e4m3 q, k with e8m0 scale bytes
 // qs, ks ([B, H, S, 4]) and the bf16 dequantised v; D = 128.
 hipError_t launch_prefill_mx(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,

@@ -11,19 +11,24 @@
 //   mx_prepare_kernel: V dequantised exactly into bf16 (e4m3 * 2^e is a bf16
 //     value) in the caller's workspace, once per launch rather than once per
 //     query tile; with float scales it also converts q's and k's scales to
-//     e8m0 bytes there and flags any scale that is not a power of two in
-//     [2^-127, 2^127];
+//     e8m0 bytes there. A float scale that is not a power of two in
+//     [2^-127, 2^127] becomes the e8m0 NaN (0xFF), so the outputs it reaches
+//     are not meaningful (NaN, or 0 for a row whose logits are all NaN); the
+//     call stays asynchronous, and check_mx_scales (a separate, synchronous
+//     entry) reports such scales;
 //   the prefill kernel with MX operands (prefill.hip): QK on
 //   v_mfma_scale_f32_32x32x64_f8f6f4 with the e8m0 bytes as per-lane scales,
 //   softmax and PV (bf16 MFMA on the dequantised V) as in the bf16 kernel.
+#include <algorithm>
+
 #include "common.h"
 #include "launch.h"
 
 namespace ca {
 
-// e8m0 byte of a float32 scale: 2^k -> k + 127; returns false for anything
-// that is not a power of two with k in [-127, 127] (2^-127 is the fp32
-// subnormal 0x00400000).
+// e8m0 byte of a float32 scale: 2^k -> k + 127; anything that is not a power
+// of two with k in [-127, 127] (2^-127 is the fp32 subnormal 0x00400000)
+// gives 0xFF (NaN) and false.
 __device__ __forceinline__ bool float_to_e8m0(float x, uint32_t* e) {
   const uint32_t u = __float_as_uint(x);
   if (u == 0x00400000u) {
@@ -31,8 +36,9 @@ __device__ __forceinline__ bool float_to_e8m0(float x, uint32_t* e) {
     return true;
   }
   const uint32_t be = u >> 23;
-  *e = be & 0xff;
-  return (u & 0x807fffffu) == 0 && be >= 1 && be <= 254;
+  const bool ok = (u & 0x807fffffu) == 0 && be >= 1 && be <= 254;
+  *e = ok ? be : 0xffu;
+  return ok;
 }
 
 __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
@@ -48,24 +54,23 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
 // writes one contiguous 1 KB. (16 codes per lane, two 16-byte stores 32 bytes
 // apart, ran C5's 50 MB at ~3.4 TB/s.) With float scales (F32SC) lane l also
 // converts one of the rows' q or k scales (row l / 8, block l % 4; q when
-// (l / 4) % 2 == 0) into e8m0, and any invalid scale raises *bad.
+// (l / 4) % 2 == 0) into e8m0.
 template <bool F32SC>
 __global__ __launch_bounds__(256) void mx_prepare_kernel(
     const uint8_t* __restrict__ V, const void* __restrict__ VS, const void* __restrict__ QSf,
     const void* __restrict__ KSf, uint16_t* __restrict__ Vb, uint8_t* __restrict__ QSb,
-    uint8_t* __restrict__ KSb, uint32_t* __restrict__ bad, long long n_rows) {
+    uint8_t* __restrict__ KSb, long long n_rows) {
   constexpr int D = 128, NB = D / 32;
   const int lane = threadIdx.x & 63;
   const long long row0 = (((long long)blockIdx.x * 256 + threadIdx.x) >> 6) * 8;
   if (row0 >= n_rows) return;
-  bool ok = true;
   if (F32SC) {
     const long long r = row0 + (lane >> 3);
     const int blk = lane & 3;
     if (r < n_rows) {
       const bool isq = ((lane >> 2) & 1) == 0;
       uint32_t e;
-      ok = float_to_e8m0(((const float*)(isq ? QSf : KSf))[r * NB + blk], &e);
+      float_to_e8m0(((const float*)(isq ? QSf : KSf))[r * NB + blk], &e);
       (isq ? QSb : KSb)[r * NB + blk] = (uint8_t)e;
     }
   }
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(256) void mx_prepare_kernel(
     float sc;
     if (F32SC) {
       uint32_t e;
-      ok &= float_to_e8m0(((const float*)VS)[r * NB + blk], &e);
+      float_to_e8m0(((const float*)VS)[r * NB + blk], &e);
       sc = e8m0_to_float(e);
     } else {
       sc = e8m0_to_float(((const uint8_t*)VS)[r * NB + blk]);
@@ -91,27 +96,61 @@ __global__ __launch_bounds__(256) void mx_prepare_kernel(
     w[3] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[1], sc));
     *(u32x4*)(Vb + c) = w;
   }
-  if (F32SC && !ok) *bad = 1u;  // every writer stores the same value
 }
 
-__global__ void mx_clear_flag_kernel(uint32_t* flag) { *flag = 0u; }
+// Raises *bad for any of the n float scales that is not a power of two in
+// [2^-127, 2^127] (every writer stores the same value).
+__global__ __launch_bounds__(256) void mx_check_scales_kernel(const float* __restrict__ s, long long n,
+                                                              uint32_t* __restrict__ bad) {
+  bool ok = true;
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+    uint32_t e;
+    ok &= float_to_e8m0(s[i], &e);
+  }
+  if (!ok) *bad = 1u;
+}
 
 static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Workspace: the bf16 V ([B, H, S, D]); with float scales also q's and k's
-// e8m0 bytes ([B, H, S, D/32] each) and a 4-byte flag.
+// e8m0 bytes ([B, H, S, D/32] each).
 size_t mx_workspace_bytes(int scale_kind, int B, int H, int S, int D) {
   const size_t rows = (size_t)B * H * S;
   size_t n = align256(rows * D * 2);
-  if (scale_kind == 1) n += 2 * align256(rows * (D / 32)) + 256;
+  if (scale_kind == 1) n += 2 * align256(rows * (D / 32));
   return n;
+}
+
+// Synchronous check of three float scale arrays of n entries each: waits for
+// `stream`, then sets *bad if any scale is not a power of two in
+// [2^-127, 2^127]. Allocates (and frees) a 4-byte flag.
+hipError_t check_mx_scales(const float* qs, const float* ks, const float* vs, long long n, bool* bad,
+                           hipStream_t stream) {
+  *bad = false;
+  if (n <= 0) return hipSuccess;
+  uint32_t* flag = nullptr;
+  hipError_t e = hipMalloc((void**)&flag, sizeof(uint32_t));
+  if (e != hipSuccess) return e;
+  uint32_t h = 0;
+  e = hipMemsetAsync(flag, 0, sizeof(uint32_t), stream);
+  const long long blocks = std::min<long long>((n + 255) / 256, 4096);
+  for (const float* s : {qs, ks, vs}) {
+    if (e != hipSuccess) break;
+    hipLaunchKernelGGL(mx_check_scales_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, s, n, flag);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(&h, flag, sizeof(h), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  const hipError_t ef = hipFree(flag);
+  if (e == hipSuccess) e = ef;
+  *bad = e == hipSuccess && h != 0;
+  return e;
 }
 
 hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const void* qs,
                         const uint8_t* k, const void* ks, const uint8_t* v, const void* vs, void* o,
                         int B, int H, int S, int D, float scale, bool causal, void* ws,
-                        size_t ws_bytes, bool* bad_scales, hipStream_t stream) {
-  *bad_scales = false;
+                        size_t ws_bytes, hipStream_t stream) {
   if (D != 128) return hipErrorInvalidValue;
   const long long rows = (long long)B * H * S;
   if (rows == 0) return hipSuccess;
@@ -126,27 +165,15 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
   if (scale_kind == 1) {
     uint8_t* qsb = w;
     uint8_t* ksb = w + align256((size_t)rows * (D / 32));
-    uint32_t* flag = (uint32_t*)(ksb + align256((size_t)rows * (D / 32)));
-    hipLaunchKernelGGL(mx_clear_flag_kernel, dim3(1), dim3(1), 0, stream, flag);
     hipLaunchKernelGGL(mx_prepare_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, stream, v, vs,
-                       qs, ks, vb, qsb, ksb, flag, rows);
+                       qs, ks, vb, qsb, ksb, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // the float form reports invalid scales by status, so it waits for the
-    // check (the e8m0 form stays asynchronous)
-    uint32_t h_flag = 0;
-    e = hipMemcpyAsync(&h_flag, flag, sizeof(h_flag), hipMemcpyDeviceToHost, stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    if (e != hipSuccess) return e;
-    if (h_flag) {
-      *bad_scales = true;
-      return hipSuccess;
-    }
     qs8 = qsb;
     ks8 = ksb;
   } else {
     hipLaunchKernelGGL(mx_prepare_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, stream, v, vs,
-                       nullptr, nullptr, vb, nullptr, nullptr, nullptr, rows);
+                       nullptr, nullptr, vb, nullptr, nullptr, rows);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -200,8 +200,11 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
  * scratch, num_seqs * num_q_heads * splits * (head_dim + 1) * 4 bytes with
  * splits = ceil(max_blocks_per_seq / 128) for fp16/bf16 queries and
  * ceil(max_blocks_per_seq / 64) for float32 (none when that is 1), return
- * CA_INVALID_ARGUMENT. Every call on a device shares that device's scratch:
- * calls that overlap on one device (concurrent streams or threads) race. */
+ * CA_INVALID_ARGUMENT. Every call on a device shares that device's scratch,
+ * so the calls are serialised on the device: a call on another stream than
+ * the previous call's waits (on the GPU, through an event) for that call's
+ * kernels, and concurrent host threads take turns. Under stream capture that
+ * wait is left out and the order of the graph launches is the caller's. */
 #define CA_NOALLOC_SCRATCH_BYTES (16u << 20)
 ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
                                          const uint8_t* key_cache, const uint8_t* value_cache,
@@ -225,11 +228,11 @@ typedef enum CA_ENUM_INT { CA_SCALE_E8M0 = 0, CA_SCALE_F32 = 1 } ca_scale_kind;
  * CA_SCALE_F32 so must q_scale and v_scale). Replaces
  * dispatch_fused_microscaled_attention<T_OUT> (kernels_api.h:103-108).
  * workspace: ca_mx_workspace_bytes(...) (v dequantised to bf16; with float
- * scales also q's and k's converted scale bytes). With CA_SCALE_F32 a scale
- * that is not a power of two in [2^-127, 2^127] returns CA_INVALID_ARGUMENT
- * and no output is written; to report that, the float form waits for its
- * scale check (the stream is synchronised once), while the e8m0 form is
- * asynchronous like the other entry points. */
+ * scales also q's and k's converted scale bytes). Asynchronous in both scale
+ * forms, like the other entry points: with CA_SCALE_F32 a scale that is not a
+ * power of two in [2^-127, 2^127] is taken as the e8m0 NaN, so the outputs it
+ * reaches are not meaningful (NaN, or 0 for a row whose logits are all NaN);
+ * ca_check_mx_scales reports such scales. */
 ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, const void* q_scale,
                                          const uint8_t* k, const void* k_scale, const uint8_t* v,
                                          const void* v_scale, ca_scale_kind scale_kind, void* out,
@@ -241,6 +244,15 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, c
  * shape or scale kind). */
 size_t ca_mx_workspace_bytes(ca_scale_kind scale_kind, int batch, int num_heads, int seq_len,
                              int head_dim);
+
+/* Debug check of float MX scales (no counterpart in the reference, whose
+ * kernels_api.h:103-108 takes the scales unchecked): returns
+ * CA_INVALID_ARGUMENT if any entry of q_scale, k_scale or v_scale ([batch,
+ * num_heads, seq_len, head_dim / 32] float32 each) is not a power of two in
+ * [2^-127, 2^127], which ca_fused_microscaled_attention would take as NaN.
+ * Synchronous: it waits for `stream`; it allocates a 4-byte flag. */
+ca_status ca_check_mx_scales(const float* q_scale, const float* k_scale, const float* v_scale,
+                             int batch, int num_heads, int seq_len, int head_dim, void* stream);
 
 /* Debug check of a paged-cache block table (no counterpart in the reference,
  * which reads through the table unchecked, paged_attention_kernel.cuh:69):

@@ -164,6 +164,26 @@ int main() {
   expect(ca_check_block_tables(nullptr, nullptr, 2, 4, 10, 16, nullptr) == CA_INVALID_ARGUMENT &&
              error_mentions("null"),
          "block tables null");
+  // a table of 10^6 x 10^6 entries: rejected (null) or failing at the stream
+  // wait (no GPU here) with a status, never an allocation of its size
+  expect(ca_check_block_tables(nullptr, nullptr, 1000000, 1000000, 10, 16, nullptr) ==
+             CA_INVALID_ARGUMENT,
+         "block tables huge, null");
+  expect(ca_check_block_tables(PI, PI, 1000000, 1000000, 10, 16, nullptr) != CA_OK,
+         "block tables huge, no device");
+  // the float MX scale check
+  expect(ca_check_mx_scales(PF, PF, PF, -1, 2, 8, 128, nullptr) == CA_INVALID_ARGUMENT,
+         "mx scales negative");
+  expect(ca_check_mx_scales(PF, PF, PF, 1, 2, 8, 100, nullptr) == CA_INVALID_ARGUMENT,
+         "mx scales head_dim");
+  expect(ca_check_mx_scales(nullptr, PF, PF, 1, 2, 8, 128, nullptr) == CA_INVALID_ARGUMENT &&
+             error_mentions("null"),
+         "mx scales null");
+  expect(ca_check_mx_scales(reinterpret_cast<const float*>(odd), PF, PF, 1, 2, 8, 128, nullptr) ==
+                 CA_INVALID_ARGUMENT && error_mentions("aligned"),
+         "mx scales aligned");
+  expect(ca_check_mx_scales(nullptr, nullptr, nullptr, 1, 2, 0, 128, nullptr) == CA_OK,
+         "mx scales empty");
 
   std::printf(failures ? "abi checks: %d failed\n" : "abi checks: all passed\n", failures);
   return failures ? 1 : 0;

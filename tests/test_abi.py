@@ -191,7 +191,7 @@ def test_mxfp8_rejects_bad_arguments():
     ws = L.load().ca_mx_workspace_bytes(E8, 1, 2, 64, 128)
     assert ws == 1 * 2 * 64 * 128 * 2  # the bf16 V
     wsf = L.load().ca_mx_workspace_bytes(F32, 1, 2, 64, 128)
-    assert wsf == ws + 2 * 512 + 256   # + q/k scale bytes (256-aligned) + flag
+    assert wsf == ws + 2 * 512         # + q/k scale bytes (256-aligned)
     assert L.load().ca_mx_workspace_bytes(E8, 1, 2, 64, 64) == 0
     assert L.load().ca_mx_workspace_bytes(7, 1, 2, 64, 128) == 0
 
@@ -260,3 +260,15 @@ def test_check_block_tables_argument_checks():
     assert _status("ca_check_block_tables", None, None, 2, 4, 10, 16, None) == L.CA_INVALID_ARGUMENT
     assert b"null" in L.load().ca_last_error()
     assert _status("ca_check_block_tables", None, None, 0, 4, 10, 16, None) == L.CA_OK
+
+
+def test_check_mx_scales_argument_checks():
+    """ca_check_mx_scales rejects bad sizes, null and misaligned pointers
+    before touching device memory; an empty shape is OK."""
+    assert _status("ca_check_mx_scales", P, P, P, -1, 2, 8, 128, None) == L.CA_INVALID_ARGUMENT
+    assert _status("ca_check_mx_scales", P, P, P, 1, 2, 8, 100, None) == L.CA_INVALID_ARGUMENT
+    assert _status("ca_check_mx_scales", None, P, P, 1, 2, 8, 128, None) == L.CA_INVALID_ARGUMENT
+    assert b"null" in L.load().ca_last_error()
+    assert _status("ca_check_mx_scales", ctypes.c_void_p(18), P, P, 1, 2, 8, 128, None) == L.CA_INVALID_ARGUMENT
+    assert b"aligned" in L.load().ca_last_error()
+    assert _status("ca_check_mx_scales", None, None, None, 1, 2, 0, 128, None) == L.CA_OK

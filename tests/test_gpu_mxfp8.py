@@ -165,11 +165,21 @@ def _abi_call(x, kind, scales, out, causal=True):
         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
 
 
+def _check_scales(x, scales):
+    import ctypes
+    import cuda_amd._lib as L
+    b, h, s, d = x["q"].shape
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    return L.load().ca_check_mx_scales(p(scales[0]), p(scales[1]), p(scales[2]), b, h, s, d,
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+
+
 def test_mx_float_scale_form_of_the_c_abi(dev):
     """The reference's float-scale interface (kernels_api.h:103-108) at the C
-    ABI: float32 powers of two give the e8m0 form's output bit for bit; a
-    scale that is not such a power of two is rejected with
-    CA_INVALID_ARGUMENT before any attention kernel writes the output."""
+    ABI: float32 powers of two give the e8m0 form's output bit for bit. The
+    call is asynchronous in both forms: a scale that is not such a power of
+    two is taken as the e8m0 NaN, so the outputs it reaches are not
+    meaningful, and the separate, synchronous ca_check_mx_scales reports it."""
     import cuda_amd._lib as L
     x = mx_inputs(2, 2, 300, 128, dev, seed=7)
     e8 = [x[n + "_scale"].contiguous() for n in "qkv"]
@@ -180,19 +190,48 @@ def test_mx_float_scale_form_of_the_c_abi(dev):
     assert _abi_call(x, L.CA_SCALE_F32, f32, b) == L.CA_OK
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+    assert _check_scales(x, f32) == L.CA_OK
     d = _ref(x)
     assert_close(to_np(b), oracle.attention(d["q"], d["k"], d["v"], is_causal=True), **TOL_FP8,
                  name="float scales")
     for bad, which in ((3.0, 0), (0.0, 1), (-0.5, 2), (float("nan"), 1), (0.75, 2)):
         sc = [t.clone() for t in f32]
-        sc[which].view(-1)[123] = bad
-        out = torch.full_like(a, 7.0)
-        assert _abi_call(x, L.CA_SCALE_F32, sc, out) == L.CA_INVALID_ARGUMENT
+        sc[which].view(-1)[123] = bad          # row 30 of head (0, 0), block 3
+        assert _check_scales(x, sc) == L.CA_INVALID_ARGUMENT
         assert b"powers of two" in L.load().ca_last_error()
+        out = torch.full_like(a, 7.0)
+        assert _abi_call(x, L.CA_SCALE_F32, sc, out) == L.CA_OK
         torch.cuda.synchronize()
-        assert torch.all(out == 7.0), "no output is written for rejected scales"
+        # what the bad scale cannot reach equals the valid output bit for bit:
+        # the other heads, and for q the other query rows (what it reaches is
+        # not meaningful and is not pinned)
+        same = out == b
+        assert same[1].all() and same[0, 1].all()
+        if which == 0:
+            assert same[0, 0, :30].all() and same[0, 0, 31:].all() and not same[0, 0, 30].all()
     # the smallest and largest e8m0 values are accepted in float form
     sc = [t.clone() for t in f32]
     sc[1].view(-1)[5] = 2.0 ** -127
     sc[1].view(-1)[6] = 2.0 ** 127
+    assert _check_scales(x, sc) == L.CA_OK
     assert _abi_call(x, L.CA_SCALE_F32, sc, torch.empty_like(a)) == L.CA_OK
+
+
+def test_mx_scale_check_opt_in(dev, monkeypatch):
+    """CUDA_LLM_CHECK_MX_SCALES=1 makes the Python entry check float scales
+    first and raise; by default the call goes through (the row the bad q
+    scale reaches is not meaningful, the others are unchanged)."""
+    x = mx_inputs(1, 1, 64, 128, dev, seed=3)
+    f32 = [torch.ldexp(torch.ones_like(x[n + "_scale"], dtype=torch.float32),
+                       x[n + "_scale"].to(torch.int32) - 127) for n in "qkv"]
+    f32[0].view(-1)[0] = 0.3
+    monkeypatch.setenv("CUDA_LLM_CHECK_MX_SCALES", "0")
+    good = [t.clone() for t in f32]
+    good[0].view(-1)[0] = 1.0
+    ref = cuda_llm.fused_microscaled_attention(x["q"], good[0], x["k"], good[1], x["v"], good[2], is_causal=True)
+    out = cuda_llm.fused_microscaled_attention(x["q"], f32[0], x["k"], f32[1], x["v"], f32[2], is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out[0, 0, 1:], ref[0, 0, 1:]) and not torch.equal(out[0, 0, 0], ref[0, 0, 0])
+    monkeypatch.setenv("CUDA_LLM_CHECK_MX_SCALES", "1")
+    with pytest.raises(RuntimeError, match="powers of two"):
+        cuda_llm.fused_microscaled_attention(x["q"], f32[0], x["k"], f32[1], x["v"], f32[2], is_causal=True)

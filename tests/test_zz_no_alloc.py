@@ -19,7 +19,7 @@ from _util import TOL_FP8, assert_close, build_paged, paged_oracle, to_np
 pytestmark = pytest.mark.gpu
 
 
-def _noalloc(case, scale=None):
+def _noalloc(case, scale=None, stream=None):
     q = case["query"]
     n, hq, d = q.shape
     kc = case["key_cache"]
@@ -31,7 +31,7 @@ def _noalloc(case, scale=None):
            p(case["k_scale"]), p(case["v_scale"]), int(per_block), p(case["block_tables"]),
            p(case["context_lens"]), p(out), n, hq, kc.shape[1], d, case["block_tables"].shape[1],
            16, kc.shape[0], 1.0 / d ** 0.5 if scale is None else scale,
-           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+           ctypes.c_void_p((stream or torch.cuda.current_stream()).cuda_stream))
     return out
 
 
@@ -57,6 +57,25 @@ def test_noalloc_matches_workspace_form_twice(dev, dtype):
         tol = TOL_FP8 if dtype != torch.float32 else dict(max_abs=1e-4, mean_abs=1e-5)
         assert_close(to_np(out), paged_oracle(case, dtype=np.float64), **tol, name=name)
     assert torch.all(_noalloc(big)[3] == 0)  # empty context -> zero row
+
+
+def test_noalloc_two_streams(dev):
+    """Calls on two streams, issued back to back with no host wait between,
+    share the scratch: the second call's stream waits for the first call on
+    the GPU, so both outputs equal the workspace form bit for bit."""
+    big = build_paged([5000, 4000, 3000, 2600], 32, 8, 128, torch.bfloat16, dev, fp8=True,
+                      per_block=True, pool=1200, seed=3)
+    small = build_paged([2100, 2000, 1900], 32, 8, 128, torch.bfloat16, dev, fp8=True,
+                        per_block=True, pool=400, seed=4)
+    refs = [_with_workspace(c) for c in (big, small)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        a = _noalloc(big, stream=s1)
+        b = _noalloc(small, stream=s2)
+        c = _noalloc(big, stream=s1)
+        torch.cuda.synchronize()
+        assert torch.equal(a, refs[0]) and torch.equal(b, refs[1]) and torch.equal(c, refs[0])
 
 
 def test_noalloc_rejects_sizes_beyond_scratch(dev):
