@@ -139,12 +139,12 @@ def test_mx_persistent_grid(dev, b, h, s, causal):
 
 
 def test_baseline_c5_shape(dev):
-    """C5: B=1, H=16, S=8192, D=128, causal; sampled heads vs the oracle."""
+    """C5: B=1, H=16, S=8192, D=128, causal; every head vs the oracle."""
     x = mx_inputs(1, 16, 8192, 128, dev, seed=0)
     out = _run(x, True)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    for h in (0, 9):
+    for h in range(16):
         d = _ref(x, heads=(0, h))
         ref = oracle.attention(d["q"], d["k"], d["v"], is_causal=True)
         assert_close(to_np(out[:, h:h + 1]), ref, **TOL_FP8, name=f"C5 head {h}")

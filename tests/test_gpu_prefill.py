@@ -200,21 +200,23 @@ def test_deterministic(dev):
 
 
 @pytest.mark.parametrize("cfg", [
-    dict(b=4, h=32, s=4096, causal=True, heads=[(0, 0), (1, 17), (3, 31)]),
-    dict(b=4, h=32, s=2048, causal=False, heads=[(0, 5), (2, 20), (3, 31)]),
+    dict(b=4, h=32, s=4096, causal=True),
+    dict(b=4, h=32, s=2048, causal=False),
 ])
 def test_baseline_c2_shapes(dev, cfg):
     """BASELINE C2 (bf16 prefill B=4, H=32, S=4096 causal / 2048 non-causal,
-    D=128): sampled heads against the oracle; all heads through invariants."""
+    D=128): every head against the oracle, each head within the 16-bit
+    tolerance."""
     b, h, s = cfg["b"], cfg["h"], cfg["s"]
     q, k, v = qkv(b, h, s, 128, torch.bfloat16, dev)
     out = cuda_llm.flash_attention(q, k, v, is_causal=cfg["causal"])
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    for (bi, hi) in cfg["heads"]:
-        ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, hi:hi + 1]),
-                               to_np(v[bi:bi + 1, hi:hi + 1]), is_causal=cfg["causal"])
-        assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_16BIT, name=f"head {bi},{hi}")
+    ref = oracle.attention(to_np(q), to_np(k), to_np(v), is_causal=cfg["causal"])
+    o = to_np(out)
+    for bi in range(b):
+        for hi in range(h):
+            assert_close(o[bi, hi], ref[bi, hi], **TOL_16BIT, name=f"head {bi},{hi}")
     if cfg["causal"]:
         # row 0 attends only to key 0: output equals v[..., 0, :] up to bf16 rounding
         assert (out[:, :, 0].float() - v[:, :, 0].float()).abs().max().item() <= 1e-2
