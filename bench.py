@@ -116,15 +116,13 @@ def time_cold(fn, reps=20, flush_bytes=1 << 30):
 
 def _traffic(key):
     """HBM bytes per step measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), committed in
-    profiles/traffic.json; `key` names one kernel's entry or a tuple of the
-    entries of a multi-kernel step."""
+    WRITE_SIZE of every kernel of the step, scaled by the copy-kernel
+    calibration), committed in profiles/traffic.json by --traffic-json."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
-    keys = key if isinstance(key, tuple) else (key,)
     try:
         with open(path) as f:
             t = json.load(f)
-        return sum(float(t[k]["fetch_bytes"]) + float(t[k]["write_bytes"]) for k in keys)
+        return float(t[key]["fetch_bytes"]) + float(t[key]["write_bytes"])
     except (OSError, KeyError, ValueError, TypeError):
         return None
 
@@ -632,9 +630,16 @@ WORKLOADS = {
     "refgrid": w_refgrid,
     "host": w_host,
 }
-TRAFFIC_KEY = {"prefill": "prefill_c2_causal", "prefill_nc": "prefill_c2_noncausal",
-               "decode_fp8": "fp8_decode_c4", "decode_bf16": "bf16_decode_c3", "mxfp8": "mxfp8_c5",
-               "backward": ("backward_c2_dkv", "backward_c2_dq"), "c1": "prefill_c1_f32"}
+# the workloads whose step traffic profiles/traffic.json holds (every kernel
+# of the step: decode = split + merge, MXFP8 = prepare + attention, backward =
+# row dot + dK/dV + dQ)
+TRAFFIC_WORKLOADS = ("prefill", "prefill_nc", "decode_fp8", "decode_bf16", "mxfp8", "backward", "c1")
+TRAFFIC_KEY = {w: w for w in TRAFFIC_WORKLOADS}
+# kernels a workload's run launches outside its timed step: the streaming-read
+# ceiling the decode lines report beside them, the forward that makes the
+# backward's inputs
+TRAFFIC_NOT_STEP = {"decode_fp8": ("stream_read",), "decode_bf16": ("stream_read",),
+                    "backward": ("prefill_",)}
 
 
 def summary(name, r, read_gbs=None):
@@ -715,6 +720,51 @@ def pmc_summary(path):
     print(json.dumps({k: {c: v[0] / v[1] for c, v in d.items()} for k, d in acc.items()}, indent=1))
 
 
+def _pmc_means(path, counter):
+    """{kernel: mean counter value per dispatch} of this library's kernels
+    (and the copy kernel) in one rocprofv3 --pmc CSV."""
+    import csv
+    acc = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = _kernel_short_name(r["Kernel_Name"])
+            if r["Counter_Name"] == counter and (name.startswith("ca::") or "copyBuffer" in name):
+                a = acc.setdefault(name, [0.0, 0])
+                a[0] += float(r["Counter_Value"])
+                a[1] += 1
+    return {k: v[0] / v[1] for k, v in acc.items()}
+
+
+def traffic_json(pmc_dir, out):
+    """Writes the step traffic of each TRAFFIC_WORKLOADS workload from one
+    FETCH_SIZE and one WRITE_SIZE run per workload (rocprofv3 -d
+    <pmc_dir>/<workload>_fetch, _write; and copy_fetch, copy_write for the
+    calibration): per kernel the mean KiB per dispatch, summed over the
+    step's kernels (each runs once per step), scaled to bytes by what the
+    counters read for the copy of w_copy's known size."""
+    csvp = lambda w, c: os.path.join(pmc_dir, f"{w}_{c}", "run_counter_collection.csv")
+    nbytes = 2 << 30
+    cf = _pmc_means(csvp("copy", "fetch"), "FETCH_SIZE")
+    cw = _pmc_means(csvp("copy", "write"), "WRITE_SIZE")
+    kf = max(cf.values()) * 1024
+    kw = max(cw.values()) * 1024
+    res = {"_calibration": {"kernel": next(iter(cf)), "bytes_read": nbytes, "bytes_written": nbytes,
+                            "fetch_size_kib": kf / 1024, "write_size_kib": kw / 1024,
+                            "fetch_factor": nbytes / kf, "write_factor": nbytes / kw}}
+    for w in TRAFFIC_WORKLOADS:
+        f = _pmc_means(csvp(w, "fetch"), "FETCH_SIZE")
+        wr = _pmc_means(csvp(w, "write"), "WRITE_SIZE")
+        skip = ("copyBuffer",) + TRAFFIC_NOT_STEP.get(w, ())
+        ks = sorted(k for k in set(f) & set(wr) if not any(x in k for x in skip))
+        res[w] = {"kernels": ks,
+                  "fetch_bytes": round(sum(f[k] for k in ks) * 1024 * nbytes / kf),
+                  "write_bytes": round(sum(wr[k] for k in ks) * 1024 * nbytes / kw)}
+    with open(out, "w") as fh:
+        json.dump(res, fh, indent=1)
+        fh.write("\n")
+    print(json.dumps(res, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser(description="attention forward hot path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -732,7 +782,13 @@ def main():
                          "dispatches (no GPU needed)")
     ap.add_argument("--pmc-summary", metavar="CSV",
                     help="average a rocprofv3 --pmc CSV per kernel (no GPU needed)")
+    ap.add_argument("--traffic-json", nargs=2, metavar=("PMC_DIR", "OUT"),
+                    help="write per-workload step traffic from FETCH_SIZE / WRITE_SIZE runs "
+                         "(no GPU needed)")
     args = ap.parse_args()
+    if args.traffic_json:
+        traffic_json(*args.traffic_json)
+        return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
         return
