@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcuda_llm_amd.so")
-SOURCES = ["prefill.hip", "prefill_w64.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "backward_f32.hip",
+SOURCES = ["prefill.hip", "prefill_w64.hip", "prefill_w64_mx.hip", "decode.hip", "mxfp8.hip", "f32.hip", "backward.hip", "backward_f32.hip",
            "kv_append.hip", "rope.hip", "stream_read.hip", "abi.cpp"]
 ARCH = os.environ.get("CA_OFFLOAD_ARCH", "gfx950")
 
@@ -44,12 +44,13 @@ EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
 # Generated sources: the 64-row prefill's kernel body (hand-scheduled
 # assembly, checked for hazards by its generator) is written into the build
 # directory before the compile.
-GENERATED = {"prefill_w64.hip": ("gen_prefill_w64.py", "prefill_w64_body.inc")}
+GENERATED = {"prefill_w64.hip": ("gen_prefill_w64.py", "prefill_w64_body.inc", ()),
+             "prefill_w64_mx.hip": ("gen_prefill_w64.py", "prefill_w64_mx_body.inc", ("--mx",))}
 
 
 def _generate(src):
-    gen, out = GENERATED[src]
-    r = subprocess.run([sys.executable, os.path.join(CSRC, gen), os.path.join(BUILD, out)],
+    gen, out, flags = GENERATED[src]
+    r = subprocess.run([sys.executable, os.path.join(CSRC, gen), *flags, os.path.join(BUILD, out)],
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"{gen} failed:\n{r.stderr}")

@@ -185,6 +185,18 @@ def BLOAD_LDS(voff, rsrc, off=0):
     return Ins("vmem", t, defs=[], uses=[voff, rsrc, M0], mem="vm", m0use=True, cost=4)
 
 
+def BLOAD_LDS_DW(voff, rsrc, off=0):
+    """4 bytes per lane into LDS at M0 + off + 4 lane."""
+    t = f"buffer_load_dword {voff}, {rsrc}, 0 offen" + (f" offset:{off}" if off else "") + " lds"
+    return Ins("vmem", t, defs=[], uses=[voff, rsrc, M0], mem="vm", m0use=True, cost=4)
+
+
+def GLOAD(op, d, voff, base, off=0):
+    """Global load at base (64-bit SGPR pair) + voff (32-bit VGPR offset)."""
+    t = f"{op} {d}, {voff}, {base}" + (f" offset:{off}" if off else "")
+    return Ins("vmem", t, defs=[d], uses=[voff, base], mem="vm", cost=4)
+
+
 def BSTORE(op, data, voff, rsrc, off=0):
     t = f"{op} {data}, {voff}, {rsrc}, 0 offen" + (f" offset:{off}" if off else "")
     return Ins("vmem", t, defs=[], uses=[data, voff, rsrc], mem="vm", std=data.keys(), cost=4)
@@ -558,6 +570,77 @@ N_SGPR_OWN = 94       # s0..s93 (except s32, s33, which the compiler reserves)
 IN_S = ["ka", "wg", "ng", "wv", "lb"]
 INS_ = {nm: Sym(nm) for nm in IN_S}
 
+# ---------------------------------------------------------------------------
+# MXFP8 variant (configure(True)): Q and K are e4m3 codes with one e8m0 scale
+# byte per 32 elements along D, V the bf16 dequantisation. QK runs on
+# v_mfma_scale_f32_32x32x64_f8f6f4: per 64-d k-step s2 lane half h supplies
+# d = 64 s2 + 16 h + [0, 16) in bytes 0-15 and 64 s2 + 32 + 16 h + [0, 16) in
+# bytes 16-31, with the scale of MX block 2 s2 + h, for K rows from LDS and
+# Q rows from AGPRs alike. A lane's scale bytes sit in one register, byte
+# 2 b + s2 for row block b (key block mb / query block nb), picked by the
+# MFMA's op_sel. The K tile is 64 rows of 128 code bytes (8 KB, 128-byte-row
+# swizzle), then at +8 KB the tile's 64 scale words; V as in the bf16 walk.
+# ---------------------------------------------------------------------------
+MX = False
+_BF16_STATE = None
+# vector-memory loads per walk iteration, per query tile's Q, and of the
+# prologue after K(0) and Q (bf16: K 4 + V 4; Q 16; K(1), K(2), V(0))
+NLD_IT, NLD_Q, NLD_PRO = 8, 16, 12
+KTILE = 16384              # bytes of a K tile in HBM (64 rows)
+CLOB_SKIP_V = ()           # VGPRs below N_VGPR_OWN left to the compiler's inputs
+
+
+def configure(mx):
+    """Rebinds the register map and limits of the bf16 (mx False) or the
+    MXFP8 (mx True) kernel body."""
+    global MX, FRAG, IN_V, INV, STEADY_SPAN, NLD_IT, NLD_Q, NLD_PRO, KTILE, CLOB_SKIP_V, _BF16_STATE
+    global QA_MX, KSW, KSWT, QSC, QSW, KXM, QSO, RKS, QSP, KSP, WOFFK, OUTF16, MASKHI
+    names = ("FRAG", "IN_V", "INV", "STEADY_SPAN", "NLD_IT", "NLD_Q", "NLD_PRO", "KTILE", "CLOB_SKIP_V")
+    g = globals()
+    if _BF16_STATE is None:
+        _BF16_STATE = {nm: g[nm] for nm in names}
+    MX = mx
+    if not mx:
+        g.update(_BF16_STATE)
+        return
+    # all fragments in AGPRs, 8 per slot (a K fragment is two b128 reads, a
+    # V^T fragment uses the first 4); the VGPRs the bf16 map gives them are
+    # the scale words' and the Q scale loads'
+    FRAG = [a(160 + 8 * t, 8) for t in range(8)]
+    QA_MX = [[a(128 + 16 * nb + 8 * s2, 8) for s2 in range(2)] for nb in range(2)]
+    KSW = v(184)               # scale bytes of the lane's key rows, byte 2 mb + s2
+    KSWT = [v(185), v(186)]    # scale words of rows krow, krow + 32 as read
+    QSC = v(187)               # scale bytes of the lane's query rows, byte 2 nb + s2
+    QSW = [v(188), v(189)]     # their words, loaded with the tile's Q
+    KXM = [KA, KX, v(190), v(191)]   # K read bases of the 32-byte chunk pairs 0..3 (KA ^ 32 cp)
+    QSO = [v(192), v(193)]     # Q scale word offsets of the lane's two rows
+    CLOB_SKIP_V = tuple(range(194, 200))
+    IN_V = ["kofs", "vofs1", "vofs2", "loff0", "loff1", "loff2", "loff3", "kl0", "kl1", "sl", "ksr",
+            "psel", "qlane", "dl", "h8", "wbase", "wx", "rdl", "stl"]
+    INV = {nm: Sym(nm) for nm in IN_V}
+    STEADY_SPAN = 33
+    NLD_IT, NLD_Q, NLD_PRO = 7, 10, 10
+    KTILE = 8192
+    # SGPRs the MX kernel frees: no LSE (RL, LP), no GQA (HKV, MHQ, SHHQ,
+    # MRATIO, SHRATIO); the argument block carries the scale pointers there
+    RKS = s(52, 4)             # K scale resource, stepped like RK
+    QSP = s(8, 2)              # Q scale words (LP's slot)
+    KSP = [s(27), s(28)]       # K scale words (MRATIO, SHRATIO's slots)
+    OUTF16 = s(25)             # output element type: 0 bf16, 1 fp16 (MHQ's slot)
+    MASKHI = s(26)             # 0xffff0000: the high bf16 of a packed pair as fp32 (SHHQ's slot)
+    WOFFK = s(20)              # LDS base + 2 KB x wave: this wave's K rows of a slot (HKV's slot)
+
+
+def MFMA_SCALE(d, a_, b_, c, sa, sb, opa, opb):
+    """v_mfma_scale_f32_32x32x64_f8f6f4 (e4m3 x e4m3) with scale bytes opa of
+    register sa (A) and opb of sb (B)."""
+    cc = c if c is not None else 0
+    t = (f"v_mfma_scale_f32_32x32x64_f8f6f4 {d}, {a_}, {b_}, {cc}, {sa}, {sb}"
+         f" op_sel:[{opa & 1},{opb & 1},0] op_sel_hi:[{opa >> 1},{opb >> 1},0]")
+    uses = [a_, b_, sa, sb] + ([c] if c is not None else [])
+    return Ins("mfma", t, defs=[d], uses=uses, mdst=tuple(d.keys()), mc=tuple(c.keys()) if c is not None else None,
+               mab=a_.keys() + b_.keys() + sa.keys() + sb.keys())
+
 RSRC3 = 0x00020000     # buffer resource word 3: raw 32-bit dwords
 LDS_V = 65536          # V ring offset in LDS
 LDS_STG = 131072       # output staging offset in LDS
@@ -597,6 +680,25 @@ def k_frag_reads(f_slot, ks, mb, first_of_ks, kslot):
     return out
 
 
+def k_frag_reads_mx(f_slot, s2, mb, kslot):
+    """MX K fragment (k-step s2, key block mb) of the tile in ring slot kslot:
+    the lane's key row krow + 32 mb, chunk pairs 2 s2 and 2 s2 + 1 (bytes
+    0-15 and 16-31 of the A operand)."""
+    return [DSR("ds_read_b128", FRAG[f_slot].sl(4 * j, 4), KXM[2 * s2 + j], SLOT * kslot + 4096 * mb)
+            for j in range(2)]
+
+
+def ksw_reads(kslot):
+    """The scale words of the lane's key rows krow and krow + 32 in ring slot
+    kslot (the tile's 64 words follow its 8 KB of codes)."""
+    return [DSR("ds_read_b32", KSWT[j], INV["ksr"], SLOT * kslot + 8192 + 128 * j) for j in range(2)]
+
+
+def ksw_perm():
+    """KSW byte 2 mb + s2 = scale byte 2 s2 + h of key row krow + 32 mb."""
+    return V("v_perm_b32", KSW, KSWT[1], KSWT[0], INV["psel"])
+
+
 def v_frag_reads(f_slot, kk, ob, vslot):
     """V^T fragment (O^T block ob, P^T k-step kk) of the tile in ring slot
     vslot: two ds_read_b64_tr_b16."""
@@ -610,11 +712,11 @@ def rsrc_base(r, head, size_s):
             S("s_mov_b32", r[3], RSRC3)]
 
 
-def rsrc_step(r):
-    """Resource r moved on by one tile: base + SLOT, size - SLOT (at least 0).
+def rsrc_step(r, step=SLOT):
+    """Resource r moved on by one tile: base + step, size - step (at least 0).
     The carry pair is one bundle, so no SCC writer lands between."""
-    return [[S("s_add_u32", r[0], r[0], SLOT), S("s_addc_u32", r[1], r[1], 0)],
-            [S("s_sub_i32", r[2], r[2], SLOT)], [S("s_max_i32", r[2], r[2], 0)]]
+    return [[S("s_add_u32", r[0], r[0], step), S("s_addc_u32", r[1], r[1], 0)],
+            [S("s_sub_i32", r[2], r[2], step)], [S("s_max_i32", r[2], r[2], 0)]]
 
 
 class VOp:
@@ -699,14 +801,21 @@ def softmax_exp_program(sm, p, masked, causal, kk_release, first_sum_init=True, 
             fmas.append(sm.add(ins, deps))
         for e in range(8):
             exps.append(sm.add(V("v_exp_f32", tb[e], tb[e], trans=True), [(fmas[e], 1)]))
+        unp = {}
         for q in range(4):
             op = sm.add(V("v_cvt_pk_bf16_f32", PB[kk][nb][q], tb[2 * q], tb[2 * q + 1]),
                         [(exps[2 * q], TRANS_FWD), (exps[2 * q + 1], TRANS_FWD)], nb_gap=kk_release[kk])
             last_read[(g, 2 * q)] = last_read[(g, 2 * q + 1)] = op
+            if MX:
+                # the sums take the weights as rounded for PV (the pair back
+                # to fp32 in the temporaries), so a tile's dominant weight
+                # cancels in O / l
+                unp[2 * q] = sm.add(V("v_lshlrev_b32", tb[2 * q], 16, PB[kk][nb][q]), [(op, 1)])
+                unp[2 * q + 1] = sm.add(V("v_and_b32", tb[2 * q + 1], MASKHI, PB[kk][nb][q]), [(op, 1)])
         for e in range(8):
             acc = PSUM[nb][e % 2]
             init = first_sum_init and kk == 0 and e < 2
-            deps = [(exps[e], TRANS_FWD), (last_read[(g, e)], 1)]
+            deps = [(exps[e], TRANS_FWD), (last_read[(g, e)], 1)] + ([(unp[e], 1)] if MX else [])
             if (nb, e % 2) in last_sum:
                 deps.append((last_sum[(nb, e % 2)], 1))
             op = sm.add(V("v_add_f32", acc, 0 if init else acc, tb[e]), deps)
@@ -727,7 +836,8 @@ class Block:
             self.out.append(x)
 
 
-def schedule_iteration(blk, mfmas, reads, pre_reads, side, sm_ops, budget=30, end_ops=(), fixed=None):
+def schedule_iteration(blk, mfmas, reads, pre_reads, side, sm_ops, budget=30, end_ops=(), fixed=None,
+                       read_gaps=None):
     """Emit one iteration: `mfmas` a list of (Ins, frag index or None); `reads`
     dict frag -> list of Ins, issued at gap 2(f - LOOK) (f >= LOOK) or before
     the first MFMA (f < LOOK, unless in `pre_reads`, already in flight); `side` dict
@@ -739,6 +849,8 @@ def schedule_iteration(blk, mfmas, reads, pre_reads, side, sm_ops, budget=30, en
         if f in pre_reads:
             continue
         gap = 2 * (f - LOOK) if f >= LOOK else -1
+        if read_gaps and f in read_gaps:
+            gap = read_gaps[f]
         gap_reads.setdefault(min(gap, nm - 1), []).extend(lst)
     # LDS op bookkeeping for lgkmcnt: list of frag ids per emitted LDS op
     lds_log = list(pre_reads_log_for(pre_reads, reads))
@@ -898,6 +1010,7 @@ def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
 
     for g in range(-1, nm):
         used = 0
+        cap_g = cap if not isinstance(cap, list) else cap[max(g, 0)]
         # LDS and vector-memory bundles lead the gap: issued behind VALU work
         # (a transcendental in particular) they hold up the next MFMA
         # (measured on gfx950: +2.3 cycles per MFMA for an LDS read at the end
@@ -910,7 +1023,7 @@ def slot_schedule(mfmas, items, pre_log, cap=7, tail=()):
                     break
                 forced = [it for it in cands if it.hi is not None and it.hi <= g]
                 pick = min(forced or cands, key=lambda it: (it.hi if it.hi is not None else 10 ** 6, it.seq))
-                if not forced and used + pick.size > cap:
+                if not forced and used + pick.size > cap_g:
                     break
                 place(pick)
                 used += pick.size
@@ -995,7 +1108,7 @@ def pre_reads_log_for(pre_reads, reads):
 class Gen:
     def __init__(self, causal):
         self.causal = causal
-        self.tag = "C" if causal else "F"
+        self.tag = ("M" if MX else "") + ("C" if causal else "F")
         self.prog = []
         self.nlab = 0
 
@@ -1025,6 +1138,11 @@ class Gen:
         1 KB together); RK and RV move on to tiles i+5 and i+3 after their last
         load. 8 groups, one load each."""
         sl = self.slots(u)
+        if MX:
+            groups = [([m0, NOP(0)] if m0 is not None else []) + [ld] for m0, ld in self.mx_loads(u)]
+            for r, step, j in self.mx_steps():
+                groups[j] += [x for b in rsrc_step(r, step) for x in b]
+            return groups
         groups = []
         for r, base in ((RK, SLOT * sl["kld"]), (RV, LDS_V + SLOT * sl["vld"])):
             for j in range(4):
@@ -1036,6 +1154,59 @@ class Gen:
 
     def barrier(self, vm):
         return [WAIT(vm=vm), BAR()]
+
+    def mx_loads(self, u):
+        """MX: the 7 LDS-DMA loads of iteration i (u = i mod 4) as (M0 write or
+        None, load): K tile i+4's codes (this wave's 16 rows of 128 bytes as
+        2 x 1 KB), its 64 scale words (every wave loads all of them, to the
+        same place), then V tile i+2 as in the bf16 walk."""
+        sl = self.slots(u)
+        kb = SLOT * sl["kld"]
+        vb = LDS_V + SLOT * sl["vld"]
+        return [(S("s_add_u32", M0, WOFFK, kb), BLOAD_LDS(INV["kl0"], RK)),
+                (None, BLOAD_LDS(INV["kl1"], RK, 1024)),
+                (S("s_add_u32", M0, LDSB, kb + 8192), BLOAD_LDS_DW(INV["sl"], RKS)),
+                (S("s_add_u32", M0, WOFF, vb), BLOAD_LDS(INV["loff0"], RV))] + [
+                (None, BLOAD_LDS(INV[f"loff{j}"], RV, 1024 * j)) for j in range(1, 4)]
+
+    @staticmethod
+    def mx_steps():
+        """MX: (resource, step, index of its last load) of the ring loads."""
+        return [(RK, KTILE, 1), (RKS, 256, 2), (RV, SLOT, 6)]
+
+    @staticmethod
+    def caps(mf, cap):
+        """Issue slots per gap: the gap after a 16-pass MX QK MFMA (64 cycles)
+        holds twice the gap after an 8-pass one."""
+        if not MX:
+            return cap
+        return [2 * cap if "scale" in ins.text else cap for ins, _ in mf]
+
+    @staticmethod
+    def pre_lo(nf, j):
+        """First gap for the prefetch of the next iteration's fragment j (slot
+        j): a gap after the MFMAs of this iteration's last fragment in that slot, and
+        no more than LOOK fragments ahead."""
+        lo = -1
+        for jj in range(j + 1):          # not before the fragments ahead of it (reads stay in order)
+            prev = [f for f in range(nf) if f % NSLOT == jj % NSLOT]
+            lo = max(lo, 2 * prev[-1] + 2 if prev else -1, 2 * (nf + jj - LOOK))
+        return lo
+
+    def prefetch_items(self, nf, nm, u):
+        """[(fragment, first gap, reads)] of the prefetch; one placed after the
+        last MFMA (which may read its slot) starts with a wait state."""
+        out = []
+        for j, (f, lst) in enumerate(sorted(self.v_prefetch(nf, u).items())):
+            lo = self.pre_lo(nf, j)
+            out.append((f, lo, ([NOP(0)] if nm and lo >= nm else []) + lst))
+        return out
+
+    @staticmethod
+    def pre_log():
+        """Fragments of the LDS reads the previous iteration's prefetch left in
+        flight, in issue order."""
+        return ([0, 0] if MX else []) + [f for f in range(LOOK) for _ in range(2)]
 
     def mfma_lists(self, pv, qk_par, u):
         """MFMA list [(Ins, frag)] and frag reads {frag: [Ins]} of iteration
@@ -1049,9 +1220,19 @@ class Gen:
                     slot = f % NSLOT
                     reads[f] = v_frag_reads(slot, kk, ob, sl["vpv"])
                     for nb in range(2):
-                        mf.append((MFMA(OACC[ob][nb], FRAG[slot], PB[kk][nb], OACC[ob][nb]), f))
+                        mf.append((MFMA(OACC[ob][nb], FRAG[slot].sl(0, 4), PB[kk][nb], OACC[ob][nb]), f))
                     f += 1
-        if qk_par is not None:
+        if qk_par is not None and MX:
+            for s2 in range(2):
+                for mb in range(2):
+                    slot = f % NSLOT
+                    reads[f] = k_frag_reads_mx(slot, s2, mb, sl["krd"])
+                    for nb in range(2):
+                        dst = SACC[qk_par][mb][nb]
+                        mf.append((MFMA_SCALE(dst, FRAG[slot], QA_MX[nb][s2], None if s2 == 0 else dst, KSW, QSC,
+                                              2 * mb + s2, 2 * nb + s2), f))
+                    f += 1
+        elif qk_par is not None:
             for ks in range(8):
                 for mb in range(2):
                     slot = f % NSLOT
@@ -1067,9 +1248,13 @@ class Gen:
 
     # the V(i) fragments 0..LOOK-1 read at the end of an iteration for the next PV
     def v_prefetch(self, nf, u):
+        """(MX: first the scale words of K tile i + 2, whose QK is the next
+        iteration's, counted with its first fragment.)"""
         reads = {}
         for j in range(LOOK):
-            lst = v_frag_reads((nf + j) % NSLOT, j // 4, j % 4, self.slots(u)["vpre"])
+            lst = v_frag_reads(j % NSLOT, j // 4, j % 4, self.slots(u)["vpre"])
+            if MX and j == 0:
+                lst = ksw_reads((u + 2) % 4) + lst
             for x in lst:
                 x.frag = nf + j
             reads[nf + j] = lst
@@ -1078,21 +1263,31 @@ class Gen:
     def mfma_iteration(self, name, u, pv, qk_par, sm, prefetch, side_extra=None, budget=30, end_ops=(), fixed=None):
         mf, reads, nf = self.mfma_lists(pv, qk_par, u)
         pre = set(range(LOOK)) if pv else set()
+        assert not (MX and pv)
+        read_gaps = None
         if prefetch:
-            reads.update(self.v_prefetch(nf, u))
+            if MX:
+                pre_it = self.prefetch_items(nf, len(mf), u)
+                reads.update({f: lst for f, _, lst in pre_it})
+                read_gaps = {f: lo for f, lo, _ in pre_it}
+            else:
+                reads.update(self.v_prefetch(nf, u))
         side = {}
+        if MX and qk_par is not None:
+            # the scale bytes of this iteration's QK (no prefetch before it)
+            side[-1] = ksw_reads(self.slots(u)["krd"]) + [WAIT(lgkm=0), ksw_perm()]
         nm = len(mf)
         # loads spread over the stream
         loads = self.load_groups(u)
         for j, grp in enumerate(loads):
-            gap = (j * nm) // 8 + 1 if nm else -1
+            gap = (j * nm) // len(loads) + 1 if nm else -1
             side.setdefault(min(gap, nm - 1) if nm else -1, []).extend(grp)
         if side_extra:
             for g, lst in side_extra.items():
                 side.setdefault(g, []).extend(lst)
         blk = Block()
         schedule_iteration(blk, mf, reads, pre, side, sm.ops if sm else [], budget=budget, end_ops=end_ops,
-                           fixed=fixed)
+                           fixed=fixed, read_gaps=read_gaps)
         return blk.out
 
     # ------------------------------------------------------------ softmax programs
@@ -1251,8 +1446,28 @@ class Gen:
             items.append(it)
             return it
         sl = self.slots(u)
-        prev, last = None, {}
-        for j in range(8):
+        ksw_item = None
+        if MX and qk_par is not None:
+            # the scale bytes of this iteration's QK (no prefetch before it)
+            assert not pv
+            ksw_item = add(ksw_reads(sl["krd"]) + [WAIT(lgkm=0), ksw_perm()] + NOPS(VALU_TO_MFMA), -1, -1)
+        if MX:
+            prev, lasts = None, []
+            for j, (m0, ld) in enumerate(self.mx_loads(u)):
+                at = (j * nm) // NLD_IT
+                deps = [(prev, 0)] if prev else []
+                if m0 is not None:
+                    m = add(m0, at - 1 if nm else -1, at if nm else None, deps)
+                    deps = deps + [(m, M0_WS)]
+                prev = add(ld, at + 1 if nm else -1, None, deps)
+                lasts.append(prev)
+            for r, step, j in self.mx_steps():
+                dep = lasts[j]
+                for b in rsrc_step(r, step):
+                    dep = add(b, -1, None, [(dep, 0)])
+        if not MX:
+            prev, last = None, {}
+        for j in range(8 if not MX else 0):
             r = RK if j < 4 else RV
             at = (j * nm) // 8
             deps = [(prev, 0)] if prev else []
@@ -1262,7 +1477,7 @@ class Gen:
                 deps = deps + [(m, M0_WS)]
             prev = add(BLOAD_LDS(INV[f"loff{j % 4}"], r, 1024 * (j % 4)), at + 1 if nm else -1, None, deps)
             last[r.i] = prev
-        for r in (RK, RV):
+        for r in (RK, RV) if not MX else ():
             dep = last[r.i]
             for b in rsrc_step(r):
                 dep = add(b, -1, None, [(dep, 0)])
@@ -1278,12 +1493,12 @@ class Gen:
             if xor:                            # KX for this ks, after the last read of the old one
                 xitem = add(xor, max(lo - 2, -1), max(2 * f - 6, -1) if nm else None,
                             [(fitem[f - 1], 0)] if f - 1 in fitem else [])
-            if ("v", KX.i) in lds[0].uses:
+            if not MX and ("v", KX.i) in lds[0].uses:
                 deps.append((xitem, 0))
             fitem[f] = add(lds, lo, hi, deps)
         if prefetch:
-            for f, lst in sorted(self.v_prefetch(nf, u).items()):
-                add(lst, max(2 * (f - NSLOT) + 1, 2 * (f - LOOK), -1) if nm else -1, None)
+            for f, lo, lst in self.prefetch_items(nf, nm, u):
+                add(lst, lo if nm else -1, None, [(ksw_item, 0)] if ksw_item else [])
         # side ops (gap -1's before the VALU program, which may read them)
         first_side = None
         for g, lst in sorted((side or {}).items()):
@@ -1297,8 +1512,8 @@ class Gen:
             for op in sm.ops:
                 deps = [(conv[id(d)], dist) for d, dist in op.deps] + ([(first_side, 0)] if first_side else [])
                 conv[id(op)] = add(op.ins, op.nb_gap if nm else -1, None, deps)
-        pre_log = [f for f in range(LOOK) for _ in range(2)] if pv else []
-        return slot_schedule(mf, items, pre_log, cap=OTHER_CAP[kind], tail=list(end_ops))
+        pre_log = self.pre_log() if pv else []
+        return slot_schedule(mf, items, pre_log, cap=self.caps(mf, OTHER_CAP[kind]), tail=list(end_ops))
 
     # ------------------------------------------------------------ iteration variants
     def it_fill(self):
@@ -1329,6 +1544,8 @@ class Gen:
         """1 <= i <= wt-2 (u = i mod 4): PV(i-1), QK(i+1) into SACC[1-p],
         softmax(i) of SACC[p] (p = u % 2) and the loads of K tile i+4 and V
         tile i+2, placed by slot_schedule."""
+        if MX:
+            return self.it_steady_mx(u)
         p = u % 2
         sl = self.slots(u)
         mf, reads, nf = self.mfma_lists(True, 1 - p, u)
@@ -1431,8 +1648,99 @@ class Gen:
         add([S("s_or_b64", CMPA, CMPA, CMPB), CBR("s_cbranch_scc1", self.L(f"redo_s{p}")),
              V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]), V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
              LABEL(self.L(f"ret_s{u}"))], 0, len(mf) - 2, [(c0, VALU_SGPR_VMEM), (c1, VALU_SGPR_VMEM)])
-        pre_log = [f for f in range(LOOK) for _ in range(2)]
-        return slot_schedule(mf, items, pre_log, cap=GAP_CAP)
+        pre_log = self.pre_log()
+        return slot_schedule(mf, items, pre_log, cap=self.caps(mf, GAP_CAP))
+
+    def it_steady_mx(self, u):
+        """MX steady iteration: 32 PV MFMAs (8 passes), then 8 QK MFMAs (16
+        passes) whose gaps hold twice the slots; the softmax spreads over gaps
+        0..STEADY_SPAN; the scale bytes of QK(i+1) are assembled from the
+        words the previous iteration's prefetch read."""
+        p = u % 2
+        mf, reads, nf = self.mfma_lists(True, 1 - p, u)
+        nm = len(mf)
+        nqk = sum(1 for ins, _ in mf if "scale" in ins.text)
+        items = []
+
+        def add(ins, lo=-1, hi=None, deps=()):
+            it = Item(ins, lo, hi, deps)
+            items.append(it)
+            return it
+
+        # the barrier as in the bf16 walk (after vmcnt(NLD_IT): the loads of
+        # i-2 and older have landed)
+        bar = add([WAIT(vm=NLD_IT), BAR()], 0, 0)
+        # KSW for QK(i+1), before its first MFMA (VALU -> MFMA wait states)
+        perm = add(ksw_perm(), 0, nm - nqk - 2)
+        # loads spread over gaps 1..nm-3, K codes, K scales, then V (the
+        # barrier's vmcnt assumes this order); M0 written in the gap before
+        prev, lasts = bar, []
+        lds_loads = self.mx_loads(u)
+        for j, (m0, ld) in enumerate(lds_loads):
+            at = (j * (nm - 4)) // len(lds_loads)
+            deps = [(prev, 0)]
+            if m0 is not None:
+                m = add(m0, max(at - 1, 0), at, deps)
+                deps = deps + [(m, M0_WS)]
+            prev = add(ld, at + 1, nm - 3, deps)
+            lasts.append(prev)
+        for r, step, j in self.mx_steps():
+            dep = lasts[j]
+            for b in rsrc_step(r, step):
+                dep = add(b, -1, None, [(dep, 0)])
+        # fragment reads (one AGPR ring for V^T and K fragments)
+        for f in range(LOOK, nf):
+            add(reads[f], max(2 * (f - NSLOT) + 1, 2 * (f - LOOK)), 2 * f - 5)
+        # prefetch of V(i) fragments 0..LOOK-1 and K(i+2)'s scale words
+        for j, (f, lo, lst) in enumerate(self.prefetch_items(nf, nm, u)):
+            add(lst, lo, None, [(bar, 0)] + ([(perm, 0)] if j == 0 else []))
+        # softmax of tile i (as the bf16 steady iteration, over 0..STEADY_SPAN)
+        rel = [8 * kk + 7 for kk in range(4)]
+        tmp = [v(160 + j) for j in range(24)]
+        fma, exp, adds, cvt = {}, {}, {}, {}
+        for e in range(64):
+            pos = (e * STEADY_SPAN) // 63
+            g = e // 8
+            kk, nb = g // 2, g % 2
+            srcr = SACC[p][kk // 2][nb][8 * (kk % 2) + e % 8]
+            t = tmp[e % 24]
+            x = V("v_fma_f32", t, srcr, SCALE, "-" + str(MSUB[nb]))
+            x.uses.append(("v", MSUB[nb].i))
+            deps = []
+            if e >= 24:
+                deps += [(adds[e - 24], 0), (cvt[(e - 24) // 2], 0)]
+            fma[e] = add(x, max(0, pos - 3), pos + 1, deps)
+            exp[e] = add(V("v_exp_f32", t, t, trans=True), pos, pos + 2, [(fma[e], 0)])
+            if e % 2 == 0:
+                continue
+            # the pair packed for PV, back to fp32 as rounded, into the sums
+            # (so a tile's dominant weight cancels in O / l)
+            i = e // 2
+            lo = max(pos + 1, rel[kk])
+            w = PB[kk][nb][(e % 8) // 2]
+            cvt[i] = add(V("v_cvt_pk_bf16_f32", w, tmp[(e - 1) % 24], t),
+                         lo, min(lo + 6, nm - 2), [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
+            unp = [add(V("v_lshlrev_b32", tmp[(e - 1) % 24], 16, w), lo, min(lo + 8, nm - 2), [(cvt[i], 0)]),
+                   add(V("v_and_b32", t, MASKHI, w), lo, min(lo + 8, nm - 2), [(cvt[i], 0)])]
+            for ee, un in ((e - 1, unp[0]), (e, unp[1])):
+                acc = PSUM[nb][ee % 2]
+                init = kk == 0 and ee % 8 < 2
+                deps = [(un, 0)]
+                if not init:
+                    prev_same = max(j for j in adds if (j // 8) % 2 == nb and j % 2 == ee % 2)
+                    deps.append((adds[prev_same], 0))
+                adds[ee] = add(V("v_add_f32", acc, 0 if init else acc, tmp[ee % 24]), lo, min(lo + 10, nm - 2),
+                               deps)
+        last0 = [adds[e] for e in range(64) if (e // 8) % 2 == 0]
+        last1 = [adds[e] for e in range(64) if (e // 8) % 2 == 1]
+        s0 = add(V("v_add_f32", PSUM[0][0], PSUM[0][0], PSUM[0][1]), 0, None, [(a_, 0) for a_ in last0])
+        c0 = add(V("v_cmp_nle_f32", CMPA, PSUM[0][0], BOUND), 0, None, [(s0, 0)])
+        s1 = add(V("v_add_f32", PSUM[1][0], PSUM[1][0], PSUM[1][1]), 0, None, [(a_, 0) for a_ in last1])
+        c1 = add(V("v_cmp_nle_f32", CMPB, PSUM[1][0], BOUND), 0, None, [(s1, 0)])
+        add([S("s_or_b64", CMPA, CMPA, CMPB), CBR("s_cbranch_scc1", self.L(f"redo_s{p}")),
+             V("v_add_f32", LRUN[0], LRUN[0], PSUM[0][0]), V("v_add_f32", LRUN[1], LRUN[1], PSUM[1][0]),
+             LABEL(self.L(f"ret_s{u}"))], 0, None, [(c0, VALU_SGPR_VMEM), (c1, VALU_SGPR_VMEM)])
+        return slot_schedule(mf, items, self.pre_log(), cap=self.caps(mf, GAP_CAP))
 
     def it_last(self, u):
         """i = wt-1 >= 1 (u = i mod 4): PV(i-1), masked softmax(i) of SACC[u % 2]."""
@@ -1456,7 +1764,22 @@ class Gen:
 
     def it_idle(self):
         """An iteration with no tile of this wave's walk: its share of the loads
-        only, slots and resources from ITER."""
+        only, slots and resources from ITER (MX: the resources step on from the
+        iteration before, as in every other iteration)."""
+        if MX:
+            t1, t2 = T[1], T[2]
+            out = [S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14), S("s_add_u32", SKLD, t1, WOFFK),
+                   S("s_add_u32", T[5], t1, LDSB), S("s_add_u32", T[5], T[5], 8192),
+                   S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
+                   S("s_add_u32", SVLD, t2, WOFF), S("s_add_u32", SVLD, SVLD, LDS_V)]
+            dst = {0: SKLD, 2: T[5], 3: SVLD}
+            for j, (m0, ld) in enumerate(self.mx_loads(0)):
+                if m0 is not None:
+                    out += [S("s_mov_b32", M0, dst[j]), NOP(0)]
+                out.append(ld)
+            for r, step, _ in self.mx_steps():
+                out += [x for b in rsrc_step(r, step) for x in b]
+            return out
         t1, t2, t3 = T[1], T[2], T[3]
         out = [S("s_and_b32", t1, ITER, 3), S("s_lshl_b32", t1, t1, 14), S("s_add_u32", SKLD, t1, WOFF),
                S("s_add_i32", t2, ITER, 2), S("s_and_b32", t2, t2, 3), S("s_lshl_b32", t2, t2, 14),
@@ -1483,7 +1806,14 @@ class Gen:
         LT = [SCR[2], SCR[3]]
         X = SCR[4]
         out += NOPS(MFMA_WS + 4)
-        for nb in range(2):
+        for nb in range(2 if MX else 0):
+            # MX: no LSE output
+            out += [V("v_mov_b32", X, LRUN[nb])] + NOPS(PERM_WS) + [
+                V("v_permlane32_swap_b32", LRUN[nb], X, perm=True)] + NOPS(PERM_WS) + [
+                V("v_add_f32", LT[nb], LRUN[nb], X),
+                V("v_rcp_f32", INVL[nb], LT[nb], trans=True), NOP(1),
+                V("v_cmp_lt_f32", VCC, 0, LT[nb]), NOP(1), V("v_cndmask_b32", INVL[nb], 0, INVL[nb], VCC)]
+        for nb in range(2 if not MX else 0):
             out += [V("v_mov_b32", X, LRUN[nb])] + NOPS(PERM_WS) + [
                 V("v_permlane32_swap_b32", LRUN[nb], X, perm=True)] + NOPS(PERM_WS) + [
                 V("v_add_f32", LT[nb], LRUN[nb], X),
@@ -1501,7 +1831,15 @@ class Gen:
         out += [S("s_mov_b32", OQW, QW0)] + [S("s_mov_b32", ORO[j], RO[j]) for j in range(4)]
         return out
 
-    def output_o(self, bundles=()):
+    def output_o_any(self, tag):
+        """output_o; MX: bf16 or fp16 by OUTF16."""
+        if not MX:
+            return self.output_o()[0]
+        L = lambda n: self.L(f"{n}_{tag}")
+        return ([S("s_cmp_eq_u32", OUTF16, 0), CBR("s_cbranch_scc0", L("o16"))] + self.output_o()[0] +
+                [BR(L("odone")), LABEL(L("o16"))] + self.output_o(f16=True)[0] + [LABEL(L("odone"))])
+
+    def output_o(self, bundles=(), f16=False):
         """O / l through the wave's LDS staging area to global memory
         (16 buffer_store_dwordx4), from ORO, OQW and INVL; `bundles` (the next
         tile's prologue loads) go one per 4-row block. Returns the program and
@@ -1527,7 +1865,8 @@ class Gen:
                     V("v_add_u32", VO[k], T[3], INV["stl"])]
         for ps in range(2):
             dst = [v(128 + 4 * k, 4) for k in range(8)] if ps == 0 else \
-                  [TMP[0].sl(0, 4), TMP[0].sl(4, 4), FRAG[0], FRAG[1], FRAG[2], FRAG[3], SCR.sl(8, 4), SCR.sl(12, 4)]
+                  [TMP[0].sl(0, 4), TMP[0].sl(4, 4)] + [FRAG[k].sl(0, 4) for k in range(4)] + [
+                   SCR.sl(8, 4), SCR.sl(12, 4)]
             for j in range(2):
                 ob = 2 * ps + j
                 for nb in range(2):
@@ -1541,7 +1880,8 @@ class Gen:
                         o = OACC[ob][nb]
                         out += [ACCR(t[e], o[4 * aa + e]) for e in range(4)]
                         out += [V("v_mul_f32", t[e], INVL[nb], t[e]) for e in range(4)]
-                        out += [V("v_cvt_pk_bf16_f32", t[0], t[0], t[1]), V("v_cvt_pk_bf16_f32", t[1], t[2], t[3])]
+                        cvt = "v_cvt_pk_f16_f32" if f16 else "v_cvt_pk_bf16_f32"
+                        out += [V(cvt, t[0], t[0], t[1]), V(cvt, t[1], t[2], t[3])]
                         c = 4 * j + aa
                         out += [DSW("ds_write_b64", WA[c], Reg(t[0].f, t[0].i, 2), 4096 * nb)]
             out += [WAIT(lgkm=0)]
@@ -1559,6 +1899,8 @@ class Gen:
     def setup_loads(self):
         """Registers of the query tile (BH, QT) and its prologue loads: K(0),
         Q, K(1), K(2), V(0) (32 vector-memory operations)."""
+        if MX:
+            return self.setup_loads_mx()
         L = self.L
         out = []
         t = T
@@ -1599,6 +1941,79 @@ class Gen:
                 V("v_add_u32", QOFF[1], 0x2000, QOFF[0])]
         return out
 
+    def setup_loads_mx(self):
+        """MX: the registers of query tile (BH, QT) (no GQA: the K and V head
+        is BH): K codes and Q codes 128 bytes per row, V and O 256, K scale
+        words 4 (RKS's base; its size is set with K(0)'s loads)."""
+        t = T
+        out = [S("s_lshl_b32", t[3], SEQ, 8), S("s_lshl_b32", t[6], SEQ, 7)]
+        out += [S("s_mul_i32", t[4], BH, t[6]), S("s_mul_hi_u32", t[5], BH, t[6]),
+                S("s_add_u32", KH[0], KP[0], t[4]), S("s_addc_u32", KH[1], KP[1], t[5]),
+                S("s_add_u32", RQ[0], QP[0], t[4]), S("s_addc_u32", RQ[1], QP[1], t[5]),
+                S("s_and_b32", RQ[1], RQ[1], 0xFFFF), S("s_mov_b32", RQ[2], t[6]), S("s_mov_b32", RQ[3], RSRC3)]
+        out += [S("s_mul_i32", t[4], BH, t[3]), S("s_mul_hi_u32", t[5], BH, t[3]),
+                S("s_add_u32", VH[0], VP[0], t[4]), S("s_addc_u32", VH[1], VP[1], t[5]),
+                S("s_add_u32", RO[0], OP[0], t[4]), S("s_addc_u32", RO[1], OP[1], t[5]),
+                S("s_and_b32", RO[1], RO[1], 0xFFFF), S("s_mov_b32", RO[2], t[3]), S("s_mov_b32", RO[3], RSRC3)]
+        out += [S("s_lshl_b32", t[6], SEQ, 2), S("s_mul_i32", t[4], BH, t[6]), S("s_mul_hi_u32", t[5], BH, t[6]),
+                S("s_add_u32", RKS[0], KSP[0], t[4]), S("s_addc_u32", RKS[1], KSP[1], t[5]),
+                S("s_and_b32", RKS[1], RKS[1], 0xFFFF), S("s_mov_b32", RKS[3], RSRC3)]
+        # q0, kv_end, tiles, this wave's first row and walk length (as bf16)
+        out += [S("s_lshl_b32", Q0, QT, 8), S("s_sub_i32", Q0, Q0, QSHIFT)]
+        if self.causal:
+            out += [S("s_add_i32", KVEND, Q0, 256), S("s_min_i32", KVEND, KVEND, SEQ)]
+        else:
+            out += [S("s_mov_b32", KVEND, SEQ)]
+        out += [S("s_add_i32", NT, KVEND, 63), S("s_ashr_i32", NT, NT, 6), S("s_lshl_b32", KVB, KVEND, 8),
+                S("s_lshl_b32", t[0], WAVE, 6), S("s_add_i32", QW0, Q0, t[0])]
+        if self.causal:
+            out += [S("s_ashr_i32", t[0], QW0, 6), S("s_add_i32", t[0], t[0], 1), S("s_min_i32", t[0], t[0], NT),
+                    S("s_cmp_ge_i32", QW0, 0), S("s_cselect_b32", WT, t[0], 0)]
+        else:
+            out += [S("s_cmp_ge_i32", QW0, 0), S("s_cselect_b32", WT, NT, 0)]
+        return out + self.q_offsets_mx(QW0)
+
+    def q_offsets_mx(self, qw):
+        """MX: QOFF (codes) and QSO (scale words) of the lane's rows qw + l32
+        and qw + 32 + l32 of head BH. The scale rows are clamped into [0, S)
+        (a global load has no range check; the codes of rows outside read as
+        zeros, so their products are zero)."""
+        t = T
+        return [S("s_lshl_b32", t[0], qw, 7), V("v_add_u32", QOFF[0], t[0], INV["qlane"]),
+                V("v_add_u32", QOFF[1], 0x1000, QOFF[0]),
+                V("v_lshrrev_b32", QSO[0], 7, INV["qlane"]), V("v_add_u32", QSO[0], qw, QSO[0]),
+                V("v_add_u32", QSO[1], 32, QSO[0]), S("s_sub_i32", t[1], SEQ, 1),
+                V("v_med3_i32", QSO[0], QSO[0], 0, t[1]), V("v_med3_i32", QSO[1], QSO[1], 0, t[1]),
+                S("s_mul_i32", t[2], BH, SEQ),
+                V("v_add_u32", QSO[0], t[2], QSO[0]), V("v_add_u32", QSO[1], t[2], QSO[1]),
+                V("v_lshlrev_b32", QSO[0], 2, QSO[0]), V("v_lshlrev_b32", QSO[1], 2, QSO[1])]
+
+    def prologue_loads_mx(self, with_q=True):
+        """MX prologue bundles, each ending in one load: K(0) (codes, scale
+        words), Q (unless the previous walk loaded it), K(1), K(2), V(0); RK,
+        RKS and RV end at the first iteration's tiles (K 3, V 1)."""
+        def flat(bl):
+            return [x for b in bl for x in b]
+
+        def bundles(lds, pre):
+            return [(pre if j == 0 else []) + ([m0, NOP(0)] if m0 is not None else []) + [ld]
+                    for j, (m0, ld) in enumerate(lds)]
+        k0 = [S("s_mov_b32", RK[0], KH[0]), S("s_and_b32", RK[1], KH[1], 0xFFFF), S("s_lshl_b32", RK[2], KVEND, 7),
+              S("s_max_i32", RK[2], RK[2], 0), S("s_mov_b32", RK[3], RSRC3),
+              S("s_lshl_b32", RKS[2], KVEND, 2), S("s_max_i32", RKS[2], RKS[2], 0)]
+        step = flat(rsrc_step(RK, KTILE)) + flat(rsrc_step(RKS, 256))
+        b = bundles(self.mx_loads(0)[:3], k0)
+        if with_q:
+            b += self.q_loads()
+            assert len(b) == self.N_EARLY_MX
+        for tl in (1, 2):
+            b += bundles(self.mx_loads(tl)[:3], step)
+        b += bundles(self.mx_loads(2)[3:], step + rsrc_base(RV, VH, KVB))
+        b[-1] += flat(rsrc_step(RV))
+        return b
+
+    N_EARLY_MX = 13
+
     # the prologue loads of K(0) and Q are the first N_EARLY bundles
     N_EARLY = 20
 
@@ -1606,6 +2021,9 @@ class Gen:
         """The query tile's prologue loads as bundles, each ending in one
         load: K(0), Q (unless the previous walk loaded it), K(1), K(2), V(0);
         the last leaves RK, RV at the first iteration's tiles (K 3, V 1)."""
+        if MX:
+            return self.prologue_loads_mx(with_q)
+
         def flat(bl):
             return [x for b in bl for x in b]
 
@@ -1623,12 +2041,23 @@ class Gen:
         return b
 
     def q_loads(self):
-        """The 16 loads of this wave's 64 Q rows into QA (from RQ, QOFF)."""
+        """The 16 loads of this wave's 64 Q rows into QA (from RQ, QOFF); MX:
+        8 loads of codes into QA_MX, then the rows' 2 scale words."""
+        if MX:
+            return [[BLOAD("buffer_load_dwordx4", QA_MX[nb][s2].sl(4 * j, 4), QOFF[nb], RQ, 64 * s2 + 32 * j)]
+                    for nb in range(2) for s2 in range(2) for j in range(2)] + [
+                    [GLOAD("global_load_dword", QSW[nb], QSO[nb], QSP)] for nb in range(2)]
         return [[BLOAD("buffer_load_dwordx4", QA[nb][ks], QOFF[nb], RQ, 32 * ks)] for nb in range(2) for ks in range(8)]
 
     def q_address(self):
-        """RQ and QOFF of query tile (BH, QT) for this wave's rows."""
+        """RQ and QOFF of query tile (BH, QT) for this wave's rows (MX: and QSO)."""
         t = T
+        if MX:
+            return [S("s_lshl_b32", t[3], SEQ, 7), S("s_mul_i32", t[4], BH, t[3]), S("s_mul_hi_u32", t[5], BH, t[3]),
+                    S("s_add_u32", RQ[0], QP[0], t[4]), S("s_addc_u32", RQ[1], QP[1], t[5]),
+                    S("s_and_b32", RQ[1], RQ[1], 0xFFFF), S("s_mov_b32", RQ[2], t[3]), S("s_mov_b32", RQ[3], RSRC3),
+                    S("s_lshl_b32", t[3], QT, 8), S("s_sub_i32", t[3], t[3], QSHIFT), S("s_lshl_b32", t[4], WAVE, 6),
+                    S("s_add_i32", t[3], t[3], t[4])] + self.q_offsets_mx(t[3])
         return [S("s_lshl_b32", t[3], SEQ, 8), S("s_mul_i32", t[4], BH, t[3]), S("s_mul_hi_u32", t[5], BH, t[3]),
                 S("s_add_u32", RQ[0], QP[0], t[4]), S("s_addc_u32", RQ[1], QP[1], t[5]),
                 S("s_and_b32", RQ[1], RQ[1], 0xFFFF), S("s_mov_b32", RQ[2], t[3]), S("s_mov_b32", RQ[3], RSRC3),
@@ -1659,10 +2088,13 @@ class Gen:
         K(0) and Q have landed, and the barrier after them has passed)."""
         L = self.L
         out = [S("s_mov_b32", ITER, -1)]
+        if MX:
+            # the tile's Q scale bytes (its Q landed before the walk's barrier)
+            out = [V("v_perm_b32", QSC, QSW[1], QSW[0], INV["psel"])] + out
         out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("idle_m1"))]
         out += self.it_fill()
         out += [BR(L("it0")), LABEL(L("idle_m1"))] + self.it_idle()
-        out += [LABEL(L("it0")), S("s_mov_b32", ITER, 0)] + self.barrier(8)
+        out += [LABEL(L("it0")), S("s_mov_b32", ITER, 0)] + self.barrier(NLD_IT)
         out += [S("s_cmp_ge_i32", WT, 2), CBR("s_cbranch_scc1", L("first")),
                 S("s_cmp_eq_u32", WT, 1), CBR("s_cbranch_scc1", L("first_last"))]
         out += self.it_idle() + [BR(L("it1"))]
@@ -1684,14 +2116,14 @@ class Gen:
             else:
                 out += [CBR("s_cbranch_scc0", L(f"last{(u + 1) % 4}"))]
         for u in range(4):
-            out += [LABEL(L(f"last{u}"))] + self.barrier(8) + self.it_last(u)
+            out += [LABEL(L(f"last{u}"))] + self.barrier(NLD_IT) + self.it_last(u)
             out += [S("s_add_i32", ITER, ITER, 1), BR(L(f"drain{(u + 1) % 4}"))]
         for u in range(4):
             # the last iteration's 8 ring loads and 16 Q loads may be in flight
-            out += [LABEL(L(f"drain{u}"))] + self.barrier(8 + 16) + self.it_drain(u)
+            out += [LABEL(L(f"drain{u}"))] + self.barrier(NLD_IT + NLD_Q) + self.it_drain(u)
             out += [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("idle_chk")), S("s_cmp_le_i32", ITER, NT), CBR("s_cbranch_scc0", L("walk_end"))]
-        out += self.barrier(8) + self.it_idle() + [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
+        out += self.barrier(NLD_IT) + self.it_idle() + [S("s_add_i32", ITER, ITER, 1), BR(L("idle_chk"))]
         out += [LABEL(L("walk_end"))] + [WAIT(vm=0, lgkm=0), BAR()]
         return out
 
@@ -1746,6 +2178,12 @@ class Gen:
                V("v_add_u32", VA[0][0], LDS_V, VA[0][0]), V("v_add_u32", VA[0][1], LDS_V, VA[0][1])] + [
                V("v_xor_b32", VA[ob][j], 64 * ob, VA[0][j]) for ob in range(1, 4) for j in range(2)] + [
                WAIT(lgkm=0)]
+        if MX:
+            # after the argument loads (WOFFK takes HKV's slot): this wave's K
+            # code rows of a slot, the K read bases of chunk pairs 1..3
+            out += [S("s_lshl_b32", WOFFK, INS_["wv"], 11), S("s_add_u32", WOFFK, WOFFK, INS_["lb"]),
+                    S("s_mov_b32", MASKHI, 0xFFFF0000)] + [
+                V("v_xor_b32", KXM[cp], 32 * cp, KA) for cp in range(1, 4)]
         t = T
         # A tile's walk, then its LSE; the next tile's setup and prologue
         # loads go out before this tile's O is written, so the loads land
@@ -1753,7 +2191,7 @@ class Gen:
         out += [S("s_cmp_ge_u32", ITEMV, NWORK), CBR("s_cbranch_scc1", L("end"))]
         loads = [x for b in self.prologue_loads() for x in b]
         out += self.decode("d0") + [S("s_mov_b32", PASS, 0)] + self.select() + self.setup_loads() + loads
-        out += self.barrier(12) + [BR(L("walk"))]
+        out += self.barrier(NLD_PRO) + [BR(L("walk"))]
         out += [LABEL(L("walk"))] + self.next_tile() + self.walk()
         out += [S("s_mov_b32", OQW, -1), S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("lse_done"))]
         out += self.output_lse() + [LABEL(L("lse_done"))]
@@ -1764,11 +2202,11 @@ class Gen:
         # this wave had rows, so its last iteration loaded the next Q: K(0),
         # K(1), K(2), V(0), then the output's 16 stores; the barrier waits for
         # K(0) (the 12 loads and 16 stores after it may be in flight)
-        out += [x for b in self.prologue_loads(False) for x in b] + self.output_o()[0]
-        out += self.barrier(12 + 16) + [BR(L("walk"))]
-        out += [LABEL(L("no_out"))] + loads + self.barrier(12) + [BR(L("walk"))]
+        out += [x for b in self.prologue_loads(False) for x in b] + self.output_o_any("a")
+        out += self.barrier(NLD_PRO + 16) + [BR(L("walk"))]
+        out += [LABEL(L("no_out"))] + loads + self.barrier(NLD_PRO) + [BR(L("walk"))]
         out += [LABEL(L("final")), S("s_cmp_lt_i32", OQW, 0), CBR("s_cbranch_scc1", L("end"))]
-        out += self.output_o()[0] + [BR(L("end"))]
+        out += self.output_o_any("b") + [BR(L("end"))]
         out += self.redo_blocks()
         out += [LABEL(L("end")), WAIT(vm=0, lgkm=0)]
         self.prog = out
@@ -1814,7 +2252,7 @@ def to_macro(name, prog):
 
 
 def clobbers():
-    regs = [f'"v{i}"' for i in range(N_VGPR_OWN)] + [f'"a{i}"' for i in range(256)]
+    regs = [f'"v{i}"' for i in range(N_VGPR_OWN) if i not in CLOB_SKIP_V] + [f'"a{i}"' for i in range(256)]
     regs += [f'"s{i}"' for i in range(N_SGPR_OWN) if i not in (32, 33)]
     regs += ['"vcc"', '"scc"', '"memory"']
     return ", ".join(regs)
@@ -1827,7 +2265,13 @@ def stats(prog):
 
 
 def main(argv):
-    out_path = argv[1] if len(argv) > 1 else None
+    """gen_prefill_w64.py [--mx] OUT.inc: the bf16 bodies (CA_PFW64_*) or, with
+    --mx, the MXFP8 ones (CA_PFW64MX_*)."""
+    mx = "--mx" in argv[1:]
+    args = [x for x in argv[1:] if x != "--mx"]
+    out_path = args[0] if args else None
+    configure(mx)
+    pre = "CA_PFW64MX_" if mx else "CA_PFW64_"
     text = ["// Generated by gen_prefill_w64.py: the 64-row prefill kernel bodies. Do not edit.",
             "#pragma once", ""]
     for causal in (True, False):
@@ -1835,10 +2279,10 @@ def main(argv):
         prog = g.kernel()
         check(prog, g.tag)
         check_scc(prog, g.tag)
-        text.append(to_macro("CA_PFW64_BODY_" + ("CAUSAL" if causal else "FULL"), prog))
+        text.append(to_macro(pre + "BODY_" + ("CAUSAL" if causal else "FULL"), prog))
         print(f"variant {g.tag}: {len(prog)} lines {stats(prog)}", file=sys.stderr)
-    text.append("#define CA_PFW64_CLOBBERS " + clobbers())
-    text.append(f"#define CA_PFW64_IN_V {len(IN_V)}")
+    text.append(f"#define {pre}CLOBBERS " + clobbers())
+    text.append(f"#define {pre}IN_V {len(IN_V)}")
     src = "\n".join(text) + "\n"
     if out_path:
         with open(out_path, "w") as f:

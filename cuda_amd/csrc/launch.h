@@ -35,6 +35,20 @@ bool prefill_w64_supported(int D, int S, float scale, bool rope);
 hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void* o, float* lse, int B,
                               int Hq, int Hkv, int S, float scale, bool causal, hipStream_t stream);
 void magic_div(uint32_t d, uint32_t* m, uint32_t* sh);
+// Work decomposition of the 64-row kernels (grid 0: nothing to launch).
+struct PfW64Geom {
+  long long grid;
+  int n_qt, n_work, paired, q_shift, n_bh, n_full, half;
+  uint32_t m_nqt, sh_nqt, m_half, sh_half;
+  int xcd_q, xcd_r;
+};
+hipError_t w64_geometry(int B, int Hq, int S, bool causal, PfW64Geom* g);
+// The MXFP8 form (prefill_w64_mx.hip): e4m3 Q, K with e8m0 scales [rows][4],
+// bf16 V, bf16 (out_f16 false) or fp16 output; the conditions of
+// prefill_w64_supported. launch_prefill_mx dispatches to it when they hold.
+hipError_t launch_prefill_w64_mx(bool out_f16, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
+                                 const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
+                                 float scale, bool causal, hipStream_t stream);
 
 // float32 prefill (f32.hip)
 hipError_t launch_prefill_f32(const void* q, const void* k, const void* v, void* o, float* lse,

@@ -145,19 +145,36 @@ bool prefill_w64_supported(int D, int S, float scale, bool rope) {
   return D == 128 && !rope && sl2 >= 0.f && sl2 <= 3.0e38f && S > 0 && S < (1 << 22);
 }
 
-hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void* o, float* lse, int B,
-                              int Hq, int Hkv, int S, float scale, bool causal, hipStream_t stream) {
+hipError_t w64_geometry(int B, int Hq, int S, bool causal, PfW64Geom* g) {
   constexpr int kRows = 256, kBN = 64;
+  *g = PfW64Geom{};
   const int n_qt = (S + kRows - 1) / kRows;
   // padding rows of a ragged S go before row 0, in whole key tiles, so every
   // wave's causal diagonal is its last key tile
-  const int q_shift = (n_qt * kRows - S) / kBN * kBN;
-  int paired = 0;
-  const long long n_work = prefill_grid(B, Hq, n_qt, causal, 1, &paired);
+  g->q_shift = (n_qt * kRows - S) / kBN * kBN;
+  const long long n_work = prefill_grid(B, Hq, n_qt, causal, 1, &g->paired);
   if (n_work == 0) return hipSuccess;
   if (n_work > 0x7fffffffLL || (long long)B * Hq > 0x7fffffffLL) return hipErrorInvalidValue;
   const long long slots = device_cus() / 8 * 8;
-  const long long grid = ((!causal || paired) && slots > 0 && n_work > slots) ? slots : n_work;
+  g->grid = ((!causal || g->paired) && slots > 0 && n_work > slots) ? slots : n_work;
+  g->n_qt = n_qt;
+  g->n_work = (int)n_work;
+  g->n_bh = B * Hq;
+  g->half = n_qt >> 1;
+  g->n_full = g->n_bh * g->half;
+  magic_div((uint32_t)n_qt, &g->m_nqt, &g->sh_nqt);
+  magic_div((uint32_t)(g->half > 0 ? g->half : 1), &g->m_half, &g->sh_half);
+  g->xcd_q = (int)(n_work / 8);
+  g->xcd_r = (int)(n_work % 8);
+  return hipSuccess;
+}
+
+hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                              int Hq, int Hkv, int S, float scale, bool causal, hipStream_t stream) {
+  PfW64Geom g;
+  const hipError_t ge = w64_geometry(B, Hq, S, causal, &g);
+  if (ge != hipSuccess || g.grid == 0) return ge;
+  const long long grid = g.grid;
   PfW64Args a{};
   a.q = q;
   a.k = k;
@@ -165,22 +182,24 @@ hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void*
   a.o = o;
   a.lse = lse;
   a.S = S;
-  a.n_qt = n_qt;
-  a.n_work = (int)n_work;
-  a.paired = paired;
-  a.q_shift = q_shift;
+  a.n_qt = g.n_qt;
+  a.n_work = g.n_work;
+  a.paired = g.paired;
+  a.q_shift = g.q_shift;
   a.scale_log2 = scale * kLog2e;
-  a.n_bh = B * Hq;
-  a.half = n_qt >> 1;
-  a.n_full = a.n_bh * a.half;
+  a.n_bh = g.n_bh;
+  a.half = g.half;
+  a.n_full = g.n_full;
   a.hq = Hq;
   a.hkv = Hkv;
-  magic_div((uint32_t)n_qt, &a.m_nqt, &a.sh_nqt);
-  magic_div((uint32_t)(a.half > 0 ? a.half : 1), &a.m_half, &a.sh_half);
+  a.m_nqt = g.m_nqt;
+  a.sh_nqt = g.sh_nqt;
+  a.m_half = g.m_half;
+  a.sh_half = g.sh_half;
   magic_div((uint32_t)Hq, &a.m_hq, &a.sh_hq);
   magic_div((uint32_t)(Hq / Hkv), &a.m_ratio, &a.sh_ratio);
-  a.xcd_q = (int)(n_work / 8);
-  a.xcd_r = (int)(n_work % 8);
+  a.xcd_q = g.xcd_q;
+  a.xcd_r = g.xcd_r;
   if (causal) {
     hipLaunchKernelGGL(prefill_w64_kernel<true>, dim3((unsigned)grid), dim3(kW64Threads), 0, stream, a);
   } else {
