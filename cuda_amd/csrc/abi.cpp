@@ -357,8 +357,8 @@ ca_status ca_fused_microscaled_attention(ca_dtype out_dtype, const uint8_t* q, c
   const uintptr_t scale_align = scale_kind == CA_SCALE_F32 ? 4u : 1u;
   if ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(v_scale)) & (scale_align - 1))
     return fail(CA_INVALID_ARGUMENT, "%s: float scales must be 4-byte aligned", what);
-  if ((reinterpret_cast<uintptr_t>(k_scale) & 3u) != 0)
-    return fail(CA_INVALID_ARGUMENT, "%s: k_scale must be 4-byte aligned", what);
+  if (((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale)) & 3u) != 0)
+    return fail(CA_INVALID_ARGUMENT, "%s: q_scale and k_scale must be 4-byte aligned", what);
   ca_status st;
   if ((st = check_sizes(batch, num_heads, seq_len, head_dim, what)) != CA_OK) return st;
   const size_t need = ca::mx_workspace_bytes((int)scale_kind, batch, num_heads, seq_len, head_dim);

@@ -626,7 +626,7 @@ def configure(mx):
     RKS = s(52, 4)             # K scale resource, stepped like RK
     QSP = s(8, 2)              # Q scale words (LP's slot)
     KSP = [s(27), s(28)]       # K scale words (MRATIO, SHRATIO's slots)
-    OUTF16 = s(25)             # output element type: 0 bf16, 1 fp16 (MHQ's slot)
+    OUTF16 = s(25)             # flags (MHQ's slot): bit 0 fp16 output (else bf16), bit 1 negate Q
     MASKHI = s(26)             # 0xffff0000: the high bf16 of a packed pair as fp32 (SHHQ's slot)
     WOFFK = s(20)              # LDS base + 2 KB x wave: this wave's K rows of a slot (HKV's slot)
 
@@ -1718,10 +1718,12 @@ class Gen:
             i = e // 2
             lo = max(pos + 1, rel[kk])
             w = PB[kk][nb][(e % 8) // 2]
+            def dl(x):       # a deadline; past the MFMA stream: the tail
+                return x if x <= nm - 2 else None
             cvt[i] = add(V("v_cvt_pk_bf16_f32", w, tmp[(e - 1) % 24], t),
-                         lo, min(lo + 6, nm - 2), [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
-            unp = [add(V("v_lshlrev_b32", tmp[(e - 1) % 24], 16, w), lo, min(lo + 8, nm - 2), [(cvt[i], 0)]),
-                   add(V("v_and_b32", t, MASKHI, w), lo, min(lo + 8, nm - 2), [(cvt[i], 0)])]
+                         lo, dl(lo + 6), [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
+            unp = [add(V("v_lshlrev_b32", tmp[(e - 1) % 24], 16, w), lo, dl(lo + 8), [(cvt[i], 0)]),
+                   add(V("v_and_b32", t, MASKHI, w), lo, dl(lo + 8), [(cvt[i], 0)])]
             for ee, un in ((e - 1, unp[0]), (e, unp[1])):
                 acc = PSUM[nb][ee % 2]
                 init = kk == 0 and ee % 8 < 2
@@ -1729,8 +1731,7 @@ class Gen:
                 if not init:
                     prev_same = max(j for j in adds if (j // 8) % 2 == nb and j % 2 == ee % 2)
                     deps.append((adds[prev_same], 0))
-                adds[ee] = add(V("v_add_f32", acc, 0 if init else acc, tmp[ee % 24]), lo, min(lo + 10, nm - 2),
-                               deps)
+                adds[ee] = add(V("v_add_f32", acc, 0 if init else acc, tmp[ee % 24]), lo, dl(lo + 10), deps)
         last0 = [adds[e] for e in range(64) if (e // 8) % 2 == 0]
         last1 = [adds[e] for e in range(64) if (e // 8) % 2 == 1]
         s0 = add(V("v_add_f32", PSUM[0][0], PSUM[0][0], PSUM[0][1]), 0, None, [(a_, 0) for a_ in last0])
@@ -1836,7 +1837,7 @@ class Gen:
         if not MX:
             return self.output_o()[0]
         L = lambda n: self.L(f"{n}_{tag}")
-        return ([S("s_cmp_eq_u32", OUTF16, 0), CBR("s_cbranch_scc0", L("o16"))] + self.output_o()[0] +
+        return ([S("s_bitcmp1_b32", OUTF16, 0), CBR("s_cbranch_scc1", L("o16"))] + self.output_o()[0] +
                 [BR(L("odone")), LABEL(L("o16"))] + self.output_o(f16=True)[0] + [LABEL(L("odone"))])
 
     def output_o(self, bundles=(), f16=False):
@@ -2089,8 +2090,17 @@ class Gen:
         L = self.L
         out = [S("s_mov_b32", ITER, -1)]
         if MX:
-            # the tile's Q scale bytes (its Q landed before the walk's barrier)
-            out = [V("v_perm_b32", QSC, QSW[1], QSW[0], INV["psel"])] + out
+            # the tile's Q scale bytes (its Q landed before the walk's barrier);
+            # for a negative softmax scale (flag bit 1, the kernel then takes
+            # |scale|) the Q codes' signs flip: softmax(c Q K^T) with c < 0 is
+            # softmax(|c| (-Q) K^T)
+            t = TMP[0]
+            flip = []
+            for j in range(32):
+                flip += [ACCR(t[j % 8], a(128 + j)), V("v_xor_b32", t[j % 8], 0x80808080, t[j % 8]),
+                         ACCW(a(128 + j), t[j % 8])]
+            out = [V("v_perm_b32", QSC, QSW[1], QSW[0], INV["psel"]), S("s_bitcmp1_b32", OUTF16, 1),
+                   CBR("s_cbranch_scc0", L("pos"))] + flip + NOPS(VALU_TO_MFMA) + [LABEL(L("pos"))] + out
         out += [S("s_cmp_ge_i32", WT, 1), CBR("s_cbranch_scc0", L("idle_m1"))]
         out += self.it_fill()
         out += [BR(L("it0")), LABEL(L("idle_m1"))] + self.it_idle()

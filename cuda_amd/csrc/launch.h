@@ -44,8 +44,8 @@ struct PfW64Geom {
 };
 hipError_t w64_geometry(int B, int Hq, int S, bool causal, PfW64Geom* g);
 // The MXFP8 form (prefill_w64_mx.hip): e4m3 Q, K with e8m0 scales [rows][4],
-// bf16 V, bf16 (out_f16 false) or fp16 output; the conditions of
-// prefill_w64_supported. launch_prefill_mx dispatches to it when they hold.
+// bf16 V, bf16 (out_f16 false) or fp16 output; any finite softmax scale,
+// S < 2^22 and B * H * S < 2^30 (else hipErrorInvalidValue).
 hipError_t launch_prefill_w64_mx(bool out_f16, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                                  const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
                                  float scale, bool causal, hipStream_t stream);
@@ -171,10 +171,5 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
 // the three float scale arrays is not a power of two in [2^-127, 2^127].
 hipError_t check_mx_scales(const float* qs, const float* ks, const float* vs, long long n, bool* bad,
                            hipStream_t stream);
-// The MX prefill kernel (prefill.hip): e4m3 q, k with e8m0 scale bytes
-// qs, ks ([B, H, S, 4]) and the bf16 dequantised v; D = 128.
-hipError_t launch_prefill_mx(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
-                             const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
-                             float scale, bool causal, hipStream_t stream);
 
 }  // namespace ca

@@ -16,9 +16,12 @@
 //     are not meaningful (NaN, or 0 for a row whose logits are all NaN); the
 //     call stays asynchronous, and check_mx_scales (a separate, synchronous
 //     entry) reports such scales;
-//   the prefill kernel with MX operands (prefill.hip): QK on
+//   the 64-row prefill kernel with MX operands (prefill_w64_mx.hip): QK on
 //   v_mfma_scale_f32_32x32x64_f8f6f4 with the e8m0 bytes as per-lane scales,
 //   softmax and PV (bf16 MFMA on the dequantised V) as in the bf16 kernel.
+//   Limits: a finite softmax scale (a negative one is applied to -Q), S below
+//   2^22 and B * H * S below 2^30 rows; otherwise the call fails before
+//   launching anything.
 #include <algorithm>
 
 #include "common.h"
@@ -151,9 +154,12 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
                         const uint8_t* k, const void* ks, const uint8_t* v, const void* vs, void* o,
                         int B, int H, int S, int D, float scale, bool causal, void* ws,
                         size_t ws_bytes, hipStream_t stream) {
-  if (D != 128) return hipErrorInvalidValue;
+  if (D != 128 || (out_dtype != kDtypeBF16 && out_dtype != kDtypeF16)) return hipErrorInvalidValue;
   const long long rows = (long long)B * H * S;
   if (rows == 0) return hipSuccess;
+  // the attention kernel's limits (checked before the prepare launch)
+  if (!prefill_w64_supported(128, S, scale < 0.f ? -scale : scale, false) || rows >= (1LL << 30))
+    return hipErrorInvalidValue;
   if (ws_bytes < mx_workspace_bytes(scale_kind, B, H, S, D)) return hipErrorInvalidValue;
   unsigned char* w = (unsigned char*)ws;
   uint16_t* vb = (uint16_t*)w;
@@ -177,7 +183,7 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  return launch_prefill_mx(out_dtype, q, qs8, k, ks8, vb, o, B, H, S, scale, causal, stream);
+  return launch_prefill_w64_mx(out_dtype == kDtypeF16, q, qs8, k, ks8, vb, o, B, H, S, scale, causal, stream);
 }
 
 }  // namespace ca

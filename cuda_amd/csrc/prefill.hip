@@ -983,23 +983,6 @@ static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v
   return launch_prefill_kernel<Tr, Tr, D, CAUSAL, false>(a, B, Hq, Hkv, S, scale, stream, rq);
 }
 
-hipError_t launch_prefill_mx(int out_dtype, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
-                             const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
-                             float scale, bool causal, hipStream_t stream) {
-  if ((out_dtype == kDtypeBF16 || out_dtype == kDtypeF16) && prefill_w64_supported(128, S, scale, false) &&
-      (long long)B * H * S * 4 <= 0xffffffffLL)
-    return launch_prefill_w64_mx(out_dtype == kDtypeF16, q, qs, k, ks, v_bf16, o, B, H, S, scale, causal, stream);
-  const PfArgs a{q, k, qs, ks, v_bf16, o, nullptr};
-#define CA_PF_MX(OUT)                                                                           \
-  return causal ? launch_prefill_kernel<BF16, OUT, 128, true, true>(a, B, H, H, S, scale, stream,  \
-                                                                    RopeQ{})                   \
-                : launch_prefill_kernel<BF16, OUT, 128, false, true>(a, B, H, H, S, scale, stream, \
-                                                                     RopeQ{});
-  if (out_dtype == kDtypeBF16) { CA_PF_MX(BF16) }
-  if (out_dtype == kDtypeF16) { CA_PF_MX(F16) }
-#undef CA_PF_MX
-  return hipErrorInvalidValue;
-}
 
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                           int B, int Hq, int Hkv, int S, int D, float scale, bool causal,

@@ -7,7 +7,8 @@
 // reference declares without a kernel; semantics as mxfp8.hip states): Q and
 // K are OCP e4m3 codes with one e8m0 scale byte per 32 elements along D
 // ([rows][4]), V the exact bf16 dequantisation (mx_prepare_kernel), the
-// output bf16 or fp16; softmax scales >= 0 (prefill.hip serves the others).
+// output bf16 or fp16. A negative softmax scale c runs as |c| on -Q (the
+// codes' sign bits flipped in registers at the start of each query tile).
 //
 // QK runs on v_mfma_scale_f32_32x32x64_f8f6f4 (16 passes): per 64-d k-step
 // s2, lane half h supplies d = 64 s2 + 16 h + [0, 16) in bytes 0-15 and
@@ -44,13 +45,13 @@ struct PfW64MxArgs {
   float scale_log2;
   int n_bh, n_full, half, hq, unused0;
   uint32_t m_nqt, sh_nqt, m_half, sh_half;
-  uint32_t out_f16, unused1, ks_lo, ks_hi;
+  uint32_t flags, unused1, ks_lo, ks_hi;  // flags: bit 0 fp16 output, bit 1 negate Q
   int xcd_q, xcd_r, pad;
 };
 static_assert(sizeof(PfW64MxArgs) == 128, "kernel argument block");
 static_assert(offsetof(PfW64MxArgs, qs) == 32 && offsetof(PfW64MxArgs, S) == 40 &&
                   offsetof(PfW64MxArgs, scale_log2) == 60 && offsetof(PfW64MxArgs, m_nqt) == 84 &&
-                  offsetof(PfW64MxArgs, out_f16) == 100 && offsetof(PfW64MxArgs, ks_lo) == 108 &&
+                  offsetof(PfW64MxArgs, flags) == 100 && offsetof(PfW64MxArgs, ks_lo) == 108 &&
                   offsetof(PfW64MxArgs, xcd_q) == 116,
               "offsets the kernel body loads");
 
@@ -122,11 +123,14 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_mx_kernel(PfW64MxArgs args
 hipError_t launch_prefill_w64_mx(bool out_f16, const uint8_t* q, const uint8_t* qs, const uint8_t* k,
                                  const uint8_t* ks, const uint16_t* v_bf16, void* o, int B, int H, int S,
                                  float scale, bool causal, hipStream_t stream) {
+  const bool neg = scale < 0.f;
+  if (neg) scale = -scale;
+  // the Q scale words are read at 32-bit offsets from qs
+  if (!prefill_w64_supported(128, S, scale, false) || (long long)B * H * S * 4 > 0xffffffffLL)
+    return hipErrorInvalidValue;
   PfW64Geom g;
   const hipError_t ge = w64_geometry(B, H, S, causal, &g);
   if (ge != hipSuccess || g.grid == 0) return ge;
-  // the Q scale words are read at 32-bit offsets from qs
-  if ((long long)B * H * S * 4 > 0xffffffffLL) return hipErrorInvalidValue;
   PfW64MxArgs a{};
   a.q = q;
   a.k = k;
@@ -147,7 +151,7 @@ hipError_t launch_prefill_w64_mx(bool out_f16, const uint8_t* q, const uint8_t* 
   a.sh_nqt = g.sh_nqt;
   a.m_half = g.m_half;
   a.sh_half = g.sh_half;
-  a.out_f16 = out_f16 ? 1u : 0u;
+  a.flags = (out_f16 ? 1u : 0u) | (neg ? 2u : 0u);
   a.ks_lo = (uint32_t)(uintptr_t)ks;
   a.ks_hi = (uint32_t)((uint64_t)(uintptr_t)ks >> 32);
   a.xcd_q = g.xcd_q;

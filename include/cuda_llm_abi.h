@@ -224,8 +224,10 @@ typedef enum CA_ENUM_INT { CA_SCALE_E8M0 = 0, CA_SCALE_F32 = 1 } ca_scale_kind;
  * head_dim] with one scale per 32 elements along head_dim ([batch, num_heads,
  * seq_len, head_dim / 32], in scale_kind's format); value = code * scale.
  * Output [batch, num_heads, seq_len, head_dim] in out_dtype (CA_BF16 or
- * CA_F16). head_dim must be 128. k_scale must be 4-byte aligned (with
- * CA_SCALE_F32 so must q_scale and v_scale). Replaces
+ * CA_F16). head_dim must be 128. q_scale and k_scale must be 4-byte aligned
+ * (with CA_SCALE_F32 so must v_scale). Limits: a finite softmax_scale, seq_len
+ * below 2^22 and batch * num_heads * seq_len below 2^30 (else
+ * CA_INVALID_ARGUMENT, before anything is launched). Replaces
  * dispatch_fused_microscaled_attention<T_OUT> (kernels_api.h:103-108).
  * workspace: ca_mx_workspace_bytes(...) (v dequantised to bf16; with float
  * scales also q's and k's converted scale bytes). Asynchronous in both scale

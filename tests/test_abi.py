@@ -196,9 +196,9 @@ def test_mxfp8_rejects_bad_arguments():
     assert L.load().ca_mx_workspace_bytes(7, 1, 2, 64, 128) == 0
 
     def mx(*over, **kw):
-        a = dict(dt=L.CA_BF16, kind=E8, d=128, ws=P, wsb=ws, ks=P)
+        a = dict(dt=L.CA_BF16, kind=E8, d=128, ws=P, wsb=ws, ks=P, qs=P)
         a.update(kw)
-        return _status("ca_fused_microscaled_attention", a["dt"], P, P, P, a["ks"], P, P, a["kind"],
+        return _status("ca_fused_microscaled_attention", a["dt"], P, a["qs"], P, a["ks"], P, P, a["kind"],
                        P, 1, 2, 64, a["d"], 0.1, 1, a["ws"], a["wsb"], None)
     assert mx(d=64) == L.CA_INVALID_ARGUMENT
     assert mx(dt=L.CA_F32) == L.CA_UNSUPPORTED
@@ -208,6 +208,8 @@ def test_mxfp8_rejects_bad_arguments():
     assert b"workspace" in L.load().ca_last_error()
     assert mx(kind=F32) == L.CA_INVALID_ARGUMENT  # the float form needs the larger workspace
     assert mx(ks=ctypes.c_void_p(18)) == L.CA_INVALID_ARGUMENT
+    assert b"aligned" in L.load().ca_last_error()
+    assert mx(qs=ctypes.c_void_p(17)) == L.CA_INVALID_ARGUMENT      # e8m0 q scales too: dword loads
     assert b"aligned" in L.load().ca_last_error()
 
 

@@ -114,6 +114,36 @@ def test_mx_zero_scale_is_running_mean(dev, causal):
     assert_close(to_np(out), ref.cpu().numpy(), **TOL_FP8, name=f"mx zero scale causal={causal}")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_mx_negative_scale(dev, causal, out_dtype):
+    """A negative softmax scale (the kernel takes |scale| on -Q, the codes'
+    signs flipped per query tile, so every tile of a multi-tile grid, the
+    first and the ones a walk's last iteration loads, is checked)."""
+    x = mx_inputs(2, 3, 700, 128, dev, seed=7)
+    out = _run(x, causal, softmax_scale=-0.06, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    d = _ref(x)
+    ref = oracle.attention(d["q"], d["k"], d["v"], is_causal=causal, scale=-0.06)
+    assert_close(to_np(out), ref, **TOL_FP8, name=f"mx scale -0.06 causal={causal}")
+
+
+def test_mx_limits_fail_before_launch(dev):
+    """seq_len >= 2^22 and a non-finite softmax scale are rejected with
+    CA_INVALID_ARGUMENT before anything is launched (dummy pointers, never
+    read)."""
+    import ctypes
+    from cuda_amd import _lib as L
+    P = ctypes.c_void_p(256)
+    lib = L.load()
+    for s, sc in ((1 << 22, 0.1), (64, float("inf")), (64, float("nan"))):
+        ws = lib.ca_mx_workspace_bytes(L.CA_SCALE_E8M0, 1, 1, s, 128)
+        st = lib.ca_fused_microscaled_attention(L.CA_BF16, P, P, P, P, P, P, L.CA_SCALE_E8M0, P, 1, 1, s, 128,
+                                                ctypes.c_float(sc), 1, P, ws, None)
+        assert st == L.CA_INVALID_ARGUMENT, (s, sc)
+    torch.cuda.synchronize()
+
+
 def test_mx_fp16_output(dev):
     x = mx_inputs(1, 2, 64, 128, dev, seed=4)
     out = _run(x, False, out_dtype=torch.float16)
