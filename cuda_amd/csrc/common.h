@@ -62,11 +62,6 @@ struct BF16 {
     r[1] = (__bf16)b;
     return r;
   }
-  // acc + p[0] + p[1] in fp32 (one v_dot2 with ones; exact products)
-  static __device__ __forceinline__ float sum2(vec2 p, float acc) {
-    const vec2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-    return __builtin_amdgcn_fdot2_f32_bf16(p, ones, acc, false);
-  }
   static __device__ __forceinline__ float to_float(uint16_t x) {
     return __uint_as_float(((uint32_t)x) << 16);
   }
@@ -98,11 +93,6 @@ struct F16 {
     r[0] = (_Float16)a;
     r[1] = (_Float16)b;
     return r;
-  }
-  static __device__ __forceinline__ float sum2(vec2 p, float acc) {
-    typedef __fp16 h2 __attribute__((ext_vector_type(2)));
-    const h2 ones = {(__fp16)1.0f, (__fp16)1.0f};
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, p), ones, acc, false);
   }
   static __device__ __forceinline__ float to_float(uint16_t x) {
     _Float16 h = __builtin_bit_cast(_Float16, x);

@@ -15,8 +15,8 @@
 //   tiles (8 at head dim 64) shared by the 8 waves; the two waves of a SIMD
 //   run the ping-pong walk (16-bit head dim 128: one waits at the per-tile
 //   barrier before its MFMA block, the other after it, so one's softmax runs
-//   under the other's MFMAs) or the lockstep walk (MX: one barrier per two
-//   tiles; head dim 64: per four).
+//   under the other's MFMAs) or the lockstep walk (head dim 64: one barrier
+//   per four tiles).
 // Per wave and KV tile (32x32x16 MFMAs):
 //   S^T[64 keys x 32 q] = K Q^T   (A = K rows from LDS, B = Q from registers)
 //   softmax over keys: keys live in the registers of a lane (16 per 32-key
@@ -118,7 +118,7 @@ constexpr int kPfVDepth = 2;   // V^T fragments read ahead of the PV MFMAs (step
 // Key tiles per workgroup barrier of the lockstep walk: one barrier every
 // two tiles lets a SIMD's two waves drift apart within the pair instead of
 // meeting after every PV (+1.5 % over one barrier per tile on the 16-bit
-// walk then in use, +3 % on MX, same box). Head dim 64, whose 16 KB tiles
+// walk then in use). Head dim 64, whose 16 KB tiles
 // let the ring hold eight, takes a barrier every four (+1.7 to +2.4 % on
 // the reference grid's fp16 shapes).
 constexpr int kPfGroup = 2;
@@ -154,55 +154,36 @@ struct PfItem {
 // other waves may still read the ring, and the caller puts a barrier before
 // the next item.
 //
-// MX (MXFP8 attention, D = 128): Q and K are OCP e4m3 codes with one e8m0
-// scale byte per 32 elements along D (QS, KS: [rows][4]); V is its exact
-// bf16 dequantisation (written by mx_prepare_kernel), so PV and the softmax
-// are those of the bf16 kernel. QK contracts over D, the axis the MX blocks
-// run along, so it runs on v_mfma_scale_f32_32x32x64_f8f6f4: each MFMA covers
-// 64 d (two MX blocks) and takes one e8m0 byte per lane. Hardware k-block 0
-// of that instruction is bytes 0-15 of both lane halves and k-block 1 bytes
-// 16-31, with the scale of k-block b read from lane half b; so lane half h
-// supplies d = 64s + 16h + [0,16) in bytes 0-15 and d = 64s + 32 + 16h +
-// [0,16) in bytes 16-31 of k-step s, and the scale of MX block 2s + h. Both
-// operands (K rows from LDS, Q rows from registers) use that assignment, so
-// every fp8 product meets its own two scales. The K tile is 64 rows of 128
-// code bytes (the swizzle of 128-byte rows), followed in the ring stage by
-// the V tile and the tile's 64 scale words (4 bytes per key).
-template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
-__device__ CA_INLINE bool prefill_dma_qtile(
-    const void* __restrict__ Qv, const void* __restrict__ Kv, const uint8_t* __restrict__ QS,
-    const uint8_t* __restrict__ KS, const uint16_t* __restrict__ V, void* __restrict__ Ov,
-    float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2, int bh, int qt, int q_shift,
-    RopeQ rq, PfItem nx, bool pre, int& g0, typename Tr::vec8 (&qv)[MX ? 1 : D / 16],
-    i32x8 (&qx)[2], int (&qsc)[2]) {
-  static_assert(!MX || (D == 128 && std::is_same<Tr, BF16>::value), "MX: D = 128, bf16 PV");
-  using Gv = PfGeom<D>;                   // V tile geometry (and K's for 16-bit K)
-  using Gk = PfGeom<MX ? 64 : D>;         // K tile geometry: 128-byte rows for MX codes
+template <typename Tr, int D, bool CAUSAL, bool POS>
+__device__ CA_INLINE bool prefill_dma_qtile(const void* __restrict__ Qv, const void* __restrict__ Kv,
+                                            const uint16_t* __restrict__ V, void* __restrict__ Ov,
+                                            float* __restrict__ Lse, int S, int Hq, int Hkv, float scale_log2,
+                                            int bh, int qt, int q_shift, RopeQ rq, PfItem nx, bool pre,
+                                            int& g0, typename Tr::vec8 (&qv)[D / 16]) {
+  using Gv = PfGeom<D>;                   // K and V tile geometry
+  using Gk = Gv;
   using vec8 = typename Tr::vec8;
-  using ovec4 = typename OutTr::vec4;
-  using ovec2 = typename OutTr::vec2;
+  using ovec4 = typename Tr::vec4;
+  using ovec2 = typename Tr::vec2;
   constexpr int kBN = Gv::kBN;
   constexpr int kKRowB = Gk::kRowB, kVRowB = Gv::kRowB;       // bytes per K / V row in LDS
   constexpr int kKTileB = kBN * kKRowB, kVTileB = kBN * kVRowB;
-  constexpr int kScaleB = MX ? kBN * 4 : 0;                   // K scale words of a tile
-  constexpr int kStageB = kKTileB + kVTileB + kScaleB;
+  constexpr int kStageB = kKTileB + kVTileB;
   constexpr int kNOB = Gv::kNOB;
   constexpr int kBM = kPfRows, kStages = pf_stages(D), kNW = kPfWaves;
   constexpr int kGroup = pf_group(D);
   constexpr int kKL = kKTileB / 1024 / kNW;  // 1 KB K loads per wave per tile
   constexpr int kVL = kVTileB / 1024 / kNW;  // 1 KB V loads per wave per tile
-  constexpr int kSL = MX ? 1 : 0;            // scale loads (every wave loads the same 256 B)
-  constexpr int kLoads = kKL + kVL + kSL;
+  constexpr int kLoads = kKL + kVL;
   static_assert(kKL >= 1 && kVL >= 1 && kKTileB % (1024 * kNW) == 0 && kVTileB % (1024 * kNW) == 0,
                 "tile loads");
   static_assert(kStageB % 256 == 0, "stage alignment (bank rows)");
-  // QK steps (MFMAs issued after one K fragment wait): bf16 k-steps of 16 d;
-  // MX (key block, k-step of 64 d) pairs
-  constexpr int kQkSteps = MX ? 4 : Gv::kNKS;
-  // The ping-pong walk (below) for 16-bit head dim 128: same-box C2 +6.6 %,
-  // C2' +4.9 %; at head dim 64 (-5 to -7 %) and MX (-5 %) the MFMA blocks
-  // are too short to hide the partner's softmax and the lockstep walk stays.
-  constexpr bool kPingPong = D == 128 && !MX;
+  // QK steps (MFMAs issued after one K fragment wait): k-steps of 16 d
+  constexpr int kQkSteps = Gv::kNKS;
+  // The ping-pong walk (below) for head dim 128: same-box C2 +6.6 %, C2'
+  // +4.9 %; at head dim 64 (-5 to -7 %) the MFMA blocks are too short to
+  // hide the partner's softmax and the lockstep walk stays.
+  constexpr bool kPingPong = D == 128;
   static_assert(kQkSteps % kLoads == 0, "loads spread over the QK steps");
   static_assert((kStages & (kStages - 1)) == 0, "ring slots: tile & (kStages - 1)");
 
@@ -211,7 +192,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   constexpr int kOStgB = 32 * 128;
   __shared__ __attribute__((aligned(16))) unsigned char ostg[kNW * kOStgB];
 
-  // the K (V, MX scale) rows of head bh's kv head
+  // the K (V) rows of head bh's kv head
   auto kv_rows = [&](int bx) CA_INLINE {
     const int hx = bx % Hq;
     return (size_t)((bx / Hq) * Hkv + hx / (Hq / Hkv)) * S;
@@ -220,7 +201,6 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   const size_t qhead = (size_t)bh * S, khead = kv_rows(bh);
   const unsigned char* Kp = (const unsigned char*)Kv + khead * kKRowB;
   const uint16_t* Vp = V + khead * D;
-  const uint8_t* KSp = MX ? KS + khead * 4 : nullptr;
 
   const int lane = __builtin_amdgcn_workitem_id_x() & 63;
   const int wave = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_workitem_id_x() >> 6);
@@ -229,47 +209,26 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   const int myq = qw0 + l32;
   const bool q_in = myq >= 0 && myq < S;
 
-  // Q as the B operand of S^T = K Q^T: qv, 16-bit Q, k-step ks: d = 16 ks +
-  // 8 hl + [0, 8); MX: qx codes of k-step s (layout above), qsc scale bytes
-  // of blocks 2s + hl. Loaded after the first K/V tiles' loads, so that
+  // Q as the B operand of S^T = K Q^T: qv, k-step ks: d = 16 ks + 8 hl +
+  // [0, 8). Loaded after the first K/V tiles' loads, so that
   // their latencies overlap: the lane's row of tile (bx, qtx), row 0 for
   // rows outside [0, S) ...
   auto load_q_raw = [&](int bx, int qtx) CA_INLINE {
     const int r = qtx * kBM - q_shift + wave * 32 + l32;
     const size_t row = (size_t)bx * S + ((r >= 0 && r < S) ? r : 0);
-    if constexpr (MX) {
-      const uint8_t* Qr = (const uint8_t*)Qv + row * D;
+    const uint16_t* Qr = (const uint16_t*)Qv + row * D;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const u32x4 lo = *(const u32x4*)(Qr + 64 * st + 16 * hl);
-        const u32x4 hi = *(const u32x4*)(Qr + 64 * st + 32 + 16 * hl);
-        qsc[st] = QS[row * 4 + 2 * st + hl];
-        qx[st] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                       (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      }
-    } else {
-      const uint16_t* Qr = (const uint16_t*)Qv + row * D;
-#pragma unroll
-      for (int ks = 0; ks < Gv::kNKS; ++ks) qv[ks] = *(const vec8*)(Qr + 16 * ks + 8 * hl);
-    }
+    for (int ks = 0; ks < Gv::kNKS; ++ks) qv[ks] = *(const vec8*)(Qr + 16 * ks + 8 * hl);
   };
-  // ... then zeroed (MX: codes 0, scale 2^0) outside [0, S) and rotated (RoPE).
+  // ... then zeroed outside [0, S) and rotated (RoPE).
   auto fix_q = [&]() CA_INLINE {
-    if constexpr (MX) {
+    if (!q_in) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        qsc[st] = q_in ? qsc[st] : 127;
-        if (!q_in) qx[st] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    } else {
-      if (!q_in) {
+      for (int ks = 0; ks < Gv::kNKS; ++ks)
 #pragma unroll
-        for (int ks = 0; ks < Gv::kNKS; ++ks)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
-      }
-      if (rq.cos && q_in) rope_q<Tr, D>(qv, rq, myq, hl);
+        for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
     }
+    if (rq.cos && q_in) rope_q<Tr, D>(qv, rq, myq, hl);
   };
 
   const int kv_end = CAUSAL ? min(S, q0 + kBM) : S;
@@ -303,7 +262,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     const int row = Gv::kRpk * (kVL * wave + i) + lane / Gv::kLpr;
     v_off[i] = row * kVRowB + 16 * ((lane % Gv::kLpr) ^ Gv::swz(row));
   }
-  // load j of tile tt: K loads, then V loads, then (MX) the scale words.
+  // load j of tile tt: K loads, then V loads.
   // Ring slot (g0 + tt) mod kStages; past this item's last tile, the next
   // item's tile tt - n_tiles when redirected (else rows past kv_end: zeros).
   auto issue_one = [&](int tt, int j) CA_INLINE {
@@ -314,13 +273,10 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     if (j < kKL) {
       dma16_buf(make_rsrc_at(o ? Kp_n : Kp, lt * kKTileB, end * kKRowB),
                 (CA_LDS void*)(st + 1024 * (kKL * wave + j)), k_off[j]);
-    } else if (j < kKL + kVL) {
+    } else {
       const int i = j - kKL;
       dma16_buf(make_rsrc_at(o ? Vp_n : Vp, lt * kVTileB, end * kVRowB),
                 (CA_LDS void*)(st + kKTileB + 1024 * (kVL * wave + i)), v_off[i]);
-    } else if constexpr (MX) {
-      dma4_buf(make_rsrc_at(KSp, lt * kScaleB, end * 4),  // never redirected (lockstep)
-               (CA_LDS void*)(st + kKTileB + kVTileB), 4 * lane);
     }
   };
   auto issue = [&](int tt) CA_INLINE {
@@ -329,8 +285,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   };
 
   // LDS read addresses (bytes from the stage base).
-  // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl
-  // (MX: chunks 4s + hl and 4s + 2 + hl, i.e. "ks" = 2s and 2s + 1).
+  // K: lane reads row krow (+32 per key block), logical chunk 2*ks + hl.
   const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
   const int fk = Gk::swz(krow);
   const uint32_t kofs = krow * kKRowB + 32 * (fk >> 1) + 16 * (hl ^ (fk & 1));  // ^ 32*ks
@@ -345,7 +300,6 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   const uint32_t vofs1 = kKTileB + tr_row * kVRowB + 64 * (fv >> 2) + 16 * (c0 ^ (fv & 3)) + 8 * (s16 & 1);
   const uint32_t vofs2 =
       kKTileB + (tr_row + 4) * kVRowB + 64 * (fv2 >> 2) + 16 * (c0 ^ (fv2 & 3)) + 8 * (s16 & 1);
-  const uint32_t sofs = kKTileB + kVTileB + 4 * krow;  // MX: the scale word of row krow
   const uint32_t lds0 = lds_off(lds);
   auto stage = [&](int tt) CA_INLINE {
     return lds0 + (uint32_t)(((g0 + tt) & (kStages - 1)) * kStageB);
@@ -363,11 +317,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   constexpr float kMaskVal = POS ? kNegInf : -kNegInf;  // raw logit whose scaled image is -inf
 
   // P for logit pair p (16 pairs: P^T k-step kk = p/4, logits 8kk + 2j, +1
-  // with j = p%4; sv[8kk + e] <-> P^T k-step kk); two partial row sums. MX
-  // sums the bf16-rounded weights that enter PV (one v_dot2 with ones per
-  // pair, exact in fp32), so the weights of a row sum to exactly 1: its
-  // wide-range data gives peaked rows, where normalising by the unrounded
-  // sum would leave the dominant key's rounding (2^-9 of |v|) in the output.
+  // with j = p%4; sv[8kk + e] <-> P^T k-step kk); two partial row sums.
   // On a masked tile a masked logit gets weight 0 directly: its exponent
   // kMaskVal * scale_log2 - msub is -inf for every nonzero scale, but NaN for
   // scale 0 (softmax_scale = 0: equal weights for the visible keys).
@@ -385,11 +335,8 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     const typename Tr::vec2 pk = Tr::pack2(p0, p1);
     pb[kk][2 * j] = pk[0];
     pb[kk][2 * j + 1] = pk[1];
-    // pairs 0 and 1 start the two chains (an add of 0.f is not folded away)
-    if constexpr (MX)
-      psum[j & 1] = Tr::sum2(pk, p < 2 ? 0.f : psum[j & 1]);
-    else
-      psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
+    // pairs 0 and 1 start the two chains
+    psum[j & 1] = p < 2 ? p0 + p1 : psum[j & 1] + (p0 + p1);
   };
   auto exp_all = [&](auto mask_tag) CA_INLINE {
 #pragma unroll
@@ -482,26 +429,13 @@ __device__ CA_INLINE bool prefill_dma_qtile(
       for (int r = 0; r < 16; ++r) sacc[mb][r] = 0.f;
     __builtin_amdgcn_s_setprio(1);
     const uint32_t ka = stage(tn) + kofs;
-    uint32_t ksw[2] = {0u, 0u};  // MX: the scale words of the lane's two key rows
-    if constexpr (MX) {
-      ksw[0] = lds_read_b32<0>(stage(tn) + sofs);
-      ksw[1] = lds_read_b32<128>(stage(tn) + sofs);
-    }
     constexpr int KD = kPfKDepth;
     u32x4 kr[KD + 1][2];
-    // step st's K fragment: bf16, k-step st of both key blocks; MX, key
-    // block st % 2, k-step st / 2, both 16-byte pieces
+    // step st's K fragment: k-step st of both key blocks
     auto kread = [&](int st) CA_INLINE {
-      if constexpr (MX) {
-        const int mb = st & 1, s2 = st >> 1;
-        const uint32_t an = ka + 32 * kKRowB * mb;
-        kr[st % (KD + 1)][0] = lds_read_b128<0>(an ^ (32 * (2 * s2)));
-        kr[st % (KD + 1)][1] = lds_read_b128<0>(an ^ (32 * (2 * s2 + 1)));
-      } else {
-        const uint32_t an = ka ^ (32 * st);
-        kr[st % (KD + 1)][0] = lds_read_b128<0>(an);
-        kr[st % (KD + 1)][1] = lds_read_b128<32 * kKRowB>(an);
-      }
+      const uint32_t an = ka ^ (32 * st);
+      kr[st % (KD + 1)][0] = lds_read_b128<0>(an);
+      kr[st % (KD + 1)][1] = lds_read_b128<32 * kKRowB>(an);
     };
 #pragma unroll
     for (int st = 0; st < KD; ++st) kread(st);
@@ -512,25 +446,11 @@ __device__ CA_INLINE bool prefill_dma_qtile(
       wait_lgkm_n(2 * (KD < kQkSteps - 1 - st ? KD : kQkSteps - 1 - st));  // step st landed
       after_wait(kr[cb][0]);
       after_wait(kr[cb][1]);
-      if constexpr (MX) {
-        if (st == 0) {
-          after_wait(ksw[0]);
-          after_wait(ksw[1]);
-        }
-        const int mb = st & 1, s2 = st >> 1;
-        const i32x8 a = {(int)kr[cb][0][0], (int)kr[cb][0][1], (int)kr[cb][0][2], (int)kr[cb][0][3],
-                         (int)kr[cb][1][0], (int)kr[cb][1][1], (int)kr[cb][1][2], (int)kr[cb][1][3]};
-        const int ksc = (ksw[mb] >> (8 * (2 * s2 + hl))) & 0xff;
-        sacc[mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qx[s2], sacc[mb], 0, 0, 0,
-                                                                  ksc, 0, qsc[s2]);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      } else {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb][mb]), qv[st], sacc[mb]);
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
-        }
+      for (int mb = 0; mb < 2; ++mb) {
+        sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, kr[cb][mb]), qv[st], sacc[mb]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // then up to 8 VALU
       }
       if (st % (kQkSteps / kLoads) == kQkSteps / kLoads - 1)
         issue_one(tn + kAhead, st / (kQkSteps / kLoads));
@@ -578,13 +498,13 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   // ---- MFMA block M(s) = PV(s-1) then QK(s) --------------------------------
   // One MFMA per step: PV steps (O^T block i / 4, P^T k-step i % 4; V^T
   // fragment = two tr16 reads) then QK steps (key block j % 2, k-step j / 2;
-  // K fragment = one b128 read, two for MX). Fragments stream kMD steps
+  // K fragment = one b128 read). Fragments stream kMD steps
   // ahead across the PV -> QK boundary, so a wave keeps the matrix pipe fed
   // on its own while its partner runs the softmax. The loads of tile s +
   // kAhead go out between the QK steps.
   constexpr int kNPV = 4 * kNOB;
-  constexpr int kNQK = MX ? 4 : 2 * Gv::kNKS;
-  constexpr int kRQK = MX ? 2 : 1;  // LDS reads per QK step
+  constexpr int kNQK = 2 * Gv::kNKS;
+  constexpr int kRQK = 1;           // LDS reads per QK step
   constexpr int kMD = 4;            // steps read ahead
   static_assert(kNQK % kLoads == 0, "loads spread over the QK steps");
   constexpr int kKK = 16 * kVRowB;  // bytes per P^T k-step of V rows
@@ -616,11 +536,6 @@ __device__ CA_INLINE bool prefill_dma_qtile(
     __builtin_amdgcn_s_setprio(1);
     const uint32_t va1 = stage(s + kStages - 1) + vofs1, va2 = stage(s + kStages - 1) + vofs2;
     const uint32_t ka = stage(s) + kofs;
-    uint32_t ksw[2] = {0u, 0u};  // MX: the scale words of the lane's two key rows
-    if constexpr (MX && DQK) {
-      ksw[0] = lds_read_b32<0>(stage(s) + sofs);
-      ksw[1] = lds_read_b32<128>(stage(s) + sofs);
-    }
     if constexpr (DQK) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
@@ -638,11 +553,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
         fr[b][0] = pv_read(va1, va2, i);
       } else {
         const int j = i - NPV, mb = j & 1, ks = j >> 1;
-        if constexpr (MX) {
-          const uint32_t an = ka + 32 * kKRowB * mb;
-          fr[b][0] = lds_read_b128<0>(an ^ (32 * (2 * ks)));
-          fr[b][kRQK - 1] = lds_read_b128<0>(an ^ (32 * (2 * ks + 1)));
-        } else if (mb == 0) {
+        if (mb == 0) {
           fr[b][0] = lds_read_b128<0>(ka ^ (32 * ks));
         } else {
           fr[b][0] = lds_read_b128<32 * kKRowB>(ka ^ (32 * ks));
@@ -677,20 +588,7 @@ __device__ CA_INLINE bool prefill_dma_qtile(
         o[ob] = Tr::mfma32(__builtin_bit_cast(vec8, va), pb[kk], o[ob]);
       } else {
         const int j = i - NPV, mb = j & 1, ks = j >> 1;
-        if constexpr (MX) {
-          if (j == 0) {
-            after_wait(ksw[0]);
-            after_wait(ksw[1]);
-          }
-          const i32x8 a = {(int)fr[b][0][0], (int)fr[b][0][1], (int)fr[b][0][2], (int)fr[b][0][3],
-                           (int)fr[b][kRQK - 1][0], (int)fr[b][kRQK - 1][1],
-                           (int)fr[b][kRQK - 1][2], (int)fr[b][kRQK - 1][3]};
-          const int ksc = (ksw[mb] >> (8 * (2 * ks + hl))) & 0xff;
-          sacc[mb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qx[ks], sacc[mb], 0, 0, 0,
-                                                                    ksc, 0, qsc[ks]);
-        } else {
-          sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, fr[b][0]), qv[ks], sacc[mb]);
-        }
+        sacc[mb] = Tr::mfma32(__builtin_bit_cast(vec8, fr[b][0]), qv[ks], sacc[mb]);
         if (j % (kNQK / kLoads) == kNQK / kLoads - 1) issue_one(s + kPpAhead, j / (kNQK / kLoads));
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -852,8 +750,8 @@ __device__ CA_INLINE bool prefill_dma_qtile(
       const int ob = kPassOb * p + j;
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const ovec2 lo = OutTr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
-        const ovec2 hi = OutTr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
+        const ovec2 lo = Tr::pack2(o[ob][4 * a] * inv, o[ob][4 * a + 1] * inv);
+        const ovec2 hi = Tr::pack2(o[ob][4 * a + 2] * inv, o[ob][4 * a + 3] * inv);
         ovec4 w;
         w[0] = lo[0]; w[1] = lo[1]; w[2] = hi[0]; w[3] = hi[1];
         const int c = 4 * j + a;  // d = 64 p + 8 c + 4 hl + [0, 4)
@@ -880,19 +778,16 @@ __device__ CA_INLINE bool prefill_dma_qtile(
   return redir;
 }
 
-// Operands of a prefill launch: Q, K as 16-bit rows or (MX) e4m3 codes with
-// e8m0 scale bytes QS, KS; V 16-bit rows; O the output rows.
+// Operands of a prefill launch: Q, K, V 16-bit rows; O the output rows.
 struct PfArgs {
   const void* q;
   const void* k;
-  const uint8_t* qs;
-  const uint8_t* ks;
   const uint16_t* v;
   void* o;
   float* lse;
 };
 
-template <typename Tr, typename OutTr, int D, bool CAUSAL, bool POS, bool MX>
+template <typename Tr, int D, bool CAUSAL, bool POS>
 __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
     PfArgs a, int S, int Hq, int Hkv, float scale_log2, int n_qt, int n_bh, int n_work, int paired,
     int q_shift, RopeQ rq) {
@@ -902,9 +797,7 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
   // tiles; a pair's long tile runs first: the pair workgroups of a head then
   // start their walks together over the same keys and share their L2 lines
   // (short tile first measured slower on C2, with more HBM fetches).
-  typename Tr::vec8 qv[MX ? 1 : D / 16];
-  i32x8 qx[2];
-  int qsc[2];
+  typename Tr::vec8 qv[D / 16];
   int g0 = 0;  // ring tiles taken by the earlier query tiles
   bool pre = false;
   int v = __builtin_amdgcn_workgroup_id_x(), pass = 0;
@@ -928,9 +821,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
                                    : PfItem{0, -1};
     const PfItem nx{__builtin_amdgcn_readfirstlane(nx0.bh), __builtin_amdgcn_readfirstlane(nx0.qt)};
     g0 = __builtin_amdgcn_readfirstlane(g0);
-    pre = prefill_dma_qtile<Tr, OutTr, D, CAUSAL, POS, MX>(a.q, a.k, a.qs, a.ks, a.v, a.o, a.lse, S,
-                                                           Hq, Hkv, scale_log2, bh, qt, q_shift, rq,
-                                                           nx, pre, g0, qv, qx, qsc);
+    pre = prefill_dma_qtile<Tr, D, CAUSAL, POS>(a.q, a.k, a.v, a.o, a.lse, S, Hq, Hkv, scale_log2, bh, qt,
+                                                 q_shift, rq, nx, pre, g0, qv);
     if (nx.qt < 0) break;
     // a drained ring is refilled by the next tile: every wave must be done reading it
     if (!pre) __builtin_amdgcn_s_barrier();
@@ -940,8 +832,8 @@ __global__ __launch_bounds__(64 * kPfWaves, 1) void prefill_dma_kernel(
   }
 }
 
-// Grid, ragged-S shift and launch of the prefill kernel (16-bit or MX).
-template <typename Tr, typename OutTr, int D, bool CAUSAL, bool MX>
+// Grid, ragged-S shift and launch of the prefill kernel.
+template <typename Tr, int D, bool CAUSAL>
 static hipError_t launch_prefill_kernel(const PfArgs& a, int B, int Hq, int Hkv, int S, float scale,
                                         hipStream_t stream, RopeQ rq) {
   using Gm = PfGeom<D>;
@@ -964,11 +856,11 @@ static hipError_t launch_prefill_kernel(const PfArgs& a, int B, int Hq, int Hkv,
   const float sl2 = scale * kLog2e;
   const dim3 block(64 * kPfWaves);
   if (sl2 >= 0.f) {
-    hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, true, MX>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, true>), dim3((unsigned)grid),
                        block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)n_work, paired,
                        q_shift, rq);
   } else {
-    hipLaunchKernelGGL((prefill_dma_kernel<Tr, OutTr, D, CAUSAL, false, MX>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((prefill_dma_kernel<Tr, D, CAUSAL, false>), dim3((unsigned)grid),
                        block, 0, stream, a, S, Hq, Hkv, sl2, n_qt, B * Hq, (int)n_work, paired,
                        q_shift, rq);
   }
@@ -979,8 +871,8 @@ template <typename Tr, int D, bool CAUSAL>
 static hipError_t launch_prefill_dma(const void* q, const void* k, const void* v, void* o, float* lse,
                                      int B, int Hq, int Hkv, int S, float scale,
                                      hipStream_t stream, RopeQ rq) {
-  const PfArgs a{q, k, nullptr, nullptr, (const uint16_t*)v, o, lse};
-  return launch_prefill_kernel<Tr, Tr, D, CAUSAL, false>(a, B, Hq, Hkv, S, scale, stream, rq);
+  const PfArgs a{q, k, (const uint16_t*)v, o, lse};
+  return launch_prefill_kernel<Tr, D, CAUSAL>(a, B, Hq, Hkv, S, scale, stream, rq);
 }
 
 
