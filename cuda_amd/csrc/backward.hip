@@ -420,7 +420,12 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
   const int G = Hq / Hkv;
   const int K0 = kt * BK;
   const size_t kvoff = (size_t)(b * Hkv + hk) * S;
-  const int lane = __builtin_amdgcn_workitem_id_x() & 63;
+  // The lane index is made opaque per call: otherwise the compiler hoists
+  // the lane-derived load offsets of both passes out of the kernel's pass
+  // loop and keeps them live through the tile loop, which at 256 VGPRs
+  // spills them (measured: 13-14 spilled registers at D = 128).
+  int lane = __builtin_amdgcn_workitem_id_x() & 63;
+  asm volatile("" : "+v"(lane));
   const int wave = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_workitem_id_x() >> 6);
   const int l32 = lane & 31, hl = lane >> 5;
   const int kw0 = K0 + 32 * wave;
