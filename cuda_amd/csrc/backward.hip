@@ -39,6 +39,15 @@ namespace {
 
 __device__ __forceinline__ int rho32(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
+// The lane index (0..63) recomputed where it is used, from v_mbcnt rather
+// than the work-item id: the compiler cannot hoist it (volatile) nor keep the
+// work-item id register live for it across a loop.
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Per query row of B * Hq * S: the pair (LSE * log2(e), D) with D = sum_d
 // dO[row][d] * O[row][d] (flash_attention_bwd_kernel.cuh:96-108), so the
 // kernels below fetch both terms of a row with one 8-byte load. D / 8 lanes
@@ -420,12 +429,11 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
   const int G = Hq / Hkv;
   const int K0 = kt * BK;
   const size_t kvoff = (size_t)(b * Hkv + hk) * S;
-  // The lane index is made opaque per call: otherwise the compiler hoists
-  // the lane-derived load offsets of both passes out of the kernel's pass
-  // loop and keeps them live through the tile loop, which at 256 VGPRs
-  // spills them (measured: 13-14 spilled registers at D = 128).
-  int lane = __builtin_amdgcn_workitem_id_x() & 63;
-  asm volatile("" : "+v"(lane));
+  // The lane index is recomputed per call (lane_here): otherwise the
+  // compiler hoists the lane-derived load offsets of both passes out of the
+  // kernel's pass loop and keeps them live through the tile loop, which at
+  // 256 VGPRs spills them (measured: 13-14 spilled registers at D = 128).
+  const int lane = lane_here();
   const int wave = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_workitem_id_x() >> 6);
   const int l32 = lane & 31, hl = lane >> 5;
   const int kw0 = K0 + 32 * wave;
@@ -598,8 +606,8 @@ __device__ CA_INLINE void bwd_dkv_dma_tile(const uint16_t* __restrict__ Q,
   }
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
   // the wave's V rows are no longer read: their LDS block stages dK, then dV
-  store_rowsT_lds<Tr, kNOB, kRowB>(dK + kvoff * D, kw0, S, dk, scale, lds_off(vw), lane);
-  store_rowsT_lds<Tr, kNOB, kRowB>(dV + kvoff * D, kw0, S, dv, 1.f, lds_off(vw), lane);
+  store_rowsT_lds<Tr, kNOB, kRowB>(dK + kvoff * D, kw0, S, dk, scale, lds_off(vw), lane_here());
+  store_rowsT_lds<Tr, kNOB, kRowB>(dV + kvoff * D, kw0, S, dv, 1.f, lds_off(vw), lane_here());
 }
 
 template <typename Tr, int D, bool CAUSAL>
