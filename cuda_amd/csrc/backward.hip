@@ -39,15 +39,6 @@ namespace {
 
 __device__ __forceinline__ int rho32(int i) { return (i & 0x13) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-// The lane index (0..63) recomputed where it is used, from v_mbcnt rather
-// than the work-item id: the compiler cannot hoist it (volatile) nor keep the
-// work-item id register live for it across a loop.
-__device__ __forceinline__ int lane_here() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
-
 // Per query row of B * Hq * S: the pair (LSE * log2(e), D) with D = sum_d
 // dO[row][d] * O[row][d] (flash_attention_bwd_kernel.cuh:96-108), so the
 // kernels below fetch both terms of a row with one 8-byte load. D / 8 lanes

@@ -184,6 +184,16 @@ __device__ __forceinline__ V8 cat4(V4 lo, V4 hi) {
   return r;
 }
 
+// The lane index (0..63) recomputed where it is used, from v_mbcnt rather
+// than the work-item id: the compiler can neither hoist it (volatile) nor keep
+// the work-item id register live for it across a loop, which in the kernels
+// at 256 VGPRs turned hoisted lane offsets into spills.
+__device__ __forceinline__ int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // Hardware XCD of workgroup `w`: consecutive workgroup ids are dealt
 // round-robin over the 8 XCDs of an MI355X. Returns the logical work index so
 // that each XCD walks one contiguous slice of [0, total).

@@ -60,8 +60,11 @@ __device__ CA_INLINE void prefill_f32_qtile(
   const float* Kp = K + (size_t)(b * Hkv + hk) * S * D;
   const float* Vp = V + (size_t)(b * Hkv + hk) * S * D;
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // lane recomputed per query tile (lane_here): hoisted out of the kernel's
+  // pass loop, its offsets spilled at D = 128
+  const int lane = lane_here();
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int tid = wave * 64 + lane;
   const int l32 = lane & 31, hl = lane >> 5;
   const int qw0 = q0 + wave * 32;
   const int myq = qw0 + l32;
