@@ -9,6 +9,12 @@ hide its VALU work, and every K/V fragment read from LDS feeds two MFMAs.
 That walk needs O^T and Q in AGPRs and S^T, P in VGPRs with no copies; the
 register assignment is fixed here, by hand, and the instruction order with it.
 
+With --mx it writes the MXFP8 form of the same walk (`prefill_w64_mx.hip`):
+QK on v_mfma_scale_f32_32x32x64_f8f6f4 (16 passes, e4m3 codes with per-lane
+e8m0 scale bytes picked by op_sel), K and V^T fragments in one AGPR ring,
+K scale words travelling in the K ring slot, and row sums over the
+bf16-rounded weights; `configure(mx)` rebinds the register map.
+
 This script writes the kernel body as one string-literal macro per variant
 (causal, non-causal) for an inline-asm statement, plus the clobber list. It
 also checks its own output before writing it:
@@ -22,9 +28,12 @@ also checks its own output before writing it:
 * counters: the LDS and vector-memory operations in flight are tracked in
   order, and a use of a register whose load has not been waited on by an
   s_waitcnt is rejected; at a control-flow join the in-flight lists of all
-  predecessors must agree.
+  predecessors must agree;
+* SCC: every SCC reader's producer is the instruction it was written for;
+* schedule: every placed instruction reads each register from the same
+  writer as in program order.
 
-Usage: gen_prefill_w64.py OUT.inc
+Usage: gen_prefill_w64.py [--mx] OUT.inc
 """
 import sys
 
@@ -640,6 +649,7 @@ def MFMA_SCALE(d, a_, b_, c, sa, sb, opa, opb):
     uses = [a_, b_, sa, sb] + ([c] if c is not None else [])
     return Ins("mfma", t, defs=[d], uses=uses, mdst=tuple(d.keys()), mc=tuple(c.keys()) if c is not None else None,
                mab=a_.keys() + b_.keys() + sa.keys() + sb.keys())
+
 
 RSRC3 = 0x00020000     # buffer resource word 3: raw 32-bit dwords
 LDS_V = 65536          # V ring offset in LDS
