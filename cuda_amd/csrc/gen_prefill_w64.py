@@ -136,7 +136,8 @@ class Ins:
         self.frag = None
 
 
-def MFMA(d, a, b, c, op="v_mfma_f32_32x32x16_bf16"):
+def MFMA(d, a, b, c, op=None):
+    op = op or MFMA_OP
     uses = [a, b] + ([c] if c is not None else [])
     return Ins("mfma", f"{op} {d}, {a}, {b}, {c if c is not None else 0}", defs=[d], uses=uses,
                mdst=tuple(d.keys()), mc=tuple(c.keys()) if c is not None else None,
@@ -656,6 +657,20 @@ LDS_V = 65536          # V ring offset in LDS
 LDS_STG = 131072       # output staging offset in LDS
 SLOT = 16384           # bytes per K (or V) tile of 64 rows x 256 bytes
 BOUND_F = 0x57800000   # 2^48: the stale-max bound of a tile sum with bf16 P
+# element type of Q, K, V, P and O: bf16, or fp16 (configure_f16): its MFMA,
+# the P / O pack and the stale-max bound (2^15, the largest power of two below
+# fp16's 65504, so no weight of a tile that passes the check overflows)
+F16 = False
+MFMA_OP = "v_mfma_f32_32x32x16_bf16"
+PK_OP = "v_cvt_pk_bf16_f32"
+
+
+def configure_f16(on):
+    global F16, MFMA_OP, PK_OP, BOUND_F
+    F16 = on
+    MFMA_OP = "v_mfma_f32_32x32x16_f16" if on else "v_mfma_f32_32x32x16_bf16"
+    PK_OP = "v_cvt_pk_f16_f32" if on else "v_cvt_pk_bf16_f32"
+    BOUND_F = 0x47000000 if on else 0x57800000
 LN2 = 0x3F317218
 
 
@@ -813,7 +828,7 @@ def softmax_exp_program(sm, p, masked, causal, kk_release, first_sum_init=True, 
             exps.append(sm.add(V("v_exp_f32", tb[e], tb[e], trans=True), [(fmas[e], 1)]))
         unp = {}
         for q in range(4):
-            op = sm.add(V("v_cvt_pk_bf16_f32", PB[kk][nb][q], tb[2 * q], tb[2 * q + 1]),
+            op = sm.add(V(PK_OP, PB[kk][nb][q], tb[2 * q], tb[2 * q + 1]),
                         [(exps[2 * q], TRANS_FWD), (exps[2 * q + 1], TRANS_FWD)], nb_gap=kk_release[kk])
             last_read[(g, 2 * q)] = last_read[(g, 2 * q + 1)] = op
             if MX:
@@ -1118,7 +1133,7 @@ def pre_reads_log_for(pre_reads, reads):
 class Gen:
     def __init__(self, causal):
         self.causal = causal
-        self.tag = ("M" if MX else "") + ("C" if causal else "F")
+        self.tag = ("M" if MX else "H" if F16 else "") + ("C" if causal else "F")
         self.prog = []
         self.nlab = 0
 
@@ -1636,7 +1651,7 @@ class Gen:
             if e % 2 == 1:
                 i = e // 2
                 lo = max(pos + 1, rel[kk])
-                cvt[i] = add(V("v_cvt_pk_bf16_f32", PB[kk][nb][(e % 8) // 2], tmp[(e - 1) % 24], t),
+                cvt[i] = add(V(PK_OP, PB[kk][nb][(e % 8) // 2], tmp[(e - 1) % 24], t),
                              lo, min(lo + 6, 62), [(exp[e - 1], TRANS_FWD), (exp[e], TRANS_FWD)])
             acc = PSUM[nb][e % 2]
             init = kk == 0 and e % 8 < 2
@@ -1845,7 +1860,7 @@ class Gen:
     def output_o_any(self, tag):
         """output_o; MX: bf16 or fp16 by OUTF16."""
         if not MX:
-            return self.output_o()[0]
+            return self.output_o(f16=F16)[0]
         L = lambda n: self.L(f"{n}_{tag}")
         return ([S("s_bitcmp1_b32", OUTF16, 0), CBR("s_cbranch_scc1", L("o16"))] + self.output_o()[0] +
                 [BR(L("odone")), LABEL(L("o16"))] + self.output_o(f16=True)[0] + [LABEL(L("odone"))])
@@ -2294,13 +2309,18 @@ def main(argv):
     pre = "CA_PFW64MX_" if mx else "CA_PFW64_"
     text = ["// Generated by gen_prefill_w64.py: the 64-row prefill kernel bodies. Do not edit.",
             "#pragma once", ""]
-    for causal in (True, False):
-        g = Gen(causal)
-        prog = g.kernel()
-        check(prog, g.tag)
-        check_scc(prog, g.tag)
-        text.append(to_macro(pre + "BODY_" + ("CAUSAL" if causal else "FULL"), prog))
-        print(f"variant {g.tag}: {len(prog)} lines {stats(prog)}", file=sys.stderr)
+    # the 16-bit file holds bf16 (CA_PFW64_BODY_*) and fp16 (CA_PFW64_F16_BODY_*)
+    for f16 in ((False, True) if not mx else (False,)):
+        configure_f16(f16)
+        for causal in (True, False):
+            g = Gen(causal)
+            prog = g.kernel()
+            check(prog, g.tag)
+            check_scc(prog, g.tag)
+            name = pre + ("F16_" if f16 else "") + "BODY_" + ("CAUSAL" if causal else "FULL")
+            text.append(to_macro(name, prog))
+            print(f"variant {g.tag}: {len(prog)} lines {stats(prog)}", file=sys.stderr)
+    configure_f16(False)
     text.append(f"#define {pre}CLOBBERS " + clobbers())
     text.append(f"#define {pre}IN_V {len(IN_V)}")
     src = "\n".join(text) + "\n"

@@ -29,10 +29,11 @@ struct RopeQ {
 hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v, void* o,
                           float* lse, int B, int Hq, int Hkv, int S, int D, float scale,
                           bool causal, hipStream_t stream, RopeQ rq = RopeQ{});
-// 64-row-per-wave prefill (prefill_w64.hip): bf16, head dim 128, softmax
-// scale >= 0, no RoPE; launch_prefill dispatches to it when supported.
+// 64-row-per-wave prefill (prefill_w64.hip): bf16 or fp16 (f16), head dim
+// 128, softmax scale >= 0, no RoPE; launch_prefill dispatches to it when
+// supported.
 bool prefill_w64_supported(int D, int S, float scale, bool rope);
-hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+hipError_t launch_prefill_w64(bool f16, const void* q, const void* k, const void* v, void* o, float* lse, int B,
                               int Hq, int Hkv, int S, float scale, bool causal, hipStream_t stream);
 void magic_div(uint32_t d, uint32_t* m, uint32_t* sh);
 // Work decomposition of the 64-row kernels (grid 0: nothing to launch).

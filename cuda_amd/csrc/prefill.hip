@@ -885,9 +885,9 @@ hipError_t launch_prefill(int dtype, const void* q, const void* k, const void* v
                   : launch_prefill_dma<TR, DD, false>(q, k, v, o, lse, B, Hq, Hkv, S, scale, stream, rq); \
   }
   if (dtype == kDtypeF32) return launch_prefill_f32(q, k, v, o, lse, B, Hq, Hkv, S, D, scale, causal, stream);
+  if ((dtype == kDtypeBF16 || dtype == kDtypeF16) && prefill_w64_supported(D, S, scale, rq.cos != nullptr))
+    return launch_prefill_w64(dtype == kDtypeF16, q, k, v, o, lse, B, Hq, Hkv, S, scale, causal, stream);
   if (dtype == kDtypeBF16) {
-    if (prefill_w64_supported(D, S, scale, rq.cos != nullptr))
-      return launch_prefill_w64(q, k, v, o, lse, B, Hq, Hkv, S, scale, causal, stream);
     CA_PREFILL_DMA(BF16, 64)
     CA_PREFILL_DMA(BF16, 128)
   } else if (dtype == kDtypeF16) {

@@ -1,5 +1,5 @@
-// Prefill for 16-bit head dim 128 (bf16): one wave per SIMD, 64 query rows
-// per wave, the key walk as hand-scheduled gfx950 assembly.
+// Prefill for 16-bit head dim 128 (bf16 or fp16): one wave per SIMD, 64
+// query rows per wave, the key walk as hand-scheduled gfx950 assembly.
 //
 // Computes O = softmax(Q K^T * scale [+ causal mask]) V per (batch, q-head),
 // the contract of dispatch_flash_attention_v2 / _v3_hopper / fused_gqa in the
@@ -19,16 +19,16 @@
 // each tile. The walk's code has a copy per iteration index mod 4, so every
 // ring slot is an instruction offset on LDS addresses fixed for the kernel.
 //
-// Per wave, iteration i of the walk issues 64 v_mfma_f32_32x32x16_bf16:
+// Per wave, iteration i of the walk issues 64 v_mfma_f32_32x32x16_bf16 (_f16):
 //   PV(i - 1): O^T[128 d x 64 q] += V^T P^T   (A = V^T via ds_read_b64_tr_b16,
 //              B = P^T in VGPRs, O^T accumulators in AGPRs)
 //   QK(i + 1): S^T[64 keys x 64 q] = K Q^T    (A = K from LDS, B = Q in AGPRs,
 //              S^T accumulators in VGPRs, two buffers by tile parity)
 // and between them the softmax of tile i: P = 2^(S c - m) against the
 // running max m as it stands (a tile is redone with its own max, O and l
-// rescaled, when a lane's tile sum passes 2^48 or is not finite), packed to
-// bf16 straight into the PV B operand, row sums as fp32 adds of the unrounded
-// weights. Each K or V^T fragment read from LDS feeds two MFMAs (the wave's
+// rescaled, when a lane's tile sum passes 2^48 (fp16: 2^15, so no weight
+// overflows its type) or is not finite), packed to bf16 / fp16 straight into
+// the PV B operand, row sums as fp32 adds of the unrounded weights. Each K or V^T fragment read from LDS feeds two MFMAs (the wave's
 // two 32-query blocks). The register assignment and the instruction order
 // are fixed by gen_prefill_w64.py, which writes the body and checks its
 // hazards and memory-counter waits.
@@ -71,7 +71,7 @@ static_assert(offsetof(PfW64Args, S) == 40 && offsetof(PfW64Args, scale_log2) ==
 
 constexpr int kW64Threads = 256;  // 4 waves, one per SIMD (512 registers each)
 
-template <bool CAUSAL>
+template <bool CAUSAL, bool F16>
 __global__ __launch_bounds__(kW64Threads, 1) void prefill_w64_kernel(PfW64Args args) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds[160 * 1024];
   const int tid = threadIdx.x;
@@ -115,7 +115,11 @@ __global__ __launch_bounds__(kW64Threads, 1) void prefill_w64_kernel(PfW64Args a
       [vofs1] "v"(vofs1), [vofs2] "v"(vofs2), [loff0] "v"(loff[0]), [loff1] "v"(loff[1]),         \
       [loff2] "v"(loff[2]), [loff3] "v"(loff[3]), [qlane] "v"(qlane), [dl] "v"(dl), [h8] "v"(h8), \
       [wbase] "v"(wbase), [wx] "v"(wx), [rdl] "v"(rdl), [stl] "v"(stl), [lsel] "v"(lsel)
-  if constexpr (CAUSAL) {
+  if constexpr (CAUSAL && F16) {
+    asm volatile(CA_PFW64_F16_BODY_CAUSAL ::CA_PFW64_OPERANDS : CA_PFW64_CLOBBERS);
+  } else if constexpr (F16) {
+    asm volatile(CA_PFW64_F16_BODY_FULL ::CA_PFW64_OPERANDS : CA_PFW64_CLOBBERS);
+  } else if constexpr (CAUSAL) {
     asm volatile(CA_PFW64_BODY_CAUSAL ::CA_PFW64_OPERANDS : CA_PFW64_CLOBBERS);
   } else {
     asm volatile(CA_PFW64_BODY_FULL ::CA_PFW64_OPERANDS : CA_PFW64_CLOBBERS);
@@ -169,7 +173,7 @@ hipError_t w64_geometry(int B, int Hq, int S, bool causal, PfW64Geom* g) {
   return hipSuccess;
 }
 
-hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+hipError_t launch_prefill_w64(bool f16, const void* q, const void* k, const void* v, void* o, float* lse, int B,
                               int Hq, int Hkv, int S, float scale, bool causal, hipStream_t stream) {
   PfW64Geom g;
   const hipError_t ge = w64_geometry(B, Hq, S, causal, &g);
@@ -200,10 +204,15 @@ hipError_t launch_prefill_w64(const void* q, const void* k, const void* v, void*
   magic_div((uint32_t)(Hq / Hkv), &a.m_ratio, &a.sh_ratio);
   a.xcd_q = g.xcd_q;
   a.xcd_r = g.xcd_r;
-  if (causal) {
-    hipLaunchKernelGGL(prefill_w64_kernel<true>, dim3((unsigned)grid), dim3(kW64Threads), 0, stream, a);
+  const dim3 g3((unsigned)grid), b3(kW64Threads);
+  if (causal && f16) {
+    hipLaunchKernelGGL((prefill_w64_kernel<true, true>), g3, b3, 0, stream, a);
+  } else if (f16) {
+    hipLaunchKernelGGL((prefill_w64_kernel<false, true>), g3, b3, 0, stream, a);
+  } else if (causal) {
+    hipLaunchKernelGGL((prefill_w64_kernel<true, false>), g3, b3, 0, stream, a);
   } else {
-    hipLaunchKernelGGL(prefill_w64_kernel<false>, dim3((unsigned)grid), dim3(kW64Threads), 0, stream, a);
+    hipLaunchKernelGGL((prefill_w64_kernel<false, false>), g3, b3, 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -1,6 +1,6 @@
 """CPU tier: the checks of the 64-row kernel generator (gen_prefill_w64.py).
 
-The generated bodies (bf16 and MXFP8, causal and not) pass the hazard,
+The generated bodies (bf16, fp16 and MXFP8, causal and not) pass the hazard,
 memory-counter, SCC and schedule checks the generator runs before writing
 them; and each check rejects a planted mistake of the kind it exists for: a
 dropped LDS wait, an MFMA result read too early, an SCC reader behind a
@@ -17,10 +17,12 @@ sys.path.insert(0, os.path.join(ROOT, "cuda_amd", "csrc"))
 import gen_prefill_w64 as G  # noqa: E402
 
 
-@pytest.fixture(params=[False, True], ids=["bf16", "mx"])
+@pytest.fixture(params=["bf16", "f16", "mx"])
 def mode(request):
-    G.configure(request.param)
+    G.configure(request.param == "mx")
+    G.configure_f16(request.param == "f16")
     yield request.param
+    G.configure_f16(False)
     G.configure(False)
 
 
@@ -41,7 +43,9 @@ def test_generated_bodies_pass_checks(mode, causal):
     kinds = {x.kind for x in prog}
     assert {"mfma", "lds", "vmem", "valu", "salu", "barrier", "wait"} <= kinds
     scale = [x for x in prog if x.kind == "mfma" and "scale" in x.text]
-    assert bool(scale) == mode    # the MX body runs QK on the scaled fp8 MFMA
+    assert bool(scale) == (mode == "mx")    # the MX body runs QK on the scaled fp8 MFMA
+    f16 = [x for x in prog if x.kind == "mfma" and "_f16 " in x.text]
+    assert bool(f16) == (mode == "f16")     # only the fp16 body runs the fp16 MFMA
 
 
 def test_dropped_lds_wait_is_rejected(mode):
@@ -91,13 +95,25 @@ def test_reordered_dependency_is_rejected():
         G.check_item_order(items, [r, w])
 
 
-def test_mx_configuration_is_reversible():
-    """configure(True) then configure(False) gives back the bf16 body
-    exactly (the register map and limits are rebound, not mutated)."""
+def test_configuration_is_reversible():
+    """configure(True) or configure_f16(True), then back, gives the bf16
+    body exactly (the register map and limits are rebound, not mutated)."""
     G.configure(False)
     a = G.Gen(True).kernel()
     G.configure(True)
     G.Gen(True).kernel()
     G.configure(False)
+    G.configure_f16(True)
+    c = G.Gen(True).kernel()
+    G.configure_f16(False)
     b = G.Gen(True).kernel()
     assert [x.text for x in a] == [x.text for x in b]
+    # the fp16 body is the bf16 one with the MFMA, the P packs and the redo
+    # bound (2^48 for bf16 P, 2^15 for fp16 P) changed
+    assert len(a) == len(c)
+    ct = [y.text.replace("pfw64HC", "pfw64C") for y in c]   # labels carry the body's tag
+    diff = {(x.text.split()[0], y.split()[0]) for x, y in zip(a, ct) if x.text != y}
+    assert diff == {("v_mfma_f32_32x32x16_bf16", "v_mfma_f32_32x32x16_f16"),
+                    ("v_cvt_pk_bf16_f32", "v_cvt_pk_f16_f32"), ("s_mov_b32", "s_mov_b32")}, diff
+    bounds = [(x.text, y) for x, y in zip(a, ct) if x.text.startswith("s_mov_b32") and x.text != y]
+    assert len(bounds) == 1 and "0x57800000" in bounds[0][0] and "0x47000000" in bounds[0][1]

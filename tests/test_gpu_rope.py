@@ -61,16 +61,16 @@ def test_rope_longer_and_gqa(dev, b, hq, hkv, s, d):
 @pytest.mark.parametrize("dtype,d", [(torch.float16, 128), (torch.bfloat16, 64), (torch.bfloat16, 128)])
 def test_rope_identity_tables_equal_flash_attention(dev, dtype, d):
     """Identity tables leave Q and K as they are. Where both calls run the
-    same kernel the outputs are equal bit for bit; bf16 at head dim 128
-    without rope runs the 64-row kernel, whose summation order differs, so
-    there the two agree to the 16-bit tolerance."""
+    same kernel the outputs are equal bit for bit; at head dim 128 without
+    rope both 16-bit types run the 64-row kernel, whose summation order
+    differs, so there the two agree to the 16-bit tolerance."""
     q, k, v = qkv(2, 4, 300, d, dtype, dev)
     ones = torch.ones(300, d, device=dev)
     zeros = torch.zeros(300, d, device=dev)
     a = cuda_llm.fused_rope_flash_attention(q, k, v, ones, zeros, is_causal=True)
     b = cuda_llm.flash_attention(q, k, v, is_causal=True)
     torch.cuda.synchronize()
-    if dtype == torch.bfloat16 and d == 128:
+    if d == 128:
         assert_close(to_np(a), to_np(b), **TOL_16BIT, name="identity rope")
     else:
         assert torch.equal(a, b)
