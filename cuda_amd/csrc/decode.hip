@@ -335,7 +335,16 @@ void decode_split_kernel(
 // Layouts in a ring slot: K pages as loaded ([D][16]; the 16-bit page's
 // 16-byte chunks are XOR-swizzled on bit 3 of the chunk index by row-octet
 // parity so the tr16 reads of lane groups 0/1 and 2/3 hit disjoint banks),
-// V pages linear [D][16].
+// V pages [D][16] with the 16-bit page's chunks swizzled too (chunk q at
+// q ^ bit 4 of q): a 32-lane half of a V read takes the first or second 16
+// bytes of 16 rows, 32 bytes apart, which without the swizzle put rows r
+// and r + 8 on the same banks (a b64 read is conflict-free when each half
+// covers 256 distinct bytes modulo 256). FP8 V rows are 16 bytes, and a
+// b32 read of a lane's 4 tokens is 2-way conflicting (its halves need 32
+// distinct dwords modulo 128 bytes from 16 rows, two dwords each), so the
+// FP8 lanes read 8 bytes (tokens 8 (grp / 2) .. + 7: lane groups 0/1 and
+// 2/3 read the same addresses, 16 rows x 8 bytes per half) and keep the
+// dword of their own group.
 // ---------------------------------------------------------------------------
 // Ring depth (steps of one page, K and V, in flight per wave) and pages per
 // split of the direct-load decode: 256 KB of K and V per split for both
@@ -460,6 +469,8 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     if (FP8) return 16 * p;
     return 16 * (p ^ (((p >> 4) & 1) << 3));
   };
+  // source offset of this lane's 16 bytes in each 1 KB of a V chunk
+  const int v_src = 16 * (FP8 ? lane : lane ^ ((lane >> 4) & 1));
   const unsigned char* dummy = (const unsigned char*)Q;  // 16 valid bytes for padding loads
   auto issue_step = [&](int step, int slot) {
     unsigned char* base = ring + slot * STAGE;
@@ -473,7 +484,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       dma16<kDmaPolicy>(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + 1024 * i));
-      dma16<kDmaPolicy>(valid ? vp + 1024 * i + 16 * lane : dummy,
+      dma16<kDmaPolicy>(valid ? vp + 1024 * i + v_src : dummy,
                         (CA_LDS void*)(base + CHUNK + 1024 * i));
     }
   };
@@ -488,7 +499,10 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     k_lo = 16 * (16 * grp + 8 * par + 2 * j + (c >> 1)) + 8 * (c & 1);
     k_hi = 16 * (16 * grp + 8 * (1 - par) + 2 * j + (c >> 1)) + 8 * (c & 1);
   }
-  const uint32_t v_off = (uint32_t)(16 * l16 + 4 * grp) * ELEM;
+  // V: lane (d = l16, token group grp) needs tokens 4 grp .. 4 grp + 3 of row d
+  // (FP8: the 8 bytes of tokens 8 (grp / 2) .. + 7, then its own dword)
+  const uint32_t v_off = FP8 ? (uint32_t)(16 * l16 + 8 * (grp >> 1))
+                             : (uint32_t)(16 * ((2 * l16 + (grp >> 1)) ^ ((l16 >> 3) & 1)) + 8 * (grp & 1));
   const uint32_t ring0 = lds_off(ring);
 
   f32x4 o[NB];
@@ -508,7 +522,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 
     // ---- LDS -> operands ----
     u32x2 kraw[KRD];
-    uint32_t v8r[FP8 ? NB : 1];
+    u32x2 v8r[FP8 ? NB : 1];
     u32x2 v16r[FP8 ? 1 : NB];
     if (FP8) {
       const uint32_t a = kb + k_lo;
@@ -516,7 +530,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
       if (NKS > 1) kraw[1 % KRD] = lds_read_tr8<512>(a);
       if (NKS > 2) kraw[2 % KRD] = lds_read_tr8<1024>(a);
       if (NKS > 3) kraw[3 % KRD] = lds_read_tr8<1536>(a);
-#define CA_V8(NBI) if (NBI < NB) v8r[NBI % NB] = lds_read_b32<256 * NBI>(vb);
+#define CA_V8(NBI) if (NBI < NB) v8r[NBI % NB] = lds_read_b64<256 * NBI>(vb);
       CA_V8(0) CA_V8(1) CA_V8(2) CA_V8(3) CA_V8(4) CA_V8(5) CA_V8(6) CA_V8(7)
 #undef CA_V8
     } else {
@@ -607,7 +621,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     for (int nb = 0; nb < NB; ++nb) {
       u32x2 bw;
       if (FP8) {
-        const uint32_t v = v8r[nb % (FP8 ? NB : 1)];
+        const uint32_t v = (grp & 1) ? v8r[nb % (FP8 ? NB : 1)][1] : v8r[nb % (FP8 ? NB : 1)][0];
         bw[0] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<false>(v));
         bw[1] = __builtin_bit_cast(uint32_t, Fp8Conv<Tr>::template cvt<true>(v));
       } else {
