@@ -254,13 +254,16 @@ def test_causal_paired_query_tiles(dev, dtype, d, b, hq, hkv, s):
     assert (out[:, :, 0].float() - kv0).abs().max().item() <= 1e-2
 
 
-@pytest.mark.parametrize("s,d", [(1536, 128), (4096, 128), (3640, 128), (3640, 64)])
-def test_persistent_noncausal(dev, s, d):
+@pytest.mark.parametrize("dtype,s,d", [(torch.bfloat16, 1536, 128), (torch.bfloat16, 4096, 128),
+                                       (torch.bfloat16, 3640, 128), (torch.bfloat16, 3640, 64),
+                                       (torch.float16, 4096, 128), (torch.float16, 3640, 128)])
+def test_persistent_noncausal(dev, dtype, s, d):
     """Non-causal grids of more than 256 query tiles: the persistent launch,
     whose workgroups take several tiles each, the key ring running on from
-    one tile into the next; S = 3640 is ragged (the first tile holds 64 rows)."""
+    one tile into the next; S = 3640 is ragged (the first tile holds 64 rows).
+    fp16 at head dim 128 runs the same 64-row kernel as bf16."""
     b, hq, hkv = (4, 32, 8) if s == 1536 else (2, 32, 8)
-    q, k, v = qkv(b, hq, s, d, torch.bfloat16, dev, hkv=hkv)
+    q, k, v = qkv(b, hq, s, d, dtype, dev, hkv=hkv)
     out = cuda_llm.flash_attention(q, k, v, is_causal=False)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
