@@ -9,6 +9,10 @@ hide its VALU work, and every K/V fragment read from LDS feeds two MFMAs.
 That walk needs O^T and Q in AGPRs and S^T, P in VGPRs with no copies; the
 register assignment is fixed here, by hand, and the instruction order with it.
 
+The same run writes an fp16 body beside the bf16 one (`configure_f16`):
+v_mfma_f32_32x32x16_f16, v_cvt_pk_f16_f32 for P, and a redo bound of 2^15
+on a tile sum so that no weight passes fp16's 65504.
+
 With --mx it writes the MXFP8 form of the same walk (`prefill_w64_mx.hip`):
 QK on v_mfma_scale_f32_32x32x64_f8f6f4 (16 passes, e4m3 codes with per-lane
 e8m0 scale bytes picked by op_sel), K and V^T fragments in one AGPR ring,
@@ -16,7 +20,8 @@ K scale words travelling in the K ring slot, and row sums over the
 bf16-rounded weights; `configure(mx)` rebinds the register map.
 
 This script writes the kernel body as one string-literal macro per variant
-(causal, non-causal) for an inline-asm statement, plus the clobber list. It
+(causal, non-causal; bf16 and fp16) for an inline-asm statement, plus the
+clobber list. It
 also checks its own output before writing it:
 
 * hazards: a forward dataflow over the body's control-flow graph tracks, for
