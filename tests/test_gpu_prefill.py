@@ -272,3 +272,38 @@ def test_persistent_noncausal(dev, dtype, s, d):
         ref = oracle.attention(to_np(q[bi:bi + 1, hi:hi + 1]), to_np(k[bi:bi + 1, kh:kh + 1]),
                                to_np(v[bi:bi + 1, kh:kh + 1]))
         assert_close(to_np(out[bi:bi + 1, hi:hi + 1]), ref, **TOL_16BIT, name=f"head {bi},{hi}")
+
+
+def _random_w64_cases(n=12, seed=1234):
+    """Seeded shapes for the 64-row kernel (head dim 128, bf16 and fp16):
+    ragged lengths (a first query tile of 64-192 rows), GQA ratios, causal
+    and not, with and without the LSE output."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        g = int(rng.choice([1, 2, 4]))
+        s = int(rng.integers(65, 2600))
+        out.append((torch.float16 if i % 2 else torch.bfloat16, int(rng.integers(1, 3)), hkv * g, hkv, s,
+                    bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), float(rng.choice([0.05, 0.0884, 0.2]))))
+    return out
+
+
+@pytest.mark.parametrize("dtype,b,hq,hkv,s,causal,lse,scale", _random_w64_cases())
+def test_w64_random_shapes(dev, dtype, b, hq, hkv, s, causal, lse, scale):
+    """The 64-row kernel on seeded random shapes: every head of the first
+    batch against the oracle; the LSE, where asked for, against the oracle's
+    logsumexp."""
+    gen = torch.Generator(device=dev).manual_seed(s)
+    q, k, v = qkv(b, hq, s, 128, dtype, dev, hkv=hkv, gen=gen)
+    if lse:
+        out, l = cuda_llm.flash_attention_forward_lse(q, k, v, is_causal=causal, softmax_scale=scale)
+    else:
+        out = cuda_llm.flash_attention(q, k, v, is_causal=causal, softmax_scale=scale)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = oracle.attention(to_np(q[:1]), to_np(k[:1]), to_np(v[:1]), is_causal=causal, scale=scale)
+    assert_close(to_np(out[:1]), ref, **TOL_16BIT, name=f"{dtype} {b}x{hq}/{hkv}x{s} causal={causal}")
+    if lse:
+        lref = oracle.attention_lse(to_np(q[:1]), to_np(k[:1]), is_causal=causal, scale=scale, dtype=np.float64)
+        assert np.abs(to_np(l[:1]) - lref).max() <= 1e-3
