@@ -668,7 +668,12 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
 
 // Combines the split partials of every (sequence, query head) with more than
 // one split: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). One wave per
-// (sequence, head); each lane owns D/64 output elements.
+// (sequence, head); each lane owns D/64 output elements. The kernel is bound
+// by memory latency, not bytes: the first kMergeAhead splits' partials are
+// loaded together with the splits' log2-sum-exp, before their maximum is
+// known, so a sequence of up to kMergeAhead splits takes one round trip; the
+// sum runs over the splits in order either way.
+constexpr int kMergeAhead = 16;
 template <typename Tr, int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(
     const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
@@ -682,8 +687,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   const int n_splits = (n_pages + pages_per_split - 1) / pages_per_split;
   if (n_splits <= 1) return;
   const size_t slot0 = ((size_t)n * Hq + hq) * max_splits;
-  float M = kNegInf;
-  for (int s = lane; s < n_splits; s += 64) M = __builtin_fmaxf(M, ws_lse[slot0 + s]);
+  const float lse0 = lane < n_splits ? ws_lse[slot0 + lane] : kNegInf;  // split `lane`
+  const int n_ahead = min(kMergeAhead, n_splits);
+  float part[kMergeAhead][PER];
+#pragma unroll
+  for (int j = 0; j < kMergeAhead; ++j)
+    if (j < n_ahead) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) part[j][i] = ws_o[(slot0 + j) * D + lane * PER + i];
+    }
+  float M = lse0;
+  for (int s = lane + 64; s < n_splits; s += 64) M = __builtin_fmaxf(M, ws_lse[slot0 + s]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, 64));
   float wsum = 0.f;
@@ -693,11 +707,23 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   if (M != kNegInf) {
     for (int s0 = 0; s0 < n_splits; s0 += 64) {
       const int s = s0 + lane;
-      const float lse = (s < n_splits) ? ws_lse[slot0 + s] : kNegInf;
+      const float lse = s0 == 0 ? lse0 : (s < n_splits) ? ws_lse[slot0 + s] : kNegInf;
       const float wl = (lse == kNegInf) ? 0.f : fast_exp2(lse - M);
       const int cnt = min(64, n_splits - s0);
+      int j0 = 0;
+      if (s0 == 0) {
+#pragma unroll
+        for (int j = 0; j < kMergeAhead; ++j)
+          if (j < n_ahead) {
+            const float wj = __shfl(wl, j, 64);
+            wsum += wj;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) acc[i] += wj * part[j][i];
+          }
+        j0 = n_ahead;
+      }
 #pragma unroll 4
-      for (int j = 0; j < cnt; ++j) {
+      for (int j = j0; j < cnt; ++j) {
         const float wj = __shfl(wl, j, 64);
         wsum += wj;
         const float* src = ws_o + (slot0 + s0 + j) * D + lane * PER;
