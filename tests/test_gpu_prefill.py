@@ -307,3 +307,17 @@ def test_w64_random_shapes(dev, dtype, b, hq, hkv, s, causal, lse, scale):
     if lse:
         lref = oracle.attention_lse(to_np(q[:1]), to_np(k[:1]), is_causal=causal, scale=scale, dtype=np.float64)
         assert np.abs(to_np(l[:1]) - lref).max() <= 1e-3
+
+
+@pytest.mark.parametrize("dtype,s,causal", [(torch.bfloat16, 16384, True), (torch.float16, 16384, False),
+                                            (torch.bfloat16, 12345, False)])
+def test_w64_long_sequences(dev, dtype, s, causal):
+    """Long walks of the 64-row kernel (up to 256 key tiles per query tile,
+    64 query tiles per head) on one head against the oracle."""
+    gen = torch.Generator(device=dev).manual_seed(s)
+    q, k, v = qkv(1, 2, s, 128, dtype, dev, gen=gen)
+    out = cuda_llm.flash_attention(q, k, v, is_causal=causal)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    ref = oracle.attention(to_np(q[:, 1:]), to_np(k[:, 1:]), to_np(v[:, 1:]), is_causal=causal)
+    assert_close(to_np(out[:, 1:]), ref, **TOL_16BIT, name=f"{dtype} S={s} causal={causal}")
