@@ -38,7 +38,8 @@ COMMON = [
 # v_accvgpr_read/write per element and tile (measured: ~130-190 per tile at
 # D = 64), which a wave pays in series with its MFMAs.
 EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
-         "f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+         "f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+         "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 # Generated sources: the 64-row prefill's kernel body (hand-scheduled

@@ -307,7 +307,7 @@ ca_status ca_fp8_paged_attention_noalloc(ca_dtype dtype, const void* query,
   if (num_seqs == 0) return CA_OK;
   if (!k_scale || !v_scale) return fail(CA_INVALID_ARGUMENT, "%s: null scale pointer", what);
   const size_t need = ca::paged_decode_partials_bytes((int)dtype, 1, num_seqs, num_q_heads,
-                                                      head_dim, max_blocks_per_seq);
+                                                      num_kv_heads, head_dim, max_blocks_per_seq);
   if (need > ca::kNoAllocScratchBytes)
     return fail(CA_INVALID_ARGUMENT,
                 "%s: these sizes need %zu bytes of split partials, more than the %zu bytes of "

@@ -29,7 +29,13 @@
 //   a page multiplies that page's logits and the v scale is folded into P.
 // A sequence that fits one split writes its output directly; otherwise each
 // wave writes (o / l, log2-sum-exp) to the workspace and decode_merge_kernel
-// combines the splits.
+// combines the splits. (This describes the contiguous-cache kernel; the
+// paged kernels below stream pages HBM -> LDS, and larger paged launches
+// balance the pages over one wave per SIMD instead of splitting per
+// sequence: decode_sk_kernel.)
+#include <algorithm>
+#include <atomic>
+#include <climits>
 #include <functional>
 #include <mutex>
 
@@ -363,75 +369,65 @@ struct DmaCfg {
   // a CU, measured within +-1 % on C4 / C3)
   static constexpr int kRing = KIND == kKindPagedFp8 ? 4 : 3;
   static constexpr int kPages = KIND == kKindPagedFp8 ? 128 : kPagesPerWave;
+  // ring of the stream-K walk: the same depth (one wave per SIMD would leave
+  // LDS for deeper rings; 6 FP8 / 4 16-bit steps measured within -0.5 %)
+  static constexpr int kSkRing = KIND == kKindPagedFp8 ? 4 : 3;
   // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
   static_assert(kPages >= kPagesPerWave, "pages per split");
 };
 constexpr int kDmaPolicy = 2;  // global_load_lds cache policy bits: nt
 
-template <typename Tr, int D, int KIND>
-__global__ __launch_bounds__(64) void decode_dma_kernel(
-    const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
-    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
-    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
-    uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
-    int Hkv, int max_blocks, int num_blocks, int max_splits, int n_hc, float scale_log2) {
+// The wave's GQA group of query rows (Gc <= 16 heads from `qrow`, D each) as
+// the B operand of S^T = K^T Q^T: lane (head l16, group grp) holds d = 32 ks
+// + 8 grp .. + 7; rows past Gc are zero.
+template <typename Tr, int D>
+__device__ __forceinline__ void dma_load_q(const uint16_t* __restrict__ qrow, int Gc,
+                                           typename Tr::vec8 (&qv)[D / 32]) {
+  const int lane = threadIdx.x, l16 = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int ks = 0; ks < D / 32; ++ks) {
+    if (l16 < Gc) {
+      qv[ks] = *(const typename Tr::vec8*)(qrow + (size_t)l16 * D + 32 * ks + 8 * grp);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
+    }
+  }
+}
+
+// One wave's walk over pages [p_begin, p_end) (at most DmaCfg<KIND>::kPages)
+// of one (sequence, kv head hk) whose block-table row is `bt_row`. The
+// online-softmax state (o, m_run, l_run) is carried in and out, so a
+// context can be walked in several calls; the ring is filled at the start
+// and drained at the end of each call.
+template <typename Tr, int D, int KIND, int RING = DmaCfg<KIND>::kRing>
+__device__ __forceinline__ void dma_walk(const typename Tr::vec8 (&qv)[D / 32], f32x4 (&o)[D / 16],
+                                         float& m_run, float& l_run, unsigned char* ring,
+                                         const void* __restrict__ Kc, const void* __restrict__ Vc,
+                                         const float* __restrict__ k_scale,
+                                         const float* __restrict__ v_scale, int per_block,
+                                         const int32_t* __restrict__ bt_row, int Hkv, int hk,
+                                         int num_blocks, int p_begin, int p_end, int Lctx,
+                                         float scale_log2, const unsigned char* dummy) {
   using vec8 = typename Tr::vec8;
   using vec4 = typename Tr::vec4;
-  using vec2 = typename Tr::vec2;
   constexpr int NKS = D / 32, NB = D / 16;
   constexpr bool FP8 = KIND == kKindPagedFp8;
   constexpr int ELEM = FP8 ? 1 : 2;
   constexpr int CHUNK = D * 16 * ELEM;        // bytes of one (page, head) chunk
   constexpr int NDMA = CHUNK / 1024;          // 16 B x 64 lanes per load
   constexpr int STAGE = 2 * CHUNK;            // K and V of the step's page
-  constexpr int RING = DmaCfg<KIND>::kRing;
   constexpr int DPS = 2 * NDMA;               // loads per step
   constexpr int KRD = FP8 ? NKS : 2 * NKS;    // LDS reads for one page's K^T operands
   constexpr int kDmaPages = DmaCfg<KIND>::kPages;
   constexpr int PB = kDmaPages / 64;          // page-id registers per lane
   static_assert(kDmaPages % 64 == 0 && PB <= 2, "pages per split");
   static_assert((RING - 1) * DPS <= 63, "vmcnt range");
-  __shared__ __attribute__((aligned(1024))) unsigned char ring[RING * STAGE];
 
   const int lane = threadIdx.x;
-  int w = blockIdx.x;
-  // split index outermost, counted from each sequence's end: the waves of
-  // splits before a sequence's start (none exist) come first and retire at
-  // once, and every sequence's last (partial) split is in the final group
-  const int per_split = (int)(gridDim.x / max_splits);
-  const int from_end = max_splits - 1 - w / per_split;
-  w %= per_split;
-  const int hc = w % n_hc;
-  w /= n_hc;
-  const int hk = w % Hkv;
-  const int n = w / Hkv;
-  const int Gq = Hq / Hkv;
-  const int hq0 = hk * Gq + hc * 16;
-  const int Gc = min(16, Gq - hc * 16);
-  const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
-  const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = max(1, (n_pages + kDmaPages - 1) / kDmaPages);
-  const int split = n_splits - 1 - from_end;
-  if (split < 0) return;
-
   const int l16 = lane & 15, grp = lane >> 4;
-  const int p_begin = split * kDmaPages;
-  const int p_end = min(p_begin + kDmaPages, n_pages);
   const int n_steps = p_end - p_begin;
 
-  vec8 qv[NKS];
-  {
-    const uint16_t* qrow = Q + ((size_t)n * Hq + hq0 + l16) * D;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      if (l16 < Gc) {
-        qv[ks] = *(const vec8*)(qrow + 32 * ks + 8 * grp);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qv[ks][e] = 0;
-      }
-    }
-  }
   // page ids and per-page scales: lane j of register b holds page
   // p_begin + 64 b + j; read back for page index i (uniform) with lane_val
   int pid_lane[PB];
@@ -442,7 +438,7 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     pid_lane[pb] = 0;
     ksc_lane[pb] = vsc_lane[pb] = 1.f;
     if (page < p_end) {
-      pid_lane[pb] = block_tables[(size_t)n * max_blocks + page];
+      pid_lane[pb] = bt_row[page];
       pid_lane[pb] = min(max(pid_lane[pb], 0), num_blocks - 1);
     }
     if (FP8) {
@@ -471,16 +467,13 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   };
   // source offset of this lane's 16 bytes in each 1 KB of a V chunk
   const int v_src = 16 * (FP8 ? lane : lane ^ ((lane >> 4) & 1));
-  const unsigned char* dummy = (const unsigned char*)Q;  // 16 valid bytes for padding loads
   auto issue_step = [&](int step, int slot) {
     unsigned char* base = ring + slot * STAGE;
-    const int page = p_begin + step;
     const bool valid = step < n_steps;
     const int pid = lane_val(pid_lane, valid ? step : 0);
     const size_t chunk = ((size_t)pid * Hkv + hk) * (size_t)CHUNK;
     const unsigned char* kp = (const unsigned char*)Kc + chunk;
     const unsigned char* vp = (const unsigned char*)Vc + chunk;
-    (void)page;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       dma16<kDmaPolicy>(valid ? kp + k_src(i) : dummy, (CA_LDS void*)(base + 1024 * i));
@@ -504,11 +497,6 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
   const uint32_t v_off = FP8 ? (uint32_t)(16 * l16 + 8 * (grp >> 1))
                              : (uint32_t)(16 * ((2 * l16 + (grp >> 1)) ^ ((l16 >> 3) & 1)) + 8 * (grp & 1));
   const uint32_t ring0 = lds_off(ring);
-
-  f32x4 o[NB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf, l_run = 0.f;
 
   // RING steps in flight from the start; a slot is refilled as soon as its
   // LDS reads have returned, so RING steps stay in flight during the math
@@ -639,10 +627,21 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     slot = (slot == RING - 1) ? 0 : slot + 1;
   }
   wait_vmcnt<0>();  // no load may still target this workgroup's LDS when it exits
+}
 
+// The wave's Gc query heads normalised by their sums: written to the output
+// (`out_rows`, head g at + g D) or, when out_rows is null, as a partial for a
+// merge (o / l at po + g po_stride, log2-sum-exp at plse + g plse_stride).
+template <typename Tr, int D>
+__device__ __forceinline__ void dma_finish(const f32x4 (&o)[D / 16], float m_run, float l_run,
+                                           int Gc, uint16_t* __restrict__ out_rows,
+                                           float* __restrict__ po, size_t po_stride,
+                                           float* __restrict__ plse, size_t plse_stride) {
+  using vec2 = typename Tr::vec2;
+  constexpr int NB = D / 16;
+  const int lane = threadIdx.x, l16 = lane & 15, grp = lane >> 4;
   l_run = pair16_sum(l_run);
   l_run = pair32_sum(l_run);
-  const bool single = (n_splits == 1);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int g = 4 * grp + r;
@@ -650,54 +649,235 @@ __global__ __launch_bounds__(64) void decode_dma_kernel(
     const float mg = __shfl(m_run, g, 64);
     if (g >= Gc) continue;
     const float inv = (lg > 0.f) ? 1.f / lg : 0.f;
-    const int hq = hq0 + g;
-    if (single) {
+    if (out_rows) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const vec2 pk = Tr::pack2(o[nb][r] * inv, 0.f);
-        O[((size_t)n * Hq + hq) * D + 16 * nb + l16] = (uint16_t)(__builtin_bit_cast(uint32_t, pk) & 0xffffu);
+        out_rows[(size_t)g * D + 16 * nb + l16] = (uint16_t)(__builtin_bit_cast(uint32_t, pk) & 0xffffu);
       }
     } else {
-      const size_t sl = ((size_t)n * Hq + hq) * max_splits + split;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) ws_o[sl * D + 16 * nb + l16] = o[nb][r] * inv;
-      if (l16 == 0) ws_lse[sl] = (lg > 0.f) ? mg + __log2f(lg) : kNegInf;
+      for (int nb = 0; nb < NB; ++nb) po[g * po_stride + 16 * nb + l16] = o[nb][r] * inv;
+      if (l16 == 0) plse[g * plse_stride] = (lg > 0.f) ? mg + __log2f(lg) : kNegInf;
     }
   }
 }
 
-// Combines the split partials of every (sequence, query head) with more than
-// one split: o = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M). One wave per
-// (sequence, head); each lane owns D/64 output elements. The kernel is bound
-// by memory latency, not bytes: the first kMergeAhead splits' partials are
-// loaded together with the splits' log2-sum-exp, before their maximum is
-// known, so a sequence of up to kMergeAhead splits takes one round trip; the
-// sum runs over the splits in order either way.
-constexpr int kMergeAhead = 16;
-template <typename Tr, int D>
-__global__ __launch_bounds__(64) void decode_merge_kernel(
-    const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
-    const float* __restrict__ ws_lse, void* __restrict__ O, int Hq, int max_splits,
-    int pages_per_split) {
-  constexpr int PER = D / 64;
-  const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
-  const int lane = threadIdx.x;
-  const int Lctx = context_lens ? min(max(0, context_lens[n]), max_tokens) : max_tokens;
+// Split grid: one wave per split of DmaCfg<KIND>::kPages pages of one
+// (sequence, kv head, query-head chunk of <= 16).
+template <typename Tr, int D, int KIND>
+__global__ __launch_bounds__(64) void decode_dma_kernel(
+    const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse, int Hq,
+    int Hkv, int max_blocks, int num_blocks, int max_splits, int n_hc, float scale_log2) {
+  constexpr int NKS = D / 32, NB = D / 16;
+  constexpr int STAGE = 2 * D * 16 * (KIND == kKindPagedFp8 ? 1 : 2);
+  constexpr int kDmaPages = DmaCfg<KIND>::kPages;
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[DmaCfg<KIND>::kRing * STAGE];
+
+  int w = blockIdx.x;
+  // split index outermost, counted from each sequence's end: the waves of
+  // splits before a sequence's start (none exist) come first and retire at
+  // once, and every sequence's last (partial) split is in the final group
+  const int per_split = (int)(gridDim.x / max_splits);
+  const int from_end = max_splits - 1 - w / per_split;
+  w %= per_split;
+  const int hc = w % n_hc;
+  w /= n_hc;
+  const int hk = w % Hkv;
+  const int n = w / Hkv;
+  const int Gq = Hq / Hkv;
+  const int hq0 = hk * Gq + hc * 16;
+  const int Gc = min(16, Gq - hc * 16);
+  const int Lctx = min(max(0, context_lens[n]), max_blocks * kDecodePage);
   const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
-  const int n_splits = (n_pages + pages_per_split - 1) / pages_per_split;
-  if (n_splits <= 1) return;
-  const size_t slot0 = ((size_t)n * Hq + hq) * max_splits;
-  const float lse0 = lane < n_splits ? ws_lse[slot0 + lane] : kNegInf;  // split `lane`
-  const int n_ahead = min(kMergeAhead, n_splits);
+  const int n_splits = max(1, (n_pages + kDmaPages - 1) / kDmaPages);
+  const int split = n_splits - 1 - from_end;
+  if (split < 0) return;
+  const int p_begin = split * kDmaPages;
+  const int p_end = min(p_begin + kDmaPages, n_pages);
+
+  typename Tr::vec8 qv[NKS];
+  dma_load_q<Tr, D>(Q + ((size_t)n * Hq + hq0) * D, Gc, qv);
+  f32x4 o[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf, l_run = 0.f;
+  dma_walk<Tr, D, KIND>(qv, o, m_run, l_run, ring, Kc, Vc, k_scale, v_scale, per_block,
+                        block_tables + (size_t)n * max_blocks, Hkv, hk, num_blocks, p_begin, p_end,
+                        Lctx, scale_log2, (const unsigned char*)Q);
+  if (n_splits == 1) {
+    dma_finish<Tr, D>(o, m_run, l_run, Gc, O + ((size_t)n * Hq + hq0) * D, nullptr, 0, nullptr, 0);
+  } else {
+    const size_t sl = ((size_t)n * Hq + hq0) * max_splits + split;
+    dma_finish<Tr, D>(o, m_run, l_run, Gc, nullptr, ws_o + sl * D, (size_t)max_splits * D,
+                      ws_lse + sl, (size_t)max_splits);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Balanced ("stream-K") paged decode. The work units are (sequence, kv head,
+// query-head chunk, page) in that order (a sequence's units are its pages
+// times its Hkv * n_hc segments); wave w of W takes units [w T / W,
+// (w + 1) T / W) of the T in the launch, so every wave streams the same
+// number of pages whatever the context lengths are; W is one wave per SIMD
+// of the device, all resident at once (each wave pays its start once). A wave
+// walks its range segment by segment (a segment: one (sequence, kv head,
+// chunk), walked kPages pages per ring fill); a segment inside the range is
+// written as output, one cut by the range's start or end as a partial (at
+// most two per wave: slot 0 for the first piece, 1 for the last), which
+// decode_sk_merge_kernel combines. Every wave scans the context lengths
+// itself to find where its range starts (N <= kSkMaxSeqs, 16 per lane);
+// wave 0 also stores the inclusive prefix of units per sequence for the
+// merge.
+// Workspace: [W][2][GMAX] x D floats of o / l, [W][2][GMAX] floats of
+// log2-sum-exp, then N ints of prefix (GMAX = min(16, Hq / Hkv)).
+// ---------------------------------------------------------------------------
+constexpr int kSkMaxSeqs = 1024;
+constexpr int kSkMinPages = 16;   // fewer waves when the launch has < 16 pages each
+
+__device__ __forceinline__ int sk_waves_used(int grid, int T) {
+  return max(1, min(grid, T / kSkMinPages));
+}
+
+template <typename Tr, int D, int KIND>
+__global__ __launch_bounds__(64) void decode_sk_kernel(
+    const uint16_t* __restrict__ Q, const void* __restrict__ Kc, const void* __restrict__ Vc,
+    const float* __restrict__ k_scale, const float* __restrict__ v_scale, int per_block,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ context_lens,
+    uint16_t* __restrict__ O, float* __restrict__ ws_o, float* __restrict__ ws_lse,
+    int32_t* __restrict__ ws_prefix, int N, int Hq, int Hkv, int max_blocks, int num_blocks,
+    int n_hc, float scale_log2) {
+  constexpr int NKS = D / 32, NB = D / 16;
+  constexpr int STAGE = 2 * D * 16 * (KIND == kKindPagedFp8 ? 1 : 2);
+  constexpr int kDmaPages = DmaCfg<KIND>::kPages;
+  constexpr int NCH = kSkMaxSeqs / 64;
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[DmaCfg<KIND>::kSkRing * STAGE];
+
+  const int lane = threadIdx.x;
+  const int segs = Hkv * n_hc;
+  const int max_tokens = max_blocks * kDecodePage;
+  // inclusive prefix of units over sequences: sequence 64 c + lane in incl[c]
+  // (lanes and chunks past N hold the total)
+  int incl[NCH];
+  int carry = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    incl[c] = carry;
+    if (64 * c < N) {
+      const int n = 64 * c + lane;
+      int u = 0;
+      if (n < N) u = ((min(max(0, context_lens[n]), max_tokens) + kDecodePage - 1) / kDecodePage) * segs;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(u, off, 64);
+        if (lane >= off) u += t;
+      }
+      incl[c] = carry + u;
+      carry = __shfl(incl[c], 63, 64);
+    }
+  }
+  const int T = carry;
+  if (blockIdx.x == 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (64 * c + lane < N) ws_prefix[64 * c + lane] = incl[c];
+  }
+  if (T == 0) return;
+  const int W = sk_waves_used((int)gridDim.x, T);
+  const int w = blockIdx.x;
+  if (w >= W) return;
+  const int a = (int)((long long)w * T / W), b = (int)((long long)(w + 1) * T / W);
+  if (a == b) return;
+
+  // sequence holding unit a: the number of sequences whose units end at or before it
+  int n = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) n += __popcll(__ballot(incl[c] <= a));
+  auto incl_at = [&](int i) CA_INLINE {   // i uniform, < kSkMaxSeqs
+    int v = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      if (c == (i >> 6)) v = incl[c];
+    return __builtin_amdgcn_readlane(v, i & 63);
+  };
+  // from here on the prefix comes from the lengths (incl[] is dead in the walk)
+  int exc = n ? incl_at(n - 1) : 0, inc = incl_at(n);
+  auto seq_units = [&](int i) CA_INLINE {
+    return ((min(max(0, context_lens[i]), max_tokens) + kDecodePage - 1) / kDecodePage) * segs;
+  };
+
+  const int Gq = Hq / Hkv;
+  const int GMAX = min(16, Gq);
+  typename Tr::vec8 qv[NKS];
+  f32x4 o[NB];
+  int u = a;
+  while (u < b) {
+    const int pages = (inc - exc) / segs;   // >= 1: sequence n holds unit u
+    const int r = u - exc;
+    const int seg = r / pages, p0 = r - seg * pages;
+    const int len = min(b - u, pages - p0);
+    const int hk = seg / n_hc, hc = seg - hk * n_hc;
+    const int hq0 = hk * Gq + hc * 16, Gc = min(16, Gq - hc * 16);
+    const int Lctx = min(max(0, context_lens[n]), max_tokens);
+    dma_load_q<Tr, D>(Q + ((size_t)n * Hq + hq0) * D, Gc, qv);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegInf, l_run = 0.f;
+    // ring fills at multiples of kPages pages of the context (so waves that
+    // share a segment do not refill in step)
+    for (int p = p0; p < p0 + len;) {
+      const int pe = min(p0 + len, (p / kDmaPages + 1) * kDmaPages);
+      dma_walk<Tr, D, KIND, DmaCfg<KIND>::kSkRing>(
+          qv, o, m_run, l_run, ring, Kc, Vc, k_scale, v_scale, per_block,
+          block_tables + (size_t)n * max_blocks, Hkv, hk, num_blocks, p, pe, Lctx, scale_log2,
+          (const unsigned char*)Q);
+      p = pe;
+    }
+    if (p0 == 0 && len == pages) {
+      dma_finish<Tr, D>(o, m_run, l_run, Gc, O + ((size_t)n * Hq + hq0) * D, nullptr, 0, nullptr, 0);
+    } else {
+      const size_t row = (size_t)(2 * w + (u == a ? 0 : 1)) * GMAX;
+      dma_finish<Tr, D>(o, m_run, l_run, Gc, nullptr, ws_o + row * D, D, ws_lse + row, 1);
+    }
+    u += len;
+    if (u < b && u == inc) {   // the sequence is done: the next one with units
+      do {
+        ++n;
+        exc = inc;
+        inc = exc + seq_units(n);
+      } while (inc == exc);
+    }
+  }
+}
+
+// Combines n_parts partials (o / l rows and log2-sum-exp values, partial k at
+// row idx(k)) into output row `orow`: o = sum_k 2^(lse_k - M) o_k / sum_k
+// 2^(lse_k - M). Each lane owns D/64 output elements. Bound by memory
+// latency, not bytes: the first kMergeAhead partials are loaded together with
+// the log2-sum-exp values, before their maximum is known, so up to
+// kMergeAhead partials take one round trip; the sum runs over the partials in
+// order either way.
+constexpr int kMergeAhead = 16;
+template <typename Tr, int D, typename Idx>
+__device__ __forceinline__ void merge_rows(int n_parts, Idx idx, const float* __restrict__ ws_o,
+                                           const float* __restrict__ ws_lse, void* __restrict__ O,
+                                           size_t orow) {
+  constexpr int PER = D / 64;
+  const int lane = threadIdx.x;
+  const float lse0 = lane < n_parts ? ws_lse[idx(lane)] : kNegInf;  // partial `lane`
+  const int n_ahead = min(kMergeAhead, n_parts);
   float part[kMergeAhead][PER];
 #pragma unroll
   for (int j = 0; j < kMergeAhead; ++j)
     if (j < n_ahead) {
 #pragma unroll
-      for (int i = 0; i < PER; ++i) part[j][i] = ws_o[(slot0 + j) * D + lane * PER + i];
+      for (int i = 0; i < PER; ++i) part[j][i] = ws_o[idx(j) * D + lane * PER + i];
     }
   float M = lse0;
-  for (int s = lane + 64; s < n_splits; s += 64) M = __builtin_fmaxf(M, ws_lse[slot0 + s]);
+  for (int s = lane + 64; s < n_parts; s += 64) M = __builtin_fmaxf(M, ws_lse[idx(s)]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) M = __builtin_fmaxf(M, __shfl_xor(M, off, 64));
   float wsum = 0.f;
@@ -705,11 +885,11 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
 #pragma unroll
   for (int i = 0; i < PER; ++i) acc[i] = 0.f;
   if (M != kNegInf) {
-    for (int s0 = 0; s0 < n_splits; s0 += 64) {
+    for (int s0 = 0; s0 < n_parts; s0 += 64) {
       const int s = s0 + lane;
-      const float lse = s0 == 0 ? lse0 : (s < n_splits) ? ws_lse[slot0 + s] : kNegInf;
+      const float lse = s0 == 0 ? lse0 : (s < n_parts) ? ws_lse[idx(s)] : kNegInf;
       const float wl = (lse == kNegInf) ? 0.f : fast_exp2(lse - M);
-      const int cnt = min(64, n_splits - s0);
+      const int cnt = min(64, n_parts - s0);
       int j0 = 0;
       if (s0 == 0) {
 #pragma unroll
@@ -726,7 +906,7 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
       for (int j = j0; j < cnt; ++j) {
         const float wj = __shfl(wl, j, 64);
         wsum += wj;
-        const float* src = ws_o + (slot0 + s0 + j) * D + lane * PER;
+        const float* src = ws_o + idx(s0 + j) * D + lane * PER;
 #pragma unroll
         for (int i = 0; i < PER; ++i) acc[i] += wj * src[i];
       }
@@ -734,7 +914,60 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) Tr::store(O, ((size_t)n * Hq + hq) * D + lane * PER + i, acc[i] * inv);
+  for (int i = 0; i < PER; ++i) Tr::store(O, orow + lane * PER + i, acc[i] * inv);
+}
+
+// Split-grid merge: one wave per (sequence, query head) with more than one
+// split; the partials of split s at [n][hq][s].
+template <typename Tr, int D>
+__global__ __launch_bounds__(64) void decode_merge_kernel(
+    const int32_t* __restrict__ context_lens, int max_tokens, const float* __restrict__ ws_o,
+    const float* __restrict__ ws_lse, void* __restrict__ O, int Hq, int max_splits,
+    int pages_per_split) {
+  const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
+  const int Lctx = context_lens ? min(max(0, context_lens[n]), max_tokens) : max_tokens;
+  const int n_pages = (Lctx + kDecodePage - 1) / kDecodePage;
+  const int n_splits = (n_pages + pages_per_split - 1) / pages_per_split;
+  if (n_splits <= 1) return;
+  const size_t slot0 = ((size_t)n * Hq + hq) * max_splits;
+  merge_rows<Tr, D>(n_splits, [&](int k) CA_INLINE { return slot0 + k; }, ws_o, ws_lse, O,
+                    ((size_t)n * Hq + hq) * D);
+}
+
+// Stream-K merge: one wave per (sequence, query head). Its segment's units
+// [u0, u1) were walked by waves wave_of(u0) .. wave_of(u1 - 1); a segment of
+// one wave was written by it, an empty one (no context) is written here as
+// zeros, any other is merged from its waves' partials (the first wave's slot
+// 1 when the segment is not where that wave starts, slot 0 otherwise).
+template <typename Tr, int D>
+__global__ __launch_bounds__(64) void decode_sk_merge_kernel(
+    const int32_t* __restrict__ ws_prefix, const float* __restrict__ ws_o,
+    const float* __restrict__ ws_lse, void* __restrict__ O, int N, int Hq, int Hkv, int n_hc,
+    int grid) {
+  constexpr int PER = D / 64;
+  const int n = blockIdx.x / Hq, hq = blockIdx.x % Hq;
+  const int lane = threadIdx.x;
+  const int Gq = Hq / Hkv, GMAX = min(16, Gq);
+  const int hk = hq / Gq, j = hq - hk * Gq, hc = j / 16, g = j - 16 * hc;
+  const int segs = Hkv * n_hc;
+  const int exc = n ? ws_prefix[n - 1] : 0, inc = ws_prefix[n];
+  const int pages = (inc - exc) / segs;
+  const size_t orow = ((size_t)n * Hq + hq) * D;
+  if (pages == 0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) Tr::store(O, orow + lane * PER + i, 0.f);
+    return;
+  }
+  const int T = ws_prefix[N - 1];
+  const int W = sk_waves_used(grid, T);
+  const int u0 = exc + (hk * n_hc + hc) * pages, u1 = u0 + pages;
+  auto wave_of = [&](int u) { return (int)(((long long)(u + 1) * W - 1) / T); };
+  const int w0 = wave_of(u0), w1 = wave_of(u1 - 1);
+  if (w0 == w1) return;
+  const int s0 = ((long long)w0 * T / W < u0) ? 1 : 0;
+  merge_rows<Tr, D>(w1 - w0 + 1,
+                    [&](int k) CA_INLINE { return (size_t)(2 * (w0 + k) + (k == 0 ? s0 : 0)) * GMAX + g; },
+                    ws_o, ws_lse, O, orow);
 }
 
 // Bytes of split partials for max_splits splits per (sequence, query head):
@@ -751,6 +984,65 @@ size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
   return split_partials_bytes(N, Hq, D, pages / kPagesPerWave + (pages % kPagesPerWave != 0));
 }
 
+// Waves per CU of a stream-K launch: one per SIMD. Every wave streams the
+// same bytes, so a CU must hold a multiple of four for its SIMDs to finish
+// together, and one per SIMD measured best.
+constexpr int kSkWavesPerCu = 4;
+
+// Grid of the stream-K decode on the current device (0 if unknown), cached
+// per device like device_cus.
+template <typename Tr, int D, int KIND>
+static int sk_grid() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int g = cached[dev].load(std::memory_order_relaxed);
+  if (g == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&decode_sk_kernel<Tr, D, KIND>), 64, 0) !=
+        hipSuccess)
+      return 0;
+    g = std::min(per_cu, kSkWavesPerCu) * device_cus();
+    cached[dev].store(g, std::memory_order_relaxed);
+  }
+  return g;
+}
+
+static size_t sk_partials_bytes(int grid, int N, int Gq, int D) {
+  return (size_t)2 * grid * std::min(16, Gq) * (size_t)(D + 1) * sizeof(float) +
+         (size_t)N * sizeof(int32_t);
+}
+
+// How a paged decode launch splits its work: stream-K (grid > 0) when its
+// partials fit the workspace every caller provides (decode_workspace_bytes)
+// and the sequences fit the prefix registers; otherwise the split grid.
+struct PagedPlan {
+  int grid = 0;          // stream-K waves, 0 for the split grid
+  int max_splits = 1;    // split grid: splits of the longest context
+  size_t bytes = 0;      // partials the launch writes
+};
+template <typename Tr, int D, int KIND>
+static PagedPlan paged_plan(int N, int Hq, int Hkv, int max_blocks) {
+  PagedPlan p;
+  constexpr int kPages = DmaCfg<KIND>::kPages;
+  p.max_splits = std::max(1, max_blocks / kPages + (max_blocks % kPages != 0));
+  const int Gq = Hq / Hkv;
+  const int n_hc = (Gq + 15) / 16;
+  if (p.max_splits > 1 && N <= kSkMaxSeqs &&
+      (long long)N * max_blocks * Hkv * n_hc <= (long long)INT_MAX) {
+    const int g = sk_grid<Tr, D, KIND>();
+    const size_t need = sk_partials_bytes(g, N, Gq, D);
+    if (g > 0 && need <= decode_workspace_bytes(N, Hq, D, max_blocks * kDecodePage)) {
+      p.grid = g;
+      p.bytes = need;
+      return p;
+    }
+  }
+  p.bytes = split_partials_bytes(N, Hq, D, p.max_splits);
+  return p;
+}
+
 template <typename Tr, int D, int KIND>
 static hipError_t launch_paged_decode_t(const void* q, const void* kc, const void* vc,
                                         const float* k_scale, const float* v_scale, int per_block,
@@ -759,15 +1051,28 @@ static hipError_t launch_paged_decode_t(const void* q, const void* kc, const voi
                                         float scale, void* ws, size_t ws_bytes,
                                         hipStream_t stream) {
   const int max_tokens = max_blocks * kDecodePage;
-  // splits of DmaCfg<KIND>::kPages pages (the workspace the entry points
-  // require, sized for kPagesPerWave-page splits, covers them)
-  const int max_splits = max(1, (max_blocks + DmaCfg<KIND>::kPages - 1) / DmaCfg<KIND>::kPages);
   const int Gq = Hq / Hkv;
   const int n_hc = (Gq + 15) / 16;
-  const size_t need = split_partials_bytes(N, Hq, D, max_splits);
-  if (ws_bytes < need) return hipErrorInvalidValue;
+  const PagedPlan plan = paged_plan<Tr, D, KIND>(N, Hq, Hkv, max_blocks);
+  if (ws_bytes < plan.bytes) return hipErrorInvalidValue;
+  if (plan.grid > 0) {
+    const size_t rows = (size_t)2 * plan.grid * std::min(16, Gq);
+    float* ws_o = (float*)ws;
+    float* ws_lse = ws_o + rows * D;
+    int32_t* ws_prefix = (int32_t*)(ws_lse + rows);
+    hipLaunchKernelGGL((decode_sk_kernel<Tr, D, KIND>), dim3((unsigned)plan.grid), dim3(64), 0,
+                       stream, (const uint16_t*)q, kc, vc, k_scale, v_scale, per_block, bt, lens,
+                       (uint16_t*)out, ws_o, ws_lse, ws_prefix, N, Hq, Hkv, max_blocks,
+                       num_blocks, n_hc, scale * kLog2e);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((decode_sk_merge_kernel<Tr, D>), dim3((unsigned)(N * Hq)), dim3(64), 0,
+                       stream, ws_prefix, ws_o, ws_lse, out, N, Hq, Hkv, n_hc, plan.grid);
+    return hipGetLastError();
+  }
+  const int max_splits = plan.max_splits;
   float* ws_o = (float*)ws;
-  float* ws_lse = need ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
+  float* ws_lse = plan.bytes ? ws_o + (size_t)N * Hq * max_splits * D : nullptr;
   const long long total_waves = (long long)N * Hkv * n_hc * max_splits;
   if (total_waves == 0) return hipSuccess;
   if (total_waves > 0x7fffffffLL) return hipErrorInvalidValue;
@@ -1185,13 +1490,22 @@ hipError_t with_noalloc_scratch(hipStream_t stream, const std::function<hipError
   return e;
 }
 
-size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int D,
+size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int Hkv, int D,
                                    int max_blocks_per_seq) {
-  const int pages_per_split = (dtype == kDtypeF32) ? kPagesPerWave
-                              : cache_kind == 0    ? DmaCfg<kKindPaged16>::kPages
-                                                   : DmaCfg<kKindPagedFp8>::kPages;
-  return split_partials_bytes(N, Hq, D, max_blocks_per_seq / pages_per_split +
-                                            (max_blocks_per_seq % pages_per_split != 0));
+  if (dtype == kDtypeF32)
+    return split_partials_bytes(N, Hq, D, max_blocks_per_seq / kPagesPerWave +
+                                              (max_blocks_per_seq % kPagesPerWave != 0));
+#define CA_PLAN(TR, DD, KIND) \
+  if (D == DD) return paged_plan<TR, DD, KIND>(N, Hq, Hkv, max_blocks_per_seq).bytes;
+  if (cache_kind == 0) {
+    if (dtype == kDtypeBF16) { CA_PLAN(BF16, 64, kKindPaged16) CA_PLAN(BF16, 128, kKindPaged16) }
+    if (dtype == kDtypeF16) { CA_PLAN(F16, 64, kKindPaged16) CA_PLAN(F16, 128, kKindPaged16) }
+  } else {
+    if (dtype == kDtypeBF16) { CA_PLAN(BF16, 64, kKindPagedFp8) CA_PLAN(BF16, 128, kKindPagedFp8) }
+    if (dtype == kDtypeF16) { CA_PLAN(F16, 64, kKindPagedFp8) CA_PLAN(F16, 128, kKindPagedFp8) }
+  }
+#undef CA_PLAN
+  return 0;
 }
 
 hipError_t launch_flash_decode(int dtype, const void* q, const void* k, const void* v, void* o,

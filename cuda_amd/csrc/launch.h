@@ -120,10 +120,10 @@ hipError_t launch_paged_decode(int dtype, int cache_kind, const void* q, const v
                                int D, int max_blocks_per_seq, int num_blocks, float scale,
                                void* ws, size_t ws_bytes, hipStream_t stream);
 
-// Bytes of split partials a paged decode launch writes (the exact minimum
-// of its workspace; the entry points require decode_workspace_bytes, which
-// is at least this).
-size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int D,
+// Bytes of partials a paged decode launch writes on the current device (the
+// exact minimum of its workspace; the entry points require
+// decode_workspace_bytes, which is at least this).
+size_t paged_decode_partials_bytes(int dtype, int cache_kind, int N, int Hq, int Hkv, int D,
                                    int max_blocks_per_seq);
 
 // The allocation-free paged decode's scratch (decode.hip): a file-scope

@@ -132,3 +132,17 @@ def mx_inputs(b, h, s, d, device, seed=0):
 
 def default_scale(d):
     return 1.0 / math.sqrt(d)
+
+
+def balanced_walk_taken(n, hq, hkv, d, max_blocks, fp8):
+    """Whether a paged decode launch of these sizes takes the balanced
+    (stream-K) walk of decode.hip (paged_plan there): more than one split of
+    the longest context, at most 1024 sequences, and the walk's partials (one
+    wave per SIMD, two rows of min(16, Hq/Hkv) heads per wave, plus the
+    sequences' prefix) within the workspace every caller provides
+    (N * Hq * ceil(max_blocks / 64) rows of D + 1 floats)."""
+    split_pages = 128 if fp8 else 64
+    grid = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    sk = 2 * grid * min(16, hq // hkv) * (d + 1) * 4 + 4 * n
+    contract = n * hq * (-(-max_blocks // 64)) * (d + 1) * 4
+    return max_blocks > split_pages and n <= 1024 and sk <= contract

@@ -10,6 +10,10 @@
 * async_flash_decode / flash_decode — the reference grid
   (tests/test_attention.py:76-86: kv_len in {1, 63, 64, 1000}) plus GQA and
   split lengths;
+* the balanced (stream-K) walk the paged kernels take for larger batches:
+  ragged and empty contexts, a context cut into more partials than the merge
+  loads at once (and more than 64), fewer pages than waves, GQA groups above
+  16, head dim 64, both cache kinds and scale forms;
 * the committed golden vectors.
 """
 import os
@@ -20,7 +24,8 @@ import torch
 
 import cuda_llm
 import oracle
-from _util import TOL_16BIT, TOL_FP8, assert_close, build_paged, paged_oracle, to_np
+from _util import (TOL_16BIT, TOL_FP8, assert_close, balanced_walk_taken, build_paged,
+                   paged_oracle, to_np)
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "golden.npz")
@@ -280,6 +285,85 @@ def test_baseline_c4_shape(dev):
     o = to_np(out)
     for j, n in enumerate(seqs):
         assert_close(o[n], ref[j], **TOL_FP8, name=f"C4 sequence {n}")
+
+
+def _check_balanced(case, tol, fp8, name):
+    n, hq, d = case["query"].shape
+    hkv = case["key_cache"].shape[1]
+    assert balanced_walk_taken(n, hq, hkv, d, case["block_tables"].shape[1], fp8), \
+        f"{name}: these sizes do not take the balanced walk"
+    out = _run_paged(case)
+    again = _run_paged(case)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), f"{name}: not reproducible"
+    ref = paged_oracle(case)
+    o = to_np(out)
+    for i in range(n):
+        assert_close(o[i], ref[i], **tol, name=f"{name} sequence {i}")
+    return out
+
+
+_EDGE_LENS = [0, 1, 15, 16, 17, 1023, 1024, 1025, 2047, 2048, 2049, 4095, 4096, 4097, 8191, 8192,
+              0, 0, 0, 5000]
+
+
+@pytest.mark.parametrize("dtype,fp8,per_block", [(torch.bfloat16, False, True),
+                                                 (torch.float16, False, True),
+                                                 (torch.bfloat16, True, True),
+                                                 (torch.float16, True, False)])
+def test_balanced_walk_ragged(dev, dtype, fp8, per_block):
+    """96 sequences, GQA 32/8: the edge lengths of a 64- / 128-page split
+    (empty ones among them, written as zeros) plus random lengths up to 8192."""
+    g = torch.Generator().manual_seed(11)
+    lens = _EDGE_LENS + torch.randint(0, 8193, (96 - len(_EDGE_LENS),), generator=g).tolist()
+    case = build_paged(lens, 32, 8, 128, dtype, dev, fp8=fp8, per_block=per_block, pool=30000,
+                       seed=11)
+    out = _check_balanced(case, TOL_FP8 if fp8 else TOL_16BIT, fp8, "balanced ragged")
+    assert torch.all(out[0] == 0) and torch.all(out[16:19] == 0)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_balanced_walk_long_context(dev, fp8):
+    """One 65536-token context among 63 short ones: each of its kv heads is
+    cut across ~100 waves, so its merge takes more partials than it loads
+    ahead (16) and than one pass of lanes (64)."""
+    g = torch.Generator().manual_seed(12)
+    lens = [65536] + torch.randint(1, 200, (63,), generator=g).tolist()
+    case = build_paged(lens, 32, 8, 128, torch.bfloat16, dev, fp8=fp8, seed=12)
+    _check_balanced(case, TOL_FP8 if fp8 else TOL_16BIT, fp8, "balanced long")
+
+
+def test_balanced_walk_wide_groups_and_head_dim_64(dev):
+    """GQA groups of 32 query heads (two 16-head chunks per kv head) at head
+    dim 128, and head dim 64."""
+    g = torch.Generator().manual_seed(13)
+    lens = torch.randint(0, 8193, (80,), generator=g).tolist()
+    case = build_paged(lens, 64, 2, 128, torch.bfloat16, dev, pool=30000, seed=13)
+    _check_balanced(case, TOL_16BIT, False, "balanced Gq=32")
+    lens = torch.randint(0, 8193, (64,), generator=g).tolist()
+    for fp8 in (False, True):
+        case = build_paged(lens, 32, 8, 64, torch.bfloat16, dev, fp8=fp8, pool=20000, seed=14)
+        _check_balanced(case, TOL_FP8 if fp8 else TOL_16BIT, fp8, f"balanced D=64 fp8={fp8}")
+
+
+def _widen(case, width):
+    t = case["block_tables"]
+    case["block_tables"] = torch.cat(
+        [t, torch.zeros(t.shape[0], width - t.shape[1], dtype=t.dtype, device=t.device)], 1).contiguous()
+    return case
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_balanced_walk_few_pages(dev, fp8):
+    """Block tables 1024 entries wide with little context: fewer than 16
+    pages per wave (the launch uses fewer waves), fewer pages than 16 in all
+    (one wave), and no context at all (every row zero)."""
+    cases = [[0] * 61 + [17, 3000, 9000], [0] * 63 + [5], [0] * 64]
+    for lens in cases:
+        case = _widen(build_paged(lens, 32, 8, 128, torch.bfloat16, dev, fp8=fp8, pool=1200,
+                                  seed=15), 1024)
+        out = _check_balanced(case, TOL_FP8 if fp8 else TOL_16BIT, fp8, f"few pages {lens[-3:]}")
+        assert torch.all(out[:61] == 0)
 
 
 @pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, (2048 * 256 * 8 + 7) * 16])

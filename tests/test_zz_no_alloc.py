@@ -14,7 +14,7 @@ import torch
 
 import cuda_amd._lib as L
 import cuda_llm
-from _util import TOL_FP8, assert_close, build_paged, paged_oracle, to_np
+from _util import TOL_FP8, assert_close, balanced_walk_taken, build_paged, paged_oracle, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -59,6 +59,26 @@ def test_noalloc_matches_workspace_form_twice(dev, dtype):
     assert torch.all(_noalloc(big)[3] == 0)  # empty context -> zero row
 
 
+def test_noalloc_balanced_walk_twice(dev):
+    """Sizes that take the balanced (stream-K) walk, whose partials and
+    per-sequence prefix also live in the scratch: two calls in a row, the
+    second smaller, each bit for bit the workspace form's and within the FP8
+    tolerance of the oracle."""
+    g = torch.Generator().manual_seed(5)
+    big = build_paged(torch.randint(0, 16385, (100,), generator=g).tolist(), 32, 8, 128,
+                      torch.bfloat16, dev, fp8=True, per_block=True, seed=5)
+    small = build_paged(torch.randint(0, 8193, (64,), generator=g).tolist(), 32, 8, 128,
+                        torch.bfloat16, dev, fp8=True, per_block=False, seed=6)
+    for case, name in ((big, "first"), (small, "second, smaller")):
+        n, hq, d = case["query"].shape
+        assert balanced_walk_taken(n, hq, 8, d, case["block_tables"].shape[1], True), name
+        out = _noalloc(case)
+        ref = _with_workspace(case)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"{name}: differs from ca_fp8_paged_attention"
+        assert_close(to_np(out), paged_oracle(case, dtype=np.float64), **TOL_FP8, name=name)
+
+
 def test_noalloc_two_streams(dev):
     """Calls on two streams, issued back to back with no host wait between,
     share the scratch: the second call's stream waits for the first call on
@@ -80,10 +100,11 @@ def test_noalloc_two_streams(dev):
 
 def test_noalloc_rejects_sizes_beyond_scratch(dev):
     case = build_paged([16], 32, 8, 128, torch.bfloat16, dev, fp8=True, per_block=True)
-    # a table 2048 blocks wide for 512 sequences needs 512*32*16*129*4 bytes of partials
-    q = torch.zeros(512, 32, 128, dtype=torch.bfloat16, device=dev)
-    tables = torch.zeros(512, 2048, dtype=torch.int32, device=dev)
-    lens = torch.zeros(512, dtype=torch.int32, device=dev)
+    # 1100 sequences (more than the balanced walk's 1024, so the split grid)
+    # with a table 2048 blocks wide need 1100*32*16*129*4 bytes of partials
+    q = torch.zeros(1100, 32, 128, dtype=torch.bfloat16, device=dev)
+    tables = torch.zeros(1100, 2048, dtype=torch.int32, device=dev)
+    lens = torch.zeros(1100, dtype=torch.int32, device=dev)
     big = dict(case, query=q, block_tables=tables, context_lens=lens)
     with pytest.raises(RuntimeError, match="scratch"):
         _noalloc(big)
