@@ -51,53 +51,65 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t e) {
   return __uint_as_float(e << 23);
 }
 
-// One wave per 8 rows of V (1024 codes -> 2 KB of bf16): lane l converts
-// codes 8l .. 8l + 7 and 512 + 8l .. 512 + 8l + 7 of the wave's rows, so every
+// One wave per kMxPrepRows rows of V (kMxPrepRows x 128 codes): lane l
+// converts codes 8l .. 8l + 7 of each 512-code quarter-block (4 rows), so every
 // load instruction reads one contiguous 512 B and every store instruction
-// writes one contiguous 1 KB. (16 codes per lane, two 16-byte stores 32 bytes
-// apart, ran C5's 50 MB at ~3.4 TB/s.) With float scales (F32SC) lane l also
-// converts one of the rows' q or k scales (row l / 8, block l % 4; q when
-// (l / 4) % 2 == 0) into e8m0.
+// writes one contiguous 1 KB of bf16; all of the wave's loads are issued
+// before its first conversion, so a wave keeps kMxPrepRows x 128 bytes in
+// flight. C5's 50 MB (kernel averages, one box): 8 rows per wave 11.8 µs,
+// 16 rows 11.2 µs, 32 rows 14.8 µs (too few waves); 16 codes per lane with
+// two 16-byte stores 32 bytes apart ran at ~3.4 TB/s. With float scales (F32SC)
+// lane l also converts one q or k scale per 8 rows (row l / 8, block l % 4;
+// q when (l / 4) % 2 == 0) into e8m0.
+constexpr int kMxPrepRows = 16;
 template <bool F32SC>
 __global__ __launch_bounds__(256) void mx_prepare_kernel(
     const uint8_t* __restrict__ V, const void* __restrict__ VS, const void* __restrict__ QSf,
     const void* __restrict__ KSf, uint16_t* __restrict__ Vb, uint8_t* __restrict__ QSb,
     uint8_t* __restrict__ KSb, long long n_rows) {
-  constexpr int D = 128, NB = D / 32;
+  constexpr int D = 128, NB = D / 32, NH = kMxPrepRows / 4;
   const int lane = threadIdx.x & 63;
-  const long long row0 = (((long long)blockIdx.x * 256 + threadIdx.x) >> 6) * 8;
+  const long long row0 = (((long long)blockIdx.x * 256 + threadIdx.x) >> 6) * kMxPrepRows;
   if (row0 >= n_rows) return;
   if (F32SC) {
-    const long long r = row0 + (lane >> 3);
-    const int blk = lane & 3;
-    if (r < n_rows) {
-      const bool isq = ((lane >> 2) & 1) == 0;
-      uint32_t e;
-      float_to_e8m0(((const float*)(isq ? QSf : KSf))[r * NB + blk], &e);
-      (isq ? QSb : KSb)[r * NB + blk] = (uint8_t)e;
+#pragma unroll
+    for (int g = 0; g < kMxPrepRows / 8; ++g) {
+      const long long r = row0 + 8 * g + (lane >> 3);
+      const int blk = lane & 3;
+      if (r < n_rows) {
+        const bool isq = ((lane >> 2) & 1) == 0;
+        uint32_t e;
+        float_to_e8m0(((const float*)(isq ? QSf : KSf))[r * NB + blk], &e);
+        (isq ? QSb : KSb)[r * NB + blk] = (uint8_t)e;
+      }
     }
   }
+  const int blk = (lane & 15) >> 2;  // MX block of the lane's 8 codes
+  u32x2 cc[NH];
+  float sc[NH];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const long long c = row0 * D + 512 * h + 8 * lane;  // the lane's first code
+  for (int h = 0; h < NH; ++h) {
     const long long r = row0 + 4 * h + (lane >> 4);
     if (r >= n_rows) continue;
-    const int blk = (lane & 15) >> 2;  // MX block of the 8 codes
-    float sc;
+    cc[h] = *(const u32x2*)(V + row0 * D + 512 * h + 8 * lane);
     if (F32SC) {
       uint32_t e;
       float_to_e8m0(((const float*)VS)[r * NB + blk], &e);
-      sc = e8m0_to_float(e);
+      sc[h] = e8m0_to_float(e);
     } else {
-      sc = e8m0_to_float(((const uint8_t*)VS)[r * NB + blk]);
+      sc[h] = e8m0_to_float(((const uint8_t*)VS)[r * NB + blk]);
     }
-    const u32x2 cc = *(const u32x2*)(V + c);
+  }
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const long long r = row0 + 4 * h + (lane >> 4);
+    if (r >= n_rows) continue;
     u32x4 w;
-    w[0] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[0], sc));
-    w[1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[0], sc));
-    w[2] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[1], sc));
-    w[3] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[1], sc));
-    *(u32x4*)(Vb + c) = w;
+    w[0] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[h][0], sc[h]));
+    w[1] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[h][0], sc[h]));
+    w[2] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<false>(cc[h][1], sc[h]));
+    w[3] = __builtin_bit_cast(uint32_t, e4m3x2_to_bf16_scaled<true>(cc[h][1], sc[h]));
+    *(u32x4*)(Vb + row0 * D + 512 * h + 8 * lane) = w;
   }
 }
 
@@ -166,7 +178,7 @@ hipError_t launch_mxfp8(int out_dtype, int scale_kind, const uint8_t* q, const v
   w += align256((size_t)rows * D * 2);
   const uint8_t* qs8 = (const uint8_t*)qs;
   const uint8_t* ks8 = (const uint8_t*)ks;
-  const long long blocks = (rows + 31) / 32;  // 4 waves of 8 rows per block
+  const long long blocks = (rows + 4 * kMxPrepRows - 1) / (4 * kMxPrepRows);  // 4 waves per block
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   if (scale_kind == 1) {
     uint8_t* qsb = w;
