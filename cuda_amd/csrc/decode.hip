@@ -372,6 +372,8 @@ struct DmaCfg {
   // ring of the stream-K walk: the same depth (one wave per SIMD would leave
   // LDS for deeper rings; 6 FP8 / 4 16-bit steps measured within -0.5 %)
   static constexpr int kSkRing = KIND == kKindPagedFp8 ? 4 : 3;
+  // pages per ring fill of the stream-K walk
+  static constexpr int kSkPages = 128;
   // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
   static_assert(kPages >= kPagesPerWave, "pages per split");
 };
@@ -395,12 +397,13 @@ __device__ __forceinline__ void dma_load_q(const uint16_t* __restrict__ qrow, in
   }
 }
 
-// One wave's walk over pages [p_begin, p_end) (at most DmaCfg<KIND>::kPages)
+// One wave's walk over pages [p_begin, p_end) (at most PAGES)
 // of one (sequence, kv head hk) whose block-table row is `bt_row`. The
 // online-softmax state (o, m_run, l_run) is carried in and out, so a
 // context can be walked in several calls; the ring is filled at the start
 // and drained at the end of each call.
-template <typename Tr, int D, int KIND, int RING = DmaCfg<KIND>::kRing>
+template <typename Tr, int D, int KIND, int RING = DmaCfg<KIND>::kRing,
+          int PAGES = DmaCfg<KIND>::kPages>
 __device__ __forceinline__ void dma_walk(const typename Tr::vec8 (&qv)[D / 32], f32x4 (&o)[D / 16],
                                          float& m_run, float& l_run, unsigned char* ring,
                                          const void* __restrict__ Kc, const void* __restrict__ Vc,
@@ -419,9 +422,8 @@ __device__ __forceinline__ void dma_walk(const typename Tr::vec8 (&qv)[D / 32], 
   constexpr int STAGE = 2 * CHUNK;            // K and V of the step's page
   constexpr int DPS = 2 * NDMA;               // loads per step
   constexpr int KRD = FP8 ? NKS : 2 * NKS;    // LDS reads for one page's K^T operands
-  constexpr int kDmaPages = DmaCfg<KIND>::kPages;
-  constexpr int PB = kDmaPages / 64;          // page-id registers per lane
-  static_assert(kDmaPages % 64 == 0 && PB <= 2, "pages per split");
+  constexpr int PB = PAGES / 64;              // page-id registers per lane
+  static_assert(PAGES % 64 == 0 && PB <= 2, "pages per split");
   static_assert((RING - 1) * DPS <= 63, "vmcnt range");
 
   const int lane = threadIdx.x;
@@ -752,7 +754,7 @@ __global__ __launch_bounds__(64) void decode_sk_kernel(
     int n_hc, float scale_log2) {
   constexpr int NKS = D / 32, NB = D / 16;
   constexpr int STAGE = 2 * D * 16 * (KIND == kKindPagedFp8 ? 1 : 2);
-  constexpr int kDmaPages = DmaCfg<KIND>::kPages;
+  constexpr int kDmaPages = DmaCfg<KIND>::kSkPages;
   constexpr int NCH = kSkMaxSeqs / 64;
   __shared__ __attribute__((aligned(1024))) unsigned char ring[DmaCfg<KIND>::kSkRing * STAGE];
 
@@ -830,7 +832,7 @@ __global__ __launch_bounds__(64) void decode_sk_kernel(
     // share a segment do not refill in step)
     for (int p = p0; p < p0 + len;) {
       const int pe = min(p0 + len, (p / kDmaPages + 1) * kDmaPages);
-      dma_walk<Tr, D, KIND, DmaCfg<KIND>::kSkRing>(
+      dma_walk<Tr, D, KIND, DmaCfg<KIND>::kSkRing, kDmaPages>(
           qv, o, m_run, l_run, ring, Kc, Vc, k_scale, v_scale, per_block,
           block_tables + (size_t)n * max_blocks, Hkv, hk, num_blocks, p, pe, Lctx, scale_log2,
           (const unsigned char*)Q);
