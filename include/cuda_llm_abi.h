@@ -197,10 +197,17 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
  * the process ends). No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Sizes whose partials exceed the
- * scratch, num_seqs * num_q_heads * splits * (head_dim + 1) * 4 bytes with
- * splits = ceil(max_blocks_per_seq / 128) for fp16/bf16 queries and
- * ceil(max_blocks_per_seq / 64) for float32 (none when that is 1), return
- * CA_INVALID_ARGUMENT. Every call on a device shares that device's scratch,
+ * scratch return CA_INVALID_ARGUMENT. The partials are those of the launch's
+ * plan: for fp16/bf16 queries, when the longest context spans more than 128
+ * blocks, num_seqs <= 1024 and the balanced walk's partials fit the
+ * workspace ca_decode_workspace_bytes names, 2 * (4 * compute units) *
+ * min(16, num_q_heads / num_kv_heads) * (head_dim + 1) * 4 + 4 * num_seqs
+ * bytes (4.2 MB at head dim 128 and 4 query heads per kv head on a
+ * 256-CU device, whatever the context lengths); otherwise num_seqs *
+ * num_q_heads * splits * (head_dim + 1) * 4 bytes with splits =
+ * ceil(max_blocks_per_seq / 128) for fp16/bf16 queries and
+ * ceil(max_blocks_per_seq / 64) for float32 (none when that is 1). Every
+ * call on a device shares that device's scratch,
  * so the calls are serialised on the device: a call on another stream than
  * the previous call's waits (on the GPU, through an event) for that call's
  * kernels, and concurrent host threads take turns. Under stream capture that

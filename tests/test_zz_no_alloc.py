@@ -79,6 +79,21 @@ def test_noalloc_balanced_walk_twice(dev):
         assert_close(to_np(out), paged_oracle(case, dtype=np.float64), **TOL_FP8, name=name)
 
 
+def test_noalloc_serves_c4(dev):
+    """At the C4 shape (256 sequences up to 32768 tokens, GQA 32/8) the
+    balanced walk's partials fit the scratch: the allocation-free form runs
+    it and equals the workspace form bit for bit."""
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(2048, 32769, (256,), generator=g).tolist()
+    case = build_paged(lens, 32, 8, 128, torch.bfloat16, dev, fp8=True, per_block=True)
+    assert balanced_walk_taken(256, 32, 8, 128, case["block_tables"].shape[1], True)
+    out = _noalloc(case)
+    ref = _with_workspace(case)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, ref)
+
+
 def test_noalloc_two_streams(dev):
     """Calls on two streams, issued back to back with no host wait between,
     share the scratch: the second call's stream waits for the first call on
