@@ -367,11 +367,10 @@ template <int KIND>
 struct DmaCfg {
   // (rings of 3 / 2 fp8 steps or 2 16-bit steps, which let more waves share
   // a CU, measured within +-1 % on C4 / C3)
+  // (the stream-K walk uses the same depths: deeper rings measured within
+  // -0.5 % at head dim 128 and -3 .. +4 % at 64)
   static constexpr int kRing = KIND == kKindPagedFp8 ? 4 : 3;
   static constexpr int kPages = KIND == kKindPagedFp8 ? 128 : kPagesPerWave;
-  // ring of the stream-K walk: the same depth (one wave per SIMD would leave
-  // LDS for deeper rings; 6 FP8 / 4 16-bit steps measured within -0.5 %)
-  static constexpr int kSkRing = KIND == kKindPagedFp8 ? 4 : 3;
   // pages per ring fill of the stream-K walk
   static constexpr int kSkPages = 128;
   // decode_workspace_bytes sizes the partials for kPagesPerWave-page splits
@@ -756,7 +755,7 @@ __global__ __launch_bounds__(64) void decode_sk_kernel(
   constexpr int STAGE = 2 * D * 16 * (KIND == kKindPagedFp8 ? 1 : 2);
   constexpr int kDmaPages = DmaCfg<KIND>::kSkPages;
   constexpr int NCH = kSkMaxSeqs / 64;
-  __shared__ __attribute__((aligned(1024))) unsigned char ring[DmaCfg<KIND>::kSkRing * STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[DmaCfg<KIND>::kRing * STAGE];
 
   const int lane = threadIdx.x;
   const int segs = Hkv * n_hc;
@@ -832,7 +831,7 @@ __global__ __launch_bounds__(64) void decode_sk_kernel(
     // share a segment do not refill in step)
     for (int p = p0; p < p0 + len;) {
       const int pe = min(p0 + len, (p / kDmaPages + 1) * kDmaPages);
-      dma_walk<Tr, D, KIND, DmaCfg<KIND>::kSkRing, kDmaPages>(
+      dma_walk<Tr, D, KIND, DmaCfg<KIND>::kRing, kDmaPages>(
           qv, o, m_run, l_run, ring, Kc, Vc, k_scale, v_scale, per_block,
           block_tables + (size_t)n * max_blocks, Hkv, hk, num_blocks, p, pe, Lctx, scale_log2,
           (const unsigned char*)Q);
@@ -986,10 +985,15 @@ size_t decode_workspace_bytes(int N, int Hq, int D, int max_tokens) {
   return split_partials_bytes(N, Hq, D, pages / kPagesPerWave + (pages % kPagesPerWave != 0));
 }
 
-// Waves per CU of a stream-K launch: one per SIMD. Every wave streams the
-// same bytes, so a CU must hold a multiple of four for its SIMDs to finish
-// together, and one per SIMD measured best.
-constexpr int kSkWavesPerCu = 4;
+// Waves per CU of a stream-K launch. Every wave streams the same bytes, so a
+// CU must hold a multiple of four for its SIMDs to finish together; one per
+// SIMD measured best, except where a page step is only 2 KB (FP8 at head dim
+// 64): there one wave cannot cover its own per-step latency, and two per
+// SIMD run 5632-6006 GB/s against 4375-4611 (reference-grid shapes).
+template <int KIND, int D>
+constexpr int sk_waves_per_cu() {
+  return 2 * D * 16 * (KIND == kKindPagedFp8 ? 1 : 2) < 4096 ? 8 : 4;
+}
 
 // Grid of the stream-K decode on the current device (0 if unknown), cached
 // per device like device_cus.
@@ -1005,7 +1009,7 @@ static int sk_grid() {
             &per_cu, reinterpret_cast<const void*>(&decode_sk_kernel<Tr, D, KIND>), 64, 0) !=
         hipSuccess)
       return 0;
-    g = std::min(per_cu, kSkWavesPerCu) * device_cus();
+    g = std::min(per_cu, sk_waves_per_cu<KIND, D>()) * device_cus();
     cached[dev].store(g, std::memory_order_relaxed);
   }
   return g;
