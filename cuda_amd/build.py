@@ -36,10 +36,17 @@ COMMON = [
 # f32: MFMA accumulators in ordinary VGPRs. The fp32 split-walk kernel's VALU
 # reads its S and O accumulators every tile; allocated in AGPRs they cost a
 # v_accvgpr_read/write per element and tile (measured: ~130-190 per tile at
-# D = 64), which a wave pays in series with its MFMAs.
+# D = 64), which a wave pays in series with its MFMAs. decode: the same for
+# the paged walks' O accumulators (rescales and the output pass; C4 5918 ->
+# 6601 GB/s with one wave per SIMD).
+# backward: the instruction scheduler's max-ILP strategy (same registers, no
+# scratch, bitwise-equal gradients): C2 backward 716 -> 727 and 735 -> 748
+# TFLOP/s (two A/B runs); it made the 32-row forward at head dim 64 2-3 %
+# slower, so it stays on the backward only.
 EXTRA = {"prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
          "f32.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-         "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+         "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+         "backward.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
 # Generated sources: the 64-row prefill's kernel body (hand-scheduled
