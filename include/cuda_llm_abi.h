@@ -9,8 +9,10 @@
  * Conventions
  *  - All tensor arguments are raw device pointers to contiguous row-major
  *    buffers in the layouts stated per function; 16-byte aligned.
- *  - The library never allocates, frees or retains caller memory. Split-K
- *    decode needs a caller-provided workspace of ca_decode_workspace_bytes()
+ *  - The library never allocates, frees or retains caller memory. Decode
+ *    (split-K or the balanced walk of larger paged launches, whose partial
+ *    results are merged) needs a caller-provided workspace of
+ *    ca_decode_workspace_bytes()
  *    (ca_fp8_paged_attention_noalloc instead uses a fixed scratch array the
  *    library holds per device).
  *  - `stream` is a hipStream_t (NULL = the default stream). Calls enqueue
@@ -192,7 +194,7 @@ ca_status ca_fp8_paged_attention(ca_dtype dtype, const void* query, const uint8_
 
 /* FP8 paged decode that allocates nothing and takes no workspace: the
  * arguments, checks and results of ca_fp8_paged_attention (the same kernels),
- * with the split-K partials held in a scratch array of the library
+ * with the decode's partials held in a scratch array of the library
  * (CA_NOALLOC_SCRATCH_BYTES per device, kept from the library's load until
  * the process ends). No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
