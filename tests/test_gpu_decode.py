@@ -346,6 +346,23 @@ def test_balanced_walk_wide_groups_and_head_dim_64(dev):
         _check_balanced(case, TOL_FP8 if fp8 else TOL_16BIT, fp8, f"balanced D=64 fp8={fp8}")
 
 
+@pytest.mark.parametrize("n", [1024, 1025])
+def test_balanced_walk_sequence_limit(dev, n):
+    """1024 sequences fill every lane of the walk's prefix registers (16
+    chunks of 64); 1025 exceed them and take the split grid. Short random
+    contexts, a few long ones so that contexts span several splits."""
+    g = torch.Generator().manual_seed(16)
+    lens = torch.randint(0, 300, (n,), generator=g).tolist()
+    for i in (0, 511, n - 1):
+        lens[i] = 2100
+    case = build_paged(lens, 32, 8, 128, torch.bfloat16, dev, seed=16)
+    assert balanced_walk_taken(n, 32, 8, 128, case["block_tables"].shape[1], False) == (n <= 1024)
+    out = _run_paged(case)
+    torch.cuda.synchronize()
+    ref = paged_oracle(case)
+    assert_close(to_np(out), ref, **TOL_16BIT, name=f"N={n}")
+
+
 def _widen(case, width):
     t = case["block_tables"]
     case["block_tables"] = torch.cat(
